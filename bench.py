@@ -1,0 +1,178 @@
+"""Benchmark of the hot path: Euler steps 2-10 of the flow-matching action expert as one megakernel launch.
+
+One "step" of this benchmark is one launch that integrates Euler steps 2..10 of workload A (batch 1,
+10 layers, width 768, 12 heads x 64, MLP 3072, 10 action + 32 register rows, 96 memory rows, 300 source
+rows) from inputs already resident in HBM. Weights are random N(0, 0.02) (bf16), inputs are seeded
+synthetic tensors of the workload's shapes.
+
+Prints one JSON line: value = ms per launch (lower is better); "roofline" = algorithmic bytes per launch
+over the kernel's mean launch duration (HIP events on the launch stream) against 8 TB/s; "cpu_baseline" =
+the fp32 CPU oracle of the same steps on this host's cores, timed on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "reki-megakernel_amd")]
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "expert Euler-loop ms (steps 2–10, batch 1) + achieved HBM GB/s vs peak"
+
+
+def host_cores() -> int:
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed launches")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="A")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-runs", type=int, default=5)
+    ap.add_argument("--stage-profile", action="store_true", help="also print per-stage barrier timestamps (stderr)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the megakernel runs on a single MI355X (batch samples would shard "
+              "across GPUs with no exchange); run it with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from mkx import ExpertMegakernel, synthetic as SY
+
+    torch.set_grad_enabled(False)
+    cfg = SY.WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    W = SY.make_weights(cfg, seed=0)
+    model = SY.SyntheticReki(cfg, W, device=dev)
+    inp = SY.make_inputs(cfg)
+    past = model.register_prepare(inp["ctx"], inp["mem_states"])
+    mods, dt = model._step_modulations(cfg.num_steps, inp["state_cond"])
+    noise = inp["noise"].to(dev)
+    x1, _, _ = model._expert_first_step(noise, past, None, mods[..., :1, :], dt, cfg.action_dim)
+    mk = ExpertMegakernel(model)
+    plan = mk.plan(x1, mods, dt, past, cfg.action_dim)
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        plan.launch()
+    mk.check()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        plan.launch(stream.cuda_stream)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    mk.check()
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    ms_per_step = wall * 1e3 / args.steps
+    kern_ms = statistics.fmean(per)
+    n_euler = cfg.num_steps - 1
+    bytes_launch = SY.algorithmic_bytes_per_step(cfg) * n_euler
+    achieved = bytes_launch / (kern_ms * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"pmc_traffic_{args.workload}.json")
+    if os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    if args.stage_profile:
+        mk.set_profile(n_euler)
+        plan.launch()
+        torch.cuda.synchronize()
+        ts = mk.barrier_timestamps()[: mk.barriers(n_euler) + 1].tolist()
+        d = [(b - a) / 1e3 for a, b in zip(ts[1:-1], ts[2:])]
+        names = ["qkv", "sa_attn", "sa_o", "ca_q", "ca_attn", "ca_o", "gate_up", "down"]
+        per_step = 8 * cfg.L + 1
+        buckets = {k: [] for k in names + ["tail"]}
+        for i, v in enumerate(d):
+            j = i % per_step
+            buckets["tail" if j == per_step - 1 else names[j % 8]].append(v)
+        print(json.dumps({"stage_us_median": {k: round(statistics.median(v), 3) for k, v in buckets.items() if v},
+                          "stage_us_sum_ms": {k: round(sum(v) / 1e3, 4) for k, v in buckets.items() if v},
+                          "first_tail_us": round((ts[1] - ts[0]) / 1e3, 3)}), file=sys.stderr)
+        mk.set_profile(None)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import expert_ref as ER
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        cores = host_cores()
+        torch.set_num_threads(cores)
+        d = ER.ExpertDims(L=cfg.L, H=cfg.H, NH=cfg.NH, I=cfg.I, ctx_dim=cfg.ctx_dim, tdim=cfg.tdim, act=cfg.act)
+        st = past.register_step
+        as5 = lambda t: (t if t.dim() == 4 else t[None]).float().cpu()  # noqa: E731
+        cache = {"memk": torch.stack([as5(k) for k, _ in st["mem_kv"]]), "memv": torch.stack([as5(v) for _, v in st["mem_kv"]]),
+                 "kca": torch.stack([as5(k) for k, _ in past.cross_attn_kv]), "vca": torch.stack([as5(v) for _, v in past.cross_attn_kv]),
+                 "kv_start": st["kv_start"].cpu().long(), "ca_len": st["ca_len"].cpu().long(),
+                 "sa_cos": st["sa_pe"][0].cpu(), "sa_sin": st["sa_pe"][1].cpu(), "ca_cos": st["ca_pe"][0].cpu(),
+                 "ca_sin": st["ca_pe"][1].cpu()}
+        if cfg.m_q > cfg.T_act:
+            cache["reg_tok"] = W["reg_tok"].float()
+        OW = SY.oracle_weights(W)
+        m = mods.float().cpu()
+        m = m[None] if m.dim() == 2 else m
+        xin = x1.float().cpu()
+        times = []
+        for r in range(args.cpu_runs + 1):
+            t = time.perf_counter()
+            xr = ER.run_steps(xin, m[:, 1:], float(dt.item()), OW, cache, d, cfg.action_dim, "fp32")
+            if r:
+                times.append(time.perf_counter() - t)
+        gpu_x = plan.x_out.float().cpu()
+        dmax = float((gpu_x - xr)[..., : cfg.action_dim].abs().max())
+        cpu = {"value": round(statistics.median(times) * 1e3, 2), "unit": "ms", "cores": cores, "kind": "port",
+               "sample": f"fp32 CPU oracle (PyTorch, {cpu_model()}), Euler steps 2-10 of workload {args.workload}, "
+                         f"median of {args.cpu_runs} runs after 1 warm-up; GPU result vs this run max|d|={dmax:.2e}"}
+
+    out = {
+        "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init N(0,0.02) bf16 weights, seeded inputs)",
+        "config": {"workload": f"{args.workload}: batch {cfg.B}, L{cfg.L} H{cfg.H} NH{cfg.NH}x{cfg.HD} I{cfg.I}, "
+                               f"{cfg.T_act} action + {cfg.m_q - cfg.T_act} register rows, memory {cfg.PM} rows, "
+                               f"source {cfg.S} rows, Euler steps 2-{cfg.num_steps} in one launch",
+                   "launch": {"grid": mk.nprog, "block": mk.cfg["block"], "lds_bytes": mk.cfg["lds_bytes"]},
+                   "barriers_per_launch": mk.barriers(n_euler)},
+        "kernel_ms_mean": round(kern_ms, 4), "kernel_ms_median": round(statistics.median(per), 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": bytes_launch},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,157 @@
+/*
+ * mkx — C ABI of the MI355X (gfx950) persistent megakernel for the Euler loop of a
+ * flow-matching DiT action expert.
+ *
+ * The entry points replace the reference's Python expert-call boundary, class ExpertMegakernel in
+ * src/mk_expert.py (muninn-huginn/reki-megakernel):
+ *   mkx_create   <- ExpertMegakernel.__init__   (src/mk_expert.py:436-481: pack weights once, own scratch)
+ *   mkx_run      <- ExpertMegakernel.run        (src/mk_expert.py:483-515: marshal caches, one launch)
+ *   mkx_barriers <- ExpertMegakernel.barriers   (src/mk_expert.py:517-518: grid barriers per launch)
+ *   mkx_query    <- attributes the reference reads off the object (nprog, bar, prof; test_mk.py:44-45,
+ *                   tune_mk.py:131-153)
+ *   mkx_destroy, mkx_last_error, mkx_status_string: lifetime and error reporting the Python object
+ *                   had implicitly (the reference only asserts, src/mk_expert.py:444, 464, 480, 488, 496).
+ *
+ * Conventions: all tensor pointers are device pointers (hipMalloc'd or torch CUDA tensors). bf16 is
+ * stored as uint16. Weight matrices are row-major [out, in] like torch.nn.Linear.weight, stacked over
+ * layers exactly as the reference stacks them (src/mk_expert.py:445-460). No entry point aborts or
+ * hangs on bad input: every one returns an mkx_status, and mkx_last_error() describes the last failure
+ * on the calling thread.
+ */
+#ifndef MKX_H
+#define MKX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MKX_ABI_VERSION 1
+#define MKX_MAX_LAYERS 32
+
+typedef enum {
+  MKX_OK = 0,
+  MKX_EINVAL = 1,        /* shape / dtype / pointer / stride invalid (reference: assert) */
+  MKX_ENORESIDENT = 2,   /* the persistent grid cannot be co-resident (reference: hangs, README.md:262-263) */
+  MKX_EHIP = 3,          /* a HIP runtime call failed; mkx_last_error() names it */
+  MKX_ETIMEOUT = 4,      /* a grid-barrier wait exceeded its spin bound; results are invalid */
+  MKX_ENOMEM = 5,
+  MKX_EUNSUPPORTED = 6   /* a shape this build has no kernel instantiation for */
+} mkx_status;
+
+typedef enum { MKX_WEIGHTS_BF16 = 0, MKX_WEIGHTS_FP8_E4M3 = 1 } mkx_weight_dtype;
+typedef enum { MKX_ACT_SILU = 0, MKX_ACT_GELU_TANH = 1 } mkx_activation;
+
+typedef struct mkx_handle mkx_handle;
+
+/* Expert shapes. Reference: read off the REKI model in ExpertMegakernel.__init__ (src/mk_expert.py:438-463). */
+typedef struct {
+  int32_t L;            /* layers */
+  int32_t H;            /* width = NH * HD */
+  int32_t NH;           /* heads (MHA: n_kv_heads == NH, src/mk_expert.py:444) */
+  int32_t HD;           /* head dim (64) */
+  int32_t I;            /* MLP width */
+  int32_t A;            /* padded action width (action_in_proj.in_features, 32) */
+  int32_t max_rows;     /* max own rows per sample, M_q = T_act + R_reg (reference: TP = 16) */
+  int32_t max_batch;    /* max samples per launch */
+  int32_t max_mem_rows; /* max PM (register-memory rows) */
+  int32_t max_src_rows; /* max SP (padded cross-attention source rows) */
+  int32_t weight_dtype; /* mkx_weight_dtype */
+  int32_t activation;   /* mkx_activation (reference: SiLU, src/mk_expert.py:464) */
+  float eps;            /* AdaRMS eps (input_layernorm.eps, src/mk_expert.py:461) */
+  float qk_eps;         /* q/k RMSNorm eps (q_norm.eps, src/mk_expert.py:463) */
+} mkx_dims;
+
+/* Weights, stacked over layers (src/mk_expert.py:445-460). Linear weights are bf16, or e4m3 bytes with
+ * per-output-channel fp32 scales when weight_dtype == MKX_WEIGHTS_FP8_E4M3 (the *_scale pointers are
+ * then [L, out] and required; NULL for bf16). mkx_create copies them into the handle's own layout. */
+typedef struct {
+  const void* wqkv;   /* [L, 3H, H]  rows q;k;v (torch.cat of q_proj, k_proj, v_proj, :446-447) */
+  const void* wo;     /* [L, H, H]   self_attn.o_proj */
+  const void* wqca;   /* [L, H, H]   cross_attn.q_proj */
+  const void* woca;   /* [L, H, H]   cross_attn.o_proj */
+  const void* wg;     /* [L, I, H]   mlp.gate_proj */
+  const void* wu;     /* [L, I, H]   mlp.up_proj */
+  const void* wd;     /* [L, H, I]   mlp.down_proj */
+  const float* wqkv_scale, *wo_scale, *wqca_scale, *woca_scale, *wg_scale, *wu_scale, *wd_scale;
+  const void* qn;     /* [L, HD] bf16 self_attn.q_norm.weight (used as 1 + w) */
+  const void* kn;     /* [L, HD] bf16 self_attn.k_norm.weight */
+  const void* qcan;   /* [L, HD] bf16 cross_attn.q_norm.weight */
+  const float* win;   /* [A, H] fp32: action_in_proj.weight transposed (:457) */
+  const float* bin;   /* [H]    fp32 action_in_proj.bias */
+  const float* wout;  /* [A, H] fp32 action_out_proj.weight */
+  const float* bout;  /* [A]    fp32 action_out_proj.bias */
+} mkx_weights;
+
+/* One call: integrate n_steps Euler steps for B samples (src/mk_expert.py:483-515).
+ * Own rows of sample b are [T_act action rows || R_reg register rows]; only the action rows feed the
+ * step tail. Register rows take reg_tok as their layer-0 input in every step (reg_tok may be NULL when
+ * R_reg == 0, the reference's layout). Per-layer caches are passed as arrays of L device pointers so
+ * REKI-style per-layer tensors need no torch.stack (:489-492). Strides are in elements. */
+typedef struct {
+  const float* x_in;    /* [B, T_act, A] fp32: x after the previous step (reference: x_t after step 1) */
+  float* x_out;         /* [B, T_act, A] fp32: x after the last step (may alias x_in) */
+  const float* mods;    /* fp32 rows of MODW = 9 L H + 2 H: sample b, step s at mods + b*mods_stride_b +
+                           (mod_row0 + s) * mods_stride_step (reference: mods[N, MODW], row 1 + s, :336) */
+  int64_t mods_stride_b, mods_stride_step;
+  int32_t mod_row0;     /* first modulation row used (1 for steps 2..N, 0 for step 1) */
+  const float* dt;      /* [1] fp32 device scalar (reference: dt tensor, :320) */
+  const void* memk[MKX_MAX_LAYERS];  /* per layer [B, PM, NH, HD] bf16, pre-normed and rotated (past.register_step['mem_kv']) */
+  const void* memv[MKX_MAX_LAYERS];
+  int64_t mem_stride_b;               /* elements between samples (PM*NH*HD when packed) */
+  const int32_t* kv_start;            /* [B] first valid memory row (reference: cu_kv[0], :321) */
+  const void* kca[MKX_MAX_LAYERS];    /* per layer [B, SP, NH, HD] bf16, pre-normed and rotated (past.cross_attn_kv) */
+  const void* vca[MKX_MAX_LAYERS];
+  int64_t src_stride_b;
+  const int32_t* ca_len;              /* [B] valid source rows S (reference: cu_src[1], :322) */
+  const float* sa_cos, *sa_sin;       /* [M_q, HD] fp32 RoPE of own rows in self-attention (past.register_step['sa_pe']) */
+  const float* ca_cos, *ca_sin;       /* [M_q, HD] fp32 RoPE of own rows in cross-attention ('ca_pe') */
+  const void* reg_tok;                /* [R_reg, H] bf16 register-row input, or NULL when R_reg == 0 */
+  void* cur_k;                        /* optional out [L, B, R_reg, NH, HD] bf16: normed+rotated K of register rows, first step */
+  void* cur_v;                        /* optional out [L, B, R_reg, NH, HD] bf16: V of register rows, first step */
+  int32_t n_steps, action_dim, T_act, R_reg, B, PM, SP;
+} mkx_step_args;
+
+typedef enum {
+  MKX_Q_GRID = 0,          /* workgroups in the persistent launch (reference: nprog = SM count, :473) */
+  MKX_Q_BLOCK = 1,         /* threads per workgroup */
+  MKX_Q_BARRIER_COUNT = 2, /* barriers completed by the last launch (reference: mk.bar after the run, test_mk.py:44) */
+  MKX_Q_ERROR_FLAG = 3,    /* device error flag of the last launch (spin bound exceeded = 1) */
+  MKX_Q_PROFILE_LEN = 5,   /* entries of the caller's timestamp buffer, 0 when profiling is off */
+  MKX_Q_WEIGHT_BYTES = 6,  /* bytes of packed linear weights streamed per Euler step */
+  MKX_Q_LDS_BYTES = 7      /* dynamic LDS per workgroup */
+} mkx_query_key;
+
+/* ExpertMegakernel.__init__ (src/mk_expert.py:436-481). Validates dims, copies and repacks the weights
+ * on `stream` (synchronised before return), allocates scratch, checks co-residency. */
+int mkx_create(const mkx_dims* dims, const mkx_weights* weights, void* stream, mkx_handle** out);
+
+/* ExpertMegakernel.run (src/mk_expert.py:483-515): one persistent launch on `stream` (a hipStream_t;
+ * NULL = default stream). Inputs are borrowed for the duration of the call. A handle's scratch is shared
+ * by its calls: use one handle per stream (the reference is not re-entrant either). Asynchronous; call
+ * mkx_check after synchronising to learn whether a barrier wait timed out. */
+int mkx_run(mkx_handle* h, const mkx_step_args* args, void* stream);
+
+/* Reads the device error flag of the last launch (synchronises `stream`): MKX_OK or MKX_ETIMEOUT. */
+int mkx_check(mkx_handle* h, void* stream);
+
+/* ExpertMegakernel.barriers (src/mk_expert.py:517-518): grid barriers one launch of n_steps executes. */
+int64_t mkx_barriers(const mkx_handle* h, int32_t n_steps);
+
+/* Per-barrier timestamps (tune_mk.py PROFILE mode, src/mk_expert.py:66-69): later launches store, from
+ * workgroup 0, the ns clock after barrier nb into buf[nb] (buf[0] = launch start). buf is a caller-owned
+ * device int64 array of len entries (>= mkx_barriers(n_steps) + 1); NULL turns profiling off. */
+int mkx_set_profile(mkx_handle* h, int64_t* buf, int32_t len);
+
+int64_t mkx_query(const mkx_handle* h, int32_t key);
+int mkx_destroy(mkx_handle* h);
+const char* mkx_last_error(void);
+const char* mkx_status_string(int status);
+int32_t mkx_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MKX_H */

@@ -1,0 +1,402 @@
+// mkx C ABI (include/mkx.h): handle creation with weight packing, launch, queries.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "mkx.h"
+#include "mkx_kernel.h"
+
+using namespace mkx;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIPCHK(x)                                                                              \
+  do {                                                                                         \
+    hipError_t e_ = (x);                                                                       \
+    if (e_ != hipSuccess) return fail(MKX_EHIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr unsigned SPIN_LIMIT = 1u << 20;
+constexpr int MAX_ROWS_PADDED = 512;
+
+// W [L][N][K] row-major -> chunks (l, t, kb): dst[l*dls + (t*tstride + toff + kb)*512 + lane*8 + j] =
+// W[l][t*16 + lane%16][kb*32 + 8(lane/16) + j] (the MFMA 16x16x32 operand layout).
+__global__ void pack_tiles(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst, int L, int N, int K,
+                           long long dls, int tstride, int toff) {
+  const long long total = (long long)L * (N / 16) * (K / 32) * 64;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int lane = (int)(i % 64);
+  long long r = i / 64;
+  const int kb = (int)(r % (K / 32));
+  r /= (K / 32);
+  const int t = (int)(r % (N / 16));
+  const int l = (int)(r / (N / 16));
+  const bf16_t* s = src + ((long long)l * N + t * 16 + lane % 16) * K + kb * 32 + 8 * (lane / 16);
+  bf16_t* d = dst + (long long)l * dls + ((long long)t * tstride + toff + kb) * 512 + lane * 8;
+  *reinterpret_cast<u32x4*>(d) = *reinterpret_cast<const u32x4*>(s);
+}
+
+__global__ void xcc_probe(unsigned* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+template <int H, int I>
+const void* kernel_of() { return reinterpret_cast<const void*>(&mkx_megakernel<H, I>); }
+
+const void* pick_kernel(int H, int I) {
+  if (H == 768 && I == 3072) return kernel_of<768, 3072>();
+  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>();
+  if (H == 128 && I == 256) return kernel_of<128, 256>();
+  if (H == 256 && I == 1024) return kernel_of<256, 1024>();
+  return nullptr;
+}
+
+int lds_of(int H, int I) {
+  if (H == 768 && I == 3072) return Shape<768, 3072>::LDS;
+  if (H == 1024 && I == 4096) return Shape<1024, 4096>::LDS;
+  if (H == 128 && I == 256) return Shape<128, 256>::LDS;
+  if (H == 256 && I == 1024) return Shape<256, 1024>::LDS;
+  return 0;
+}
+
+inline int ceil16(int a) { return (a + 15) / 16 * 16; }
+inline int ceil32(int a) { return (a + 31) / 32 * 32; }
+inline int ceil4(int a) { return (a + 3) / 4 * 4; }
+
+long long frame_bytes(int H, int I, int nrp) {
+  if (H == 768 && I == 3072) return Shape<768, 3072>::frame_bytes(nrp);
+  if (H == 1024 && I == 4096) return Shape<1024, 4096>::frame_bytes(nrp);
+  if (H == 128 && I == 256) return Shape<128, 256>::frame_bytes(nrp);
+  if (H == 256 && I == 1024) return Shape<256, 1024>::frame_bytes(nrp);
+  return 0;
+}
+long long step_bytes(int H, int nrp, int nxrows, int A) { return (long long)nrp * H * 4 + (long long)((nxrows * A * 4 + 255) / 256 * 256); }
+
+}  // namespace
+
+struct mkx_handle {
+  mkx_dims d;
+  int device = 0;
+  int G = 0;
+  unsigned nx[MAX_XCD] = {};
+  unsigned xmask = 0;
+  const void* kernel = nullptr;
+  bf16_t *wqkv = nullptr, *wo = nullptr, *wqca = nullptr, *woca = nullptr, *wgu = nullptr, *wd = nullptr;
+  bf16_t *qn = nullptr, *kn = nullptr, *qcan = nullptr;
+  float *win = nullptr, *bin = nullptr, *wout = nullptr, *bout = nullptr;
+  char* frames = nullptr;
+  size_t frames_cap = 0;
+  char* steps = nullptr;
+  size_t steps_cap = 0;
+  unsigned* dcnt = nullptr;
+  BarState* bar = nullptr;
+  long long* prof = nullptr;
+  int prof_len = 0;
+  int profile = 0;
+  unsigned long long gen_before = 0;
+  long long last_nbar = 0;
+  long long weight_bytes = 0;
+};
+
+static void free_handle(mkx_handle* h) {
+  if (!h) return;
+  void* ptrs[] = {h->wqkv, h->wo, h->wqca, h->woca, h->wgu, h->wd, h->qn, h->kn, h->qcan, h->win, h->bin,
+                  h->wout, h->bout, h->frames, h->steps, h->dcnt, h->bar};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  delete h;
+}
+
+extern "C" {
+
+int32_t mkx_abi_version(void) { return MKX_ABI_VERSION; }
+
+const char* mkx_last_error(void) { return g_err.c_str(); }
+
+const char* mkx_status_string(int status) {
+  switch (status) {
+    case MKX_OK: return "ok";
+    case MKX_EINVAL: return "invalid argument";
+    case MKX_ENORESIDENT: return "persistent grid cannot be co-resident";
+    case MKX_EHIP: return "HIP runtime error";
+    case MKX_ETIMEOUT: return "grid barrier wait exceeded its spin bound";
+    case MKX_ENOMEM: return "out of device memory";
+    case MKX_EUNSUPPORTED: return "unsupported shape";
+    default: return "unknown status";
+  }
+}
+
+int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_handle** out) {
+  if (!dims || !w || !out) return fail(MKX_EINVAL, "null argument");
+  *out = nullptr;
+  const mkx_dims d = *dims;
+  if (d.L < 1 || d.L > MKX_MAX_LAYERS) return fail(MKX_EINVAL, "L must be in [1, 32]");
+  if (d.HD != HD) return fail(MKX_EUNSUPPORTED, "head dim must be 64");
+  if (d.NH * d.HD != d.H) return fail(MKX_EINVAL, "H must equal NH * HD");
+  if (d.A != 32) return fail(MKX_EUNSUPPORTED, "padded action width A must be 32");
+  if (d.weight_dtype != MKX_WEIGHTS_BF16) return fail(MKX_EUNSUPPORTED, "only bf16 weights are supported by this build");
+  if (d.activation != MKX_ACT_SILU && d.activation != MKX_ACT_GELU_TANH) return fail(MKX_EINVAL, "unknown activation");
+  if (d.max_batch < 1 || d.max_batch > MAX_BATCH) return fail(MKX_EINVAL, "max_batch must be in [1, 16]");
+  if (d.max_rows < 1 || d.max_rows > 128) return fail(MKX_EINVAL, "max_rows (own rows per sample) must be in [1, 128]");
+  if (d.max_mem_rows < 0 || d.max_mem_rows > 256) return fail(MKX_EINVAL, "max_mem_rows must be in [0, 256]");
+  const void* kern = pick_kernel(d.H, d.I);
+  if (!kern) return fail(MKX_EUNSUPPORTED, "no kernel instantiation for (H, I) = (" + std::to_string(d.H) + ", " + std::to_string(d.I) + ")");
+  if (!w->wqkv || !w->wo || !w->wqca || !w->woca || !w->wg || !w->wu || !w->wd || !w->qn || !w->kn || !w->qcan ||
+      !w->win || !w->bin || !w->wout || !w->bout)
+    return fail(MKX_EINVAL, "null weight pointer");
+  hipStream_t stream = (hipStream_t)stream_;
+  mkx_handle* h = new mkx_handle();
+  h->d = d;
+  h->kernel = kern;
+  auto bail = [&](int code) { free_handle(h); return code; };
+#define HCHK(x)                                                                                       \
+  do {                                                                                                \
+    hipError_t e_ = (x);                                                                              \
+    if (e_ != hipSuccess) return bail(fail(MKX_EHIP, std::string(#x) + ": " + hipGetErrorString(e_))); \
+  } while (0)
+  HCHK(hipGetDevice(&h->device));
+  hipDeviceProp_t prop;
+  HCHK(hipGetDeviceProperties(&prop, h->device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return bail(fail(MKX_EUNSUPPORTED, std::string("this library is built for gfx950, device is ") + prop.gcnArchName));
+  if (!prop.cooperativeLaunch) return bail(fail(MKX_ENORESIDENT, "device does not support cooperative launch"));
+  int per_cu = 0;
+  HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NTHREADS, 0));
+  if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel does not fit one workgroup per CU"));
+  h->G = prop.multiProcessorCount;
+  // XCD of each workgroup of a G-workgroup launch; the barrier's per-XCD counts come from it
+  unsigned* dx = nullptr;
+  HCHK(hipMalloc(&dx, sizeof(unsigned) * h->G));
+  hipLaunchKernelGGL(xcc_probe, dim3(h->G), dim3(NTHREADS), 0, stream, dx);
+  std::vector<unsigned> hx(h->G);
+  HCHK(hipMemcpyAsync(hx.data(), dx, sizeof(unsigned) * h->G, hipMemcpyDeviceToHost, stream));
+  HCHK(hipStreamSynchronize(stream));
+  (void)hipFree(dx);
+  // One workgroup fits per CU (LDS) and the grid has one workgroup per CU, so every XCD hosts exactly as
+  // many workgroups as it has CUs. The probe finds which XCDs exist; the dispatcher's rotation between
+  // launches changes which workgroup lands where, not how many land on each XCD.
+  if (h->G > 256) return bail(fail(MKX_EUNSUPPORTED, "more than 256 CUs"));
+  int nxcd = 0;
+  for (int i = 0; i < h->G; ++i) {
+    if (hx[i] >= MAX_XCD) return bail(fail(MKX_EUNSUPPORTED, "unexpected XCC id"));
+    if (!((h->xmask >> hx[i]) & 1u)) ++nxcd;
+    h->xmask |= 1u << hx[i];
+  }
+  if (nxcd < 1 || h->G % nxcd != 0) return bail(fail(MKX_EUNSUPPORTED, "CU count not divisible by the XCD count"));
+  for (int x = 0; x < MAX_XCD; ++x) h->nx[x] = ((h->xmask >> x) & 1u) ? (unsigned)(h->G / nxcd) : 0u;
+  // packed weights
+  const int L = d.L, H = d.H, I = d.I;
+  auto alloc = [&](void** p, size_t bytes) { return hipMalloc(p, bytes); };
+  const size_t sq = (size_t)L * 3 * H * H, so = (size_t)L * H * H, sgu = (size_t)L * 2 * I * H, sd = (size_t)L * H * I;
+  HCHK(alloc((void**)&h->wqkv, sq * 2));
+  HCHK(alloc((void**)&h->wo, so * 2));
+  HCHK(alloc((void**)&h->wqca, so * 2));
+  HCHK(alloc((void**)&h->woca, so * 2));
+  HCHK(alloc((void**)&h->wgu, sgu * 2));
+  HCHK(alloc((void**)&h->wd, sd * 2));
+  auto pack = [&](const void* src, bf16_t* dst, int N, int K, long long dls, int tstride, int toff) {
+    const long long total = (long long)L * (N / 16) * (K / 32) * 64;
+    hipLaunchKernelGGL(pack_tiles, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)src, dst,
+                       L, N, K, dls, tstride, toff);
+  };
+  pack(w->wqkv, h->wqkv, 3 * H, H, 3LL * H * H, H / 32, 0);
+  pack(w->wo, h->wo, H, H, (long long)H * H, H / 32, 0);
+  pack(w->wqca, h->wqca, H, H, (long long)H * H, H / 32, 0);
+  pack(w->woca, h->woca, H, H, (long long)H * H, H / 32, 0);
+  pack(w->wg, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), 0);
+  pack(w->wu, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), H / 32);
+  pack(w->wd, h->wd, H, I, (long long)H * I, I / 32, 0);
+  HCHK(hipGetLastError());
+  h->weight_bytes = (long long)(sq + 3 * so + sgu + sd) * 2;
+  HCHK(alloc((void**)&h->qn, (size_t)L * HD * 2));
+  HCHK(alloc((void**)&h->kn, (size_t)L * HD * 2));
+  HCHK(alloc((void**)&h->qcan, (size_t)L * HD * 2));
+  HCHK(hipMemcpyAsync(h->qn, w->qn, (size_t)L * HD * 2, hipMemcpyDeviceToDevice, stream));
+  HCHK(hipMemcpyAsync(h->kn, w->kn, (size_t)L * HD * 2, hipMemcpyDeviceToDevice, stream));
+  HCHK(hipMemcpyAsync(h->qcan, w->qcan, (size_t)L * HD * 2, hipMemcpyDeviceToDevice, stream));
+  HCHK(alloc((void**)&h->win, (size_t)d.A * H * 4));
+  HCHK(alloc((void**)&h->bin, (size_t)H * 4));
+  HCHK(alloc((void**)&h->wout, (size_t)d.A * H * 4));
+  HCHK(alloc((void**)&h->bout, (size_t)d.A * 4));
+  HCHK(hipMemcpyAsync(h->win, w->win, (size_t)d.A * H * 4, hipMemcpyDeviceToDevice, stream));
+  HCHK(hipMemcpyAsync(h->bin, w->bin, (size_t)H * 4, hipMemcpyDeviceToDevice, stream));
+  HCHK(hipMemcpyAsync(h->wout, w->wout, (size_t)d.A * H * 4, hipMemcpyDeviceToDevice, stream));
+  HCHK(hipMemcpyAsync(h->bout, w->bout, (size_t)d.A * 4, hipMemcpyDeviceToDevice, stream));
+  HCHK(alloc((void**)&h->dcnt, (size_t)(H / 16) * 4));
+  HCHK(hipMemsetAsync(h->dcnt, 0, (size_t)(H / 16) * 4, stream));
+  HCHK(alloc((void**)&h->bar, sizeof(BarState)));
+  HCHK(hipMemsetAsync(h->bar, 0, sizeof(BarState), stream));
+  HCHK(hipStreamSynchronize(stream));
+#undef HCHK
+  *out = h;
+  return MKX_OK;
+}
+
+int64_t mkx_barriers(const mkx_handle* h, int32_t n_steps) {
+  if (!h || n_steps < 0) return -1;
+  return 1 + (int64_t)n_steps * (8 * h->d.L + 1);
+}
+
+int mkx_set_profile(mkx_handle* h, int64_t* buf, int32_t len) {
+  if (!h) return fail(MKX_EINVAL, "null handle");
+  if (buf && len < 2) return fail(MKX_EINVAL, "profile buffer too short");
+  h->prof = (long long*)buf;
+  h->prof_len = buf ? len : 0;
+  h->profile = buf ? 1 : 0;
+  return MKX_OK;
+}
+
+int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
+  if (!h || !a) return fail(MKX_EINVAL, "null argument");
+  const mkx_dims& d = h->d;
+  hipStream_t stream = (hipStream_t)stream_;
+  const int L = d.L, H = d.H, I = d.I;
+  if (a->n_steps < 1) return fail(MKX_EINVAL, "n_steps must be >= 1");
+  if ((long long)a->B * a->T_act * a->action_dim * 4 > 72 * 1024) return fail(MKX_EUNSUPPORTED, "B * T_act * action_dim too large for the step tail");
+  if (a->B < 1 || a->B > d.max_batch) return fail(MKX_EINVAL, "B out of range");
+  if (a->T_act < 1 || a->R_reg < 0) return fail(MKX_EINVAL, "T_act must be >= 1 and R_reg >= 0");
+  const int Mq = a->T_act + a->R_reg;
+  if (Mq > d.max_rows || Mq > 128) return fail(MKX_EINVAL, "T_act + R_reg exceeds max_rows");
+  if (a->action_dim < 1 || a->action_dim > d.A) return fail(MKX_EINVAL, "action_dim must be in [1, A]");
+  if (a->PM < 1 || a->PM > 256 || a->PM > d.max_mem_rows) return fail(MKX_EINVAL, "PM must be in [1, min(256, max_mem_rows)]");
+  if (a->SP < 1 || a->SP > d.max_src_rows) return fail(MKX_EINVAL, "SP must be in [1, max_src_rows]");
+  if (!a->x_in || !a->x_out || !a->mods || !a->dt || !a->kv_start || !a->ca_len || !a->sa_cos || !a->sa_sin ||
+      !a->ca_cos || !a->ca_sin)
+    return fail(MKX_EINVAL, "null input pointer");
+  if (a->R_reg > 0 && !a->reg_tok) return fail(MKX_EINVAL, "reg_tok is required when R_reg > 0");
+  if ((a->cur_k != nullptr) != (a->cur_v != nullptr)) return fail(MKX_EINVAL, "cur_k and cur_v must both be set or both NULL");
+  for (int l = 0; l < L; ++l)
+    if (!a->memk[l] || !a->memv[l] || !a->kca[l] || !a->vca[l]) return fail(MKX_EINVAL, "null per-layer cache pointer");
+  if (a->mods_stride_step < 9LL * L * H + 2 * H) return fail(MKX_EINVAL, "mods_stride_step is smaller than MODW = 9 L H + 2 H");
+  const int Mqp = ceil4(Mq);
+  const int NR = a->B * Mqp;
+  const int NRP = ceil16(NR);
+  if (NRP > MAX_ROWS_PADDED) return fail(MKX_EUNSUPPORTED, "B * (T_act + R_reg) too large for this build");
+  const int nown = ceil16(Mq), pmp = ceil16(a->PM);
+  if (2 * nown * 128 + ceil32(pmp + nown) * 128 + 4096 > 72 * 1024)
+    return fail(MKX_EUNSUPPORTED, "self-attention working set (memory + own rows) does not fit LDS");
+  if (h->profile && 1 + a->n_steps * (8LL * L + 1) + 1 > h->prof_len) return fail(MKX_EINVAL, "profile buffer shorter than barriers + 1");
+  // scratch: one frame per (step, layer), one step area per step; grown on demand
+  const long long fb = frame_bytes(H, I, NRP);
+  const long long sb = step_bytes(H, NRP, a->B * a->T_act, d.A);
+  const size_t need_f = (size_t)fb * a->n_steps * L, need_s = (size_t)sb * a->n_steps;
+  if (need_f > h->frames_cap || need_s > h->steps_cap) {
+    HIPCHK(hipStreamSynchronize(stream));
+    if (need_f > h->frames_cap) {
+      if (h->frames) HIPCHK(hipFree(h->frames));
+      h->frames = nullptr;
+      h->frames_cap = 0;
+      if (hipMalloc(&h->frames, need_f) != hipSuccess) return fail(MKX_ENOMEM, "activation frames");
+      h->frames_cap = need_f;
+    }
+    if (need_s > h->steps_cap) {
+      if (h->steps) HIPCHK(hipFree(h->steps));
+      h->steps = nullptr;
+      h->steps_cap = 0;
+      if (hipMalloc(&h->steps, need_s) != hipSuccess) return fail(MKX_ENOMEM, "step areas");
+      h->steps_cap = need_s;
+    }
+  }
+  Params p;
+  std::memset(&p, 0, sizeof(p));
+  p.wqkv = h->wqkv; p.wo = h->wo; p.wqca = h->wqca; p.woca = h->woca; p.wgu = h->wgu; p.wd = h->wd;
+  p.s_qkv = 3LL * H * H; p.s_o = (long long)H * H; p.s_gu = 2LL * I * H; p.s_d = (long long)H * I;
+  p.qn = h->qn; p.kn = h->kn; p.qcan = h->qcan;
+  p.win = h->win; p.bin = h->bin; p.wout = h->wout; p.bout = h->bout;
+  p.x_in = a->x_in; p.x_out = a->x_out;
+  p.mods = a->mods; p.mods_sb = a->mods_stride_b; p.mods_ss = a->mods_stride_step; p.mod_row0 = a->mod_row0;
+  p.dt = a->dt;
+  for (int l = 0; l < L; ++l) {
+    p.memk[l] = (const bf16_t*)a->memk[l]; p.memv[l] = (const bf16_t*)a->memv[l];
+    p.kca[l] = (const bf16_t*)a->kca[l]; p.vca[l] = (const bf16_t*)a->vca[l];
+  }
+  p.mem_sb = a->mem_stride_b; p.src_sb = a->src_stride_b;
+  p.kv_start = a->kv_start; p.ca_len = a->ca_len;
+  p.sa_cos = a->sa_cos; p.sa_sin = a->sa_sin; p.ca_cos = a->ca_cos; p.ca_sin = a->ca_sin;
+  p.reg_tok = (const bf16_t*)a->reg_tok; p.cur_k = (bf16_t*)a->cur_k; p.cur_v = (bf16_t*)a->cur_v;
+  p.n_steps = a->n_steps; p.action_dim = a->action_dim; p.T = a->T_act; p.R = a->R_reg; p.B = a->B;
+  p.PM = a->PM; p.SP = a->SP; p.L = L; p.Mq = Mq; p.Mqp = Mqp; p.NR = NR; p.NRP = NRP; p.A = d.A;
+  p.act = d.activation == MKX_ACT_GELU_TANH ? 1 : 0;
+  p.eps = d.eps; p.qk_eps = d.qk_eps; p.sm_scale = 1.0f / 8.0f;
+  p.frames = h->frames; p.frame_bytes = fb; p.steps = h->steps; p.step_bytes = sb;
+  p.dcnt = h->dcnt; p.bar = h->bar;
+  for (int x = 0; x < MAX_XCD; ++x) p.nx[x] = h->nx[x];
+  p.xmask = h->xmask;
+  p.prof = h->prof; p.profile = h->profile;
+  p.spin_limit = SPIN_LIMIT;
+  void* args[] = {&p};
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIPCHK(hipStreamIsCapturing(stream, &cs));
+  if (cs == hipStreamCaptureStatusActive) {
+    // co-residency was established at creation (one workgroup per CU fits); capture a plain launch
+    HIPCHK(hipLaunchKernel(h->kernel, dim3(h->G), dim3(NTHREADS), args, 0, stream));
+  } else {
+    HIPCHK(hipLaunchCooperativeKernel(h->kernel, dim3(h->G), dim3(NTHREADS), args, 0, stream));
+  }
+  h->last_nbar = mkx_barriers(h, a->n_steps);
+  return MKX_OK;
+}
+
+int mkx_check(mkx_handle* h, void* stream_) {
+  if (!h) return fail(MKX_EINVAL, "null handle");
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream_));
+  int err = 0;
+  HIPCHK(hipMemcpy(&err, &h->bar->err, sizeof(int), hipMemcpyDeviceToHost));
+  if (err) {
+    HIPCHK(hipMemset(h->bar, 0, sizeof(BarState)));
+    HIPCHK(hipMemset(h->dcnt, 0, (size_t)(h->d.H / 16) * 4));
+    h->gen_before = 0;
+    return fail(MKX_ETIMEOUT, "a grid-barrier wait exceeded its spin bound; barrier state was reset");
+  }
+  return MKX_OK;
+}
+
+int64_t mkx_query(const mkx_handle* h, int32_t key) {
+  if (!h) return -1;
+  switch (key) {
+    case MKX_Q_GRID: return h->G;
+    case MKX_Q_BLOCK: return NTHREADS;
+    case MKX_Q_BARRIER_COUNT: {
+      // workgroup arrivals recorded by the per-XCD counters since the previous query (synchronises)
+      if (hipDeviceSynchronize() != hipSuccess) return -1;
+      std::vector<unsigned long long> arr(MAX_XCD * 32);
+      if (hipMemcpy(arr.data(), h->bar->arrive, sizeof(unsigned long long) * MAX_XCD * 32, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+      unsigned long long gen = 0;
+      if (hipMemcpy(&gen, &h->bar->gen, sizeof(gen), hipMemcpyDeviceToHost) != hipSuccess) return -1;
+      long long total = 0;
+      mkx_handle* hm = const_cast<mkx_handle*>(h);
+      for (int x = 0; x < MAX_XCD; ++x) total += (long long)(arr[x * 32] - hm->gen_before * h->nx[x]);
+      hm->gen_before = gen;
+      return total;
+    }
+    case MKX_Q_ERROR_FLAG: {
+      int err = 0;
+      if (hipMemcpy(&err, &h->bar->err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return -1;
+      return err;
+    }
+    case MKX_Q_PROFILE_LEN: return h->prof_len;
+    case MKX_Q_WEIGHT_BYTES: return h->weight_bytes;
+    case MKX_Q_LDS_BYTES: return lds_of(h->d.H, h->d.I);
+    default: return -1;
+  }
+}
+
+int mkx_destroy(mkx_handle* h) {
+  if (!h) return MKX_OK;
+  (void)hipDeviceSynchronize();
+  free_handle(h);
+  return MKX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+// Device primitives for the mkx megakernel (gfx950 / CDNA4).
+//
+// Memory-coherence scheme (MI355X has 8 XCDs, each with its own L2; the L2s are not coherent with
+// each other):
+//  * Activations cross workgroups through write-once "frames": a producer writes with sc1 (device-scope,
+//    write-through past its XCD's L2), and every frame address is written at most once per launch and
+//    only read after the barrier that follows the write. Consumers therefore read with ordinary loads:
+//    no L2 can hold a stale copy of an address that was never read before it was written, and the L2 of
+//    each XCD de-duplicates the 32 CUs' reads of the same activation rows. No cache writeback or
+//    invalidate (buffer_wbl2 / buffer_inv) is executed on the hot path.
+//  * The grid barrier is hierarchical and fence-free: each workgroup waits for its own stores to be
+//    acknowledged, bumps its XCD's arrival counter with an L2 atomic, the last arrival of an XCD publishes
+//    the epoch with a device-scope store, and every workgroup polls the eight per-XCD flags with
+//    device-scope loads. Counters are 64-bit and monotonic across launches, so nothing is reset.
+//  * Waits are bounded: a wait that exceeds its spin bound sets an error flag, and every later wait of the
+//    launch returns immediately, so a broken launch still drains.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mkx {
+
+typedef uint16_t bf16_t;
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int NTHREADS = 256;
+constexpr int NWAVES = 4;
+constexpr int HD = 64;
+constexpr int MAX_LAYERS = 32;
+constexpr int MAX_BATCH = 16;
+constexpr int MAX_XCD = 16;
+
+// cache-policy bits of buffer / LDS-DMA instructions on gfx950
+constexpr int CPOL_NONE = 0;
+constexpr int CPOL_NT = 2;
+constexpr int CPOL_SC1 = 16;
+
+__device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);                                          // round to nearest even
+  return (bf16_t)(u >> 16);
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+// 16-byte store, written through to the device coherence point (base must be wave-uniform)
+__device__ __forceinline__ void st_sc1(void* base, uint32_t byte_off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc(base), byte_off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void st_sc1_b32(void* base, uint32_t byte_off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, rsrc(base), byte_off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void st_sc1_b16(void* base, uint32_t byte_off, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, rsrc(base), byte_off, 0, CPOL_SC1);
+}
+// 16-byte device-coherent load
+__device__ __forceinline__ u32x4 ld_sc1(const void* base, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), byte_off, 0, CPOL_SC1);
+}
+// 16-byte ordinary load (frames, read-only inputs)
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// LDS DMA: each lane copies 16 bytes from `src` to lds_base + 16 * lane (lds_base wave-uniform).
+template <int CPOL = CPOL_NONE>
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_base, 16, 0, CPOL);
+}
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0); }
+
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xf;
+}
+__device__ __forceinline__ long long clock100() { return (long long)__builtin_amdgcn_s_memrealtime(); }
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// grid barrier state (device memory, zeroed at handle creation)
+struct BarState {
+  unsigned long long arrive[MAX_XCD][32];   // per-XCD arrival counters (L2 atomics), 256 B apart
+  unsigned long long done[MAX_XCD][512];    // per-XCD published epochs (device scope), 4 KB apart
+  unsigned long long gen;                   // epoch base: barriers completed by earlier launches
+  unsigned long long pad0[15];
+  int err;                                  // 1 = a wait exceeded its spin bound
+  int pad1[31];
+  unsigned long long arrivals_last;         // barriers x workgroups recorded by the last launch
+};
+
+struct BarCtx {
+  BarState* bs;
+  unsigned long long base;  // gen at launch start
+  unsigned x;               // this workgroup's XCD
+  unsigned nx;              // workgroups on this XCD
+  unsigned xmask;           // XCDs that have workgroups
+  unsigned spin_limit;
+  bool failed;
+};
+
+__device__ __forceinline__ void bar_arrive(BarCtx& c, unsigned long long e) {
+  wait_vm0();  // this wave's stores are acknowledged (sc1 stores have reached the coherence point)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long t = c.base + e;
+    unsigned long long old =
+        __hip_atomic_fetch_add(&c.bs->arrive[c.x][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (old + 1 == t * c.nx) __hip_atomic_store(&c.bs->done[c.x][0], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__device__ __forceinline__ void bar_wait(BarCtx& c, unsigned long long e) {
+  if (threadIdx.x < 64 && !c.failed) {
+    const unsigned long long t = c.base + e;
+    const unsigned lane = threadIdx.x;
+    unsigned n = 0;
+    while (true) {
+      bool ok = true;
+      if (lane < MAX_XCD && ((c.xmask >> lane) & 1u))
+        ok = __hip_atomic_load(&c.bs->done[lane][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= t;
+      if (__all(ok)) break;
+      if (++n > c.spin_limit) {
+        if (lane == 0) __hip_atomic_store(&c.bs->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        c.failed = true;
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  // every wave learns whether wave 0 gave up (so later waits are skipped uniformly)
+  __shared__ int s_failed;
+  if (threadIdx.x == 0) s_failed = c.failed ? 1 : 0;
+  __syncthreads();
+  c.failed = s_failed != 0;
+}
+
+}  // namespace mkx

@@ -1,0 +1,83 @@
+"""ctypes binding of libmkx.so (include/mkx.h). Loading fails loudly when the library is missing: there is
+no fallback path."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmkx.so")
+MAX_LAYERS = 32
+
+OK, EINVAL, ENORESIDENT, EHIP, ETIMEOUT, ENOMEM, EUNSUPPORTED = range(7)
+WEIGHTS_BF16, WEIGHTS_FP8_E4M3 = 0, 1
+ACT_SILU, ACT_GELU_TANH = 0, 1
+Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WEIGHT_BYTES, Q_LDS_BYTES = range(8)
+
+EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
+           "mkx_last_error", "mkx_status_string", "mkx_abi_version")
+
+_vp = ctypes.c_void_p
+
+
+class MkxDims(ctypes.Structure):
+    _fields_ = [("L", ctypes.c_int32), ("H", ctypes.c_int32), ("NH", ctypes.c_int32), ("HD", ctypes.c_int32),
+                ("I", ctypes.c_int32), ("A", ctypes.c_int32), ("max_rows", ctypes.c_int32),
+                ("max_batch", ctypes.c_int32), ("max_mem_rows", ctypes.c_int32), ("max_src_rows", ctypes.c_int32),
+                ("weight_dtype", ctypes.c_int32), ("activation", ctypes.c_int32), ("eps", ctypes.c_float),
+                ("qk_eps", ctypes.c_float)]
+
+
+class MkxWeights(ctypes.Structure):
+    _fields_ = [(n, _vp) for n in ("wqkv", "wo", "wqca", "woca", "wg", "wu", "wd",
+                                   "wqkv_scale", "wo_scale", "wqca_scale", "woca_scale", "wg_scale", "wu_scale", "wd_scale",
+                                   "qn", "kn", "qcan", "win", "bin", "wout", "bout")]
+
+
+class MkxStepArgs(ctypes.Structure):
+    _fields_ = [("x_in", _vp), ("x_out", _vp), ("mods", _vp), ("mods_stride_b", ctypes.c_int64),
+                ("mods_stride_step", ctypes.c_int64), ("mod_row0", ctypes.c_int32), ("dt", _vp),
+                ("memk", _vp * MAX_LAYERS), ("memv", _vp * MAX_LAYERS), ("mem_stride_b", ctypes.c_int64),
+                ("kv_start", _vp), ("kca", _vp * MAX_LAYERS), ("vca", _vp * MAX_LAYERS),
+                ("src_stride_b", ctypes.c_int64), ("ca_len", _vp), ("sa_cos", _vp), ("sa_sin", _vp),
+                ("ca_cos", _vp), ("ca_sin", _vp), ("reg_tok", _vp), ("cur_k", _vp), ("cur_v", _vp),
+                ("n_steps", ctypes.c_int32), ("action_dim", ctypes.c_int32), ("T_act", ctypes.c_int32),
+                ("R_reg", ctypes.c_int32), ("B", ctypes.c_int32), ("PM", ctypes.c_int32), ("SP", ctypes.c_int32)]
+
+
+class MkxError(RuntimeError):
+    def __init__(self, status: int, where: str, detail: str):
+        super().__init__(f"{where}: mkx status {status} ({detail})")
+        self.status = status
+
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libmkx.so (once). Raises when it has not been built: the expert has no other implementation."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build the HIP library first (python -c 'import __graft_entry__ as g; g.build()')")
+        L = ctypes.CDLL(LIB_PATH)
+        L.mkx_create.argtypes = [ctypes.POINTER(MkxDims), ctypes.POINTER(MkxWeights), _vp, ctypes.POINTER(_vp)]
+        L.mkx_run.argtypes = [_vp, ctypes.POINTER(MkxStepArgs), _vp]
+        L.mkx_check.argtypes = [_vp, _vp]
+        L.mkx_barriers.argtypes = [_vp, ctypes.c_int32]
+        L.mkx_barriers.restype = ctypes.c_int64
+        L.mkx_set_profile.argtypes = [_vp, _vp, ctypes.c_int32]
+        L.mkx_query.argtypes = [_vp, ctypes.c_int32]
+        L.mkx_query.restype = ctypes.c_int64
+        L.mkx_destroy.argtypes = [_vp]
+        L.mkx_last_error.restype = ctypes.c_char_p
+        L.mkx_status_string.argtypes = [ctypes.c_int]
+        L.mkx_status_string.restype = ctypes.c_char_p
+        L.mkx_abi_version.restype = ctypes.c_int32
+        _LIB = L
+    return _LIB
+
+
+def check(status: int, where: str) -> None:
+    if status != OK:
+        L = lib()
+        raise MkxError(status, where, f"{L.mkx_status_string(status).decode()}: {L.mkx_last_error().decode()}")

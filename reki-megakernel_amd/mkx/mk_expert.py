@@ -1,0 +1,264 @@
+"""Host-side mirror of the reference's expert-call boundary (src/mk_expert.py:429-536).
+
+``ExpertMegakernel(model)`` reads the REKI-shaped expert, stacks its weights exactly as the reference
+does (src/mk_expert.py:445-460) and hands them to ``mkx_create``, which repacks them for the HIP
+megakernel. ``run(x_t, mods, dt, past, action_dim)`` integrates Euler steps 2..N in one persistent launch
+on the current stream (src/mk_expert.py:483-515); ``barriers(n_steps)`` and ``install(model)`` keep the
+reference's names and meaning (:517-536). Argument checks raise ``ValueError`` where the reference
+asserts; a failing library call raises ``MkxError``. There is no fallback: without libmkx.so nothing
+here runs.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import MkxDims, MkxStepArgs, MkxWeights, check, lib
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+class ExpertMegakernel:
+    """Packs the expert weights once; ``run`` integrates Euler steps 2..N in one launch."""
+
+    def __init__(self, model, registers_in_loop: bool | None = None, max_rows: int = 128, max_batch: int = 16,
+                 max_mem_rows: int = 256, max_src_rows: int = 1 << 16):
+        vwe = model.vlm_with_expert
+        layers = list(vwe.action_expert.layers)
+        sa0 = layers[0].self_attn
+        self.L, self.NH, self.HD = len(layers), sa0.n_q_heads, sa0.head_dim
+        self.H = self.NH * self.HD
+        self.I = layers[0].mlp.gate_proj.out_features
+        self.A = model.action_in_proj.in_features
+        if sa0.n_kv_heads != self.NH or layers[0].cross_attn.n_kv_heads != self.NH:
+            raise ValueError("the megakernel implements multi-head attention only (n_kv_heads == n_q_heads)")
+        bf = torch.bfloat16
+        st = lambda f: torch.stack([f(lay).detach().to(bf) for lay in layers]).contiguous()  # noqa: E731
+        wqkv = st(lambda m: torch.cat([m.self_attn.q_proj.weight, m.self_attn.k_proj.weight, m.self_attn.v_proj.weight], 0))
+        wo = st(lambda m: m.self_attn.o_proj.weight)
+        wqca = st(lambda m: m.cross_attn.q_proj.weight)
+        woca = st(lambda m: m.cross_attn.o_proj.weight)
+        wg = st(lambda m: m.mlp.gate_proj.weight)
+        wu = st(lambda m: m.mlp.up_proj.weight)
+        wd = st(lambda m: m.mlp.down_proj.weight)
+        qn = st(lambda m: m.self_attn.q_norm.weight)
+        kn = st(lambda m: m.self_attn.k_norm.weight)
+        qcan = st(lambda m: m.cross_attn.q_norm.weight)
+        win = model.action_in_proj.weight.detach().float().t().contiguous()  # [A, H]
+        b_in = model.action_in_proj.bias.detach().float().contiguous()
+        wout = model.action_out_proj.weight.detach().float().contiguous()
+        bout = model.action_out_proj.bias.detach().float().contiguous()
+        self.eps = float(layers[0].input_layernorm.eps)
+        if float(vwe.action_expert.norm.eps) != self.eps:
+            raise ValueError("final norm eps differs from the layer norm eps")
+        self.qk_eps = float(sa0.q_norm.eps)
+        act = layers[0].mlp.act_fn
+        if isinstance(act, torch.nn.SiLU) or type(act).__name__ in ("SiLU", "SiLUActivation"):
+            self.activation = _lib.ACT_SILU
+        elif isinstance(act, torch.nn.GELU) and getattr(act, "approximate", "none") == "tanh":
+            self.activation = _lib.ACT_GELU_TANH
+        else:
+            raise ValueError(f"unsupported MLP activation {type(act).__name__}")
+        self.register_tokens = getattr(model, "register_tokens", None)
+        self.registers_in_loop = registers_in_loop
+        dims = MkxDims(L=self.L, H=self.H, NH=self.NH, HD=self.HD, I=self.I, A=self.A, max_rows=max_rows,
+                       max_batch=max_batch, max_mem_rows=max_mem_rows, max_src_rows=max_src_rows,
+                       weight_dtype=_lib.WEIGHTS_BF16, activation=self.activation, eps=self.eps, qk_eps=self.qk_eps)
+        w = MkxWeights(wqkv=_ptr(wqkv), wo=_ptr(wo), wqca=_ptr(wqca), woca=_ptr(woca), wg=_ptr(wg), wu=_ptr(wu),
+                       wd=_ptr(wd), qn=_ptr(qn), kn=_ptr(kn), qcan=_ptr(qcan), win=_ptr(win), bin=_ptr(b_in),
+                       wout=_ptr(wout), bout=_ptr(bout))
+        h = ctypes.c_void_p()
+        check(lib().mkx_create(ctypes.byref(dims), ctypes.byref(w), ctypes.c_void_p(_stream()), ctypes.byref(h)), "mkx_create")
+        self._h = h
+        self.nprog = int(lib().mkx_query(h, _lib.Q_GRID))
+        self.weight_bytes = int(lib().mkx_query(h, _lib.Q_WEIGHT_BYTES))
+        self.device = wqkv.device
+        self.cfg = {"block": int(lib().mkx_query(h, _lib.Q_BLOCK)), "lds_bytes": int(lib().mkx_query(h, _lib.Q_LDS_BYTES)),
+                    "grid": self.nprog, "PROFILE": False}
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                lib().mkx_destroy(h)
+            except Exception:  # interpreter shutdown
+                pass
+            self._h = None
+
+    # ------------------------------------------------------------------------------------------
+    def _args(self, x_t, mods, dt, past, action_dim, n_steps, mod_row0, first, cur_k=None, cur_v=None):
+        step = past.register_step
+        if x_t.dim() != 3 or x_t.shape[2] != self.A:
+            raise ValueError(f"x_t must be [B, T, {self.A}], got {tuple(x_t.shape)}")
+        x = x_t.float().contiguous()
+        B, T = x.shape[0], x.shape[1]
+        if not 1 <= action_dim <= self.A:
+            raise ValueError("action_dim out of range")
+        m = mods.float()
+        if m.dim() == 2:
+            if B != 1:
+                raise ValueError("mods [N, MODW] is for batch 1; pass [B, N, MODW]")
+            m = m[None]
+        m = m.contiguous()
+        modw = 9 * self.L * self.H + 2 * self.H
+        if m.shape[0] != B or m.shape[2] < modw:
+            raise ValueError(f"mods must be [B, N, >= {modw}], got {tuple(m.shape)}")
+        if m.shape[1] < mod_row0 + n_steps:
+            raise ValueError("mods has fewer rows than the steps to run")
+        sa_cos, sa_sin = step["sa_pe_first" if first and "sa_pe_first" in step else "sa_pe"]
+        ca_cos, ca_sin = step["ca_pe_first" if first and "ca_pe_first" in step else "ca_pe"]
+        sa_cos, sa_sin, ca_cos, ca_sin = (t.float().contiguous() for t in (sa_cos, sa_sin, ca_cos, ca_sin))
+        m_q = sa_cos.shape[0]
+        if sa_cos.shape != (m_q, self.HD) or ca_cos.shape != (m_q, self.HD) or m_q < T:
+            raise ValueError(f"RoPE tables must be [M_q >= T, {self.HD}]: {tuple(sa_cos.shape)}, {tuple(ca_cos.shape)}")
+        R = m_q - T
+        reg = None
+        if R > 0:
+            if self.register_tokens is None or self.register_tokens.shape[0] != R:
+                raise ValueError("RoPE tables cover register rows but the model has no matching register_tokens")
+            reg = self.register_tokens.to(torch.bfloat16).contiguous()
+        mem_kv = step["mem_kv"]
+        ca_kv = past.cross_attn_kv
+        if len(mem_kv) != self.L or len(ca_kv) != self.L:
+            raise ValueError("caches must hold one (k, v) pair per layer")
+
+        def bcheck(t, name):
+            if t.dtype != torch.bfloat16 or not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous bf16")
+            t4 = t if t.dim() == 4 else t[None]
+            if t4.shape[0] != B or t4.shape[2] != self.NH or t4.shape[3] != self.HD:
+                raise ValueError(f"{name} must be [B, rows, {self.NH}, {self.HD}], got {tuple(t.shape)}")
+            return t4
+
+        mk = [bcheck(k, "memory K") for k, _ in mem_kv]
+        mv = [bcheck(v, "memory V") for _, v in mem_kv]
+        kc = [bcheck(k, "source K") for k, _ in ca_kv]
+        vc = [bcheck(v, "source V") for _, v in ca_kv]
+        PM, SP = mk[0].shape[1], kc[0].shape[1]
+        if any(t.shape != mk[0].shape for t in mk + mv) or any(t.shape != kc[0].shape for t in kc + vc):
+            raise ValueError("per-layer caches must share one shape")
+        if "kv_start" in step and "ca_len" in step:
+            kvs, cal = step["kv_start"].to(torch.int32).contiguous(), step["ca_len"].to(torch.int32).contiguous()
+            kv_ptr, ca_ptr = kvs.data_ptr(), cal.data_ptr()
+        else:  # batch 1, reference layout: kv_start = cu_kv[0], S = cu_src[1] (src/mk_expert.py:321-322)
+            if B != 1:
+                raise ValueError("batched caches need register_step['kv_start'] and ['ca_len']")
+            kvs = step["cu_kv"].to(torch.int32).contiguous()
+            cal = step["cu_src"].to(torch.int32).contiguous()
+            kv_ptr, ca_ptr = kvs.data_ptr(), cal.data_ptr() + 4
+        x_out = torch.empty_like(x)
+        dtt = dt.float().reshape(-1)[:1].contiguous() if torch.is_tensor(dt) else torch.full((1,), float(dt), device=x.device)
+        a = MkxStepArgs()
+        a.x_in, a.x_out = x.data_ptr(), x_out.data_ptr()
+        a.mods, a.mods_stride_b, a.mods_stride_step, a.mod_row0 = m.data_ptr(), m.stride(0), m.stride(1), mod_row0
+        a.dt = dtt.data_ptr()
+        for l in range(self.L):
+            a.memk[l], a.memv[l], a.kca[l], a.vca[l] = mk[l].data_ptr(), mv[l].data_ptr(), kc[l].data_ptr(), vc[l].data_ptr()
+        a.mem_stride_b, a.src_stride_b = mk[0].stride(0), kc[0].stride(0)
+        a.kv_start, a.ca_len = kv_ptr, ca_ptr
+        a.sa_cos, a.sa_sin, a.ca_cos, a.ca_sin = sa_cos.data_ptr(), sa_sin.data_ptr(), ca_cos.data_ptr(), ca_sin.data_ptr()
+        a.reg_tok = _ptr(reg)
+        a.cur_k, a.cur_v = _ptr(cur_k), _ptr(cur_v)
+        a.n_steps, a.action_dim, a.T_act, a.R_reg, a.B, a.PM, a.SP = n_steps, action_dim, T, R, B, PM, SP
+        keep = (x, m, dtt, sa_cos, sa_sin, ca_cos, ca_sin, reg, kvs, cal, mk, mv, kc, vc)
+        return a, x_out, keep
+
+    def run(self, x_t: torch.Tensor, mods: torch.Tensor, dt, past, action_dim: int) -> torch.Tensor:
+        """x_t: [B, T, A] fp32 after Euler step 1; mods: [N, MODW] (B = 1) or [B, N, MODW], row 0 = step 1
+        (used already); returns x_t after step N (padded dims as the reference: 0 + dt * v)."""
+        n_steps = (mods.shape[-2]) - 1
+        if n_steps < 1:
+            raise ValueError("mods must hold at least two rows (step 1 and one more)")
+        a, x_out, keep = self._args(x_t, mods, dt, past, action_dim, n_steps, 1, first=False)
+        check(lib().mkx_run(self._h, ctypes.byref(a), ctypes.c_void_p(_stream())), "mkx_run")
+        self._keep = keep  # inputs must outlive the asynchronous launch
+        return x_out
+
+    def plan(self, x_t: torch.Tensor, mods: torch.Tensor, dt, past, action_dim: int) -> "LaunchPlan":
+        """Marshal the arguments of ``run`` once; ``LaunchPlan.launch()`` then enqueues the same launch with
+        no host-side work beyond the library call (the analogue of replaying the reference's captured graph,
+        profile_breakdown.py:107-130). The plan keeps its inputs alive; the output is ``plan.x_out``."""
+        n_steps = (mods.shape[-2]) - 1
+        a, x_out, keep = self._args(x_t, mods, dt, past, action_dim, n_steps, 1, first=False)
+        return LaunchPlan(self, a, x_out, keep)
+
+    def run_first(self, noise: torch.Tensor, mods1: torch.Tensor, dt, past, action_dim: int):
+        """Euler step 1 over [action rows || register rows] (what REKI's _expert_first_step computes):
+        returns (x after step 1, cur_k, cur_v) with cur_k/cur_v [L, B, R, NH, HD] bf16, the register rows'
+        normed+rotated K and V of each layer."""
+        R = 0 if self.register_tokens is None else self.register_tokens.shape[0]
+        B = noise.shape[0]
+        cur_k = torch.empty(self.L, B, R, self.NH, self.HD, device=noise.device, dtype=torch.bfloat16) if R else None
+        cur_v = torch.empty_like(cur_k) if R else None
+        a, x_out, keep = self._args(noise, mods1, dt, past, action_dim, 1, 0, first=True, cur_k=cur_k, cur_v=cur_v)
+        check(lib().mkx_run(self._h, ctypes.byref(a), ctypes.c_void_p(_stream())), "mkx_run")
+        self._keep = keep
+        return x_out, cur_k, cur_v
+
+    def barriers(self, n_steps: int) -> int:
+        return int(lib().mkx_barriers(self._h, n_steps))
+
+    def barrier_arrivals(self) -> int:
+        """Workgroup arrivals at grid barriers since the previous call (synchronises the device); equals
+        nprog * barriers(n_steps) after one launch (the reference's check, test_mk.py:44-45)."""
+        return int(lib().mkx_query(self._h, _lib.Q_BARRIER_COUNT))
+
+    def check(self) -> None:
+        """Synchronise and raise MkxError if a barrier wait of the last launch timed out."""
+        check(lib().mkx_check(self._h, ctypes.c_void_p(_stream())), "mkx_check")
+
+    def set_profile(self, n_steps: int | None) -> None:
+        """Per-barrier timestamps for later launches of up to n_steps steps (None turns them off)."""
+        if n_steps is None:
+            check(lib().mkx_set_profile(self._h, None, 0), "mkx_set_profile")
+            self._prof = None
+        else:
+            self._prof = torch.zeros(self.barriers(n_steps) + 2, dtype=torch.int64, device=self.device)
+            check(lib().mkx_set_profile(self._h, ctypes.c_void_p(self._prof.data_ptr()), self._prof.numel()), "mkx_set_profile")
+        self.cfg["PROFILE"] = n_steps is not None
+
+    def barrier_timestamps(self) -> torch.Tensor:
+        """ns clock taken by workgroup 0 at launch start (entry 0) and after each barrier of the last
+        profiled launch."""
+        if getattr(self, "_prof", None) is None:
+            raise RuntimeError("profiling is off")
+        torch.cuda.synchronize()
+        return self._prof.cpu()
+
+
+class LaunchPlan:
+    """A marshalled ``run`` call: launch() enqueues it on the current stream."""
+
+    def __init__(self, mk: ExpertMegakernel, args: MkxStepArgs, x_out: torch.Tensor, keep):
+        self.mk, self.args, self.x_out, self._keep = mk, args, x_out, keep
+        self._ref = ctypes.byref(self.args)
+
+    def launch(self, stream: int | None = None) -> torch.Tensor:
+        s = _stream() if stream is None else stream
+        check(lib().mkx_run(self.mk._h, self._ref, ctypes.c_void_p(s)), "mkx_run")
+        return self.x_out
+
+
+def install(model) -> ExpertMegakernel:
+    """Route the model's ``_expert_actions`` through the megakernel for steps 2..N; modulations and step 1
+    stay the model's own callables (src/mk_expert.py:521-536)."""
+    mk = ExpertMegakernel(model)
+    model._mk = mk
+
+    def _expert_actions(noise, cross_attn_cache, register_cache, state_cond, action_dim, num_steps):
+        mods, dt = model._step_modulations(num_steps, state_cond)
+        x_t, cur_k, cur_v = model._expert_first_step(noise, cross_attn_cache, register_cache, mods[..., :1, :], dt, action_dim)
+        if num_steps > 1:
+            x_t = mk.run(x_t, mods, dt, cross_attn_cache, action_dim)
+        return x_t, cur_k, cur_v
+
+    model._expert_actions = _expert_actions
+    return mk

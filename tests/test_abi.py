@@ -1,0 +1,74 @@
+"""The C ABI library (no GPU needed): it loads, exports every entry point include/mkx.h declares, reports
+errors through status codes, and validates arguments before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from mkx import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "mkx.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mkx_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = header_functions()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(_lib.EXPORTS) == set(names)
+
+
+def test_abi_version_and_status_strings():
+    L = _lib.lib()
+    assert L.mkx_abi_version() == 1
+    for s in range(7):
+        assert L.mkx_status_string(s).decode()
+    assert L.mkx_status_string(_lib.ETIMEOUT).decode().startswith("grid barrier")
+
+
+def _dims(**over):
+    d = dict(L=10, H=768, NH=12, HD=64, I=3072, A=32, max_rows=64, max_batch=1, max_mem_rows=96, max_src_rows=300,
+             weight_dtype=_lib.WEIGHTS_BF16, activation=_lib.ACT_SILU, eps=1e-6, qk_eps=1e-6)
+    d.update(over)
+    return _lib.MkxDims(**d)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(L=0), _lib.EINVAL), (dict(L=33), _lib.EINVAL), (dict(HD=128), _lib.EUNSUPPORTED),
+    (dict(NH=10), _lib.EINVAL), (dict(A=16), _lib.EUNSUPPORTED), (dict(weight_dtype=7), _lib.EUNSUPPORTED),
+    (dict(activation=5), _lib.EINVAL), (dict(max_batch=0), _lib.EINVAL), (dict(max_rows=200), _lib.EINVAL),
+    (dict(max_mem_rows=300), _lib.EINVAL), (dict(H=512, NH=8), _lib.EUNSUPPORTED),
+])
+def test_create_validates_dims_before_touching_the_device(over, status):
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    w = _lib.MkxWeights()
+    rc = L.mkx_create(ctypes.byref(_dims(**over)), ctypes.byref(w), None, ctypes.byref(h))
+    assert rc == status, L.mkx_last_error()
+    assert not h.value
+    assert L.mkx_last_error().decode()
+
+
+def test_create_rejects_null_weights_and_null_arguments():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    assert L.mkx_create(ctypes.byref(_dims()), ctypes.byref(_lib.MkxWeights()), None, ctypes.byref(h)) == _lib.EINVAL
+    assert L.mkx_create(None, None, None, ctypes.byref(h)) == _lib.EINVAL
+    assert L.mkx_run(None, None, None) == _lib.EINVAL
+    assert L.mkx_destroy(None) == _lib.OK
+    assert L.mkx_barriers(None, 9) == -1
+
+
+def test_struct_layouts_match_header_sizes():
+    # mkx_step_args: 4 per-layer tables of MKX_MAX_LAYERS pointers dominate the size
+    assert ctypes.sizeof(_lib.MkxStepArgs) > 4 * 32 * 8
+    assert ctypes.sizeof(_lib.MkxDims) == 14 * 4
+    assert ctypes.sizeof(_lib.MkxWeights) == 21 * 8
