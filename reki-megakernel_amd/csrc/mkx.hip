@@ -57,16 +57,14 @@ const void* kernel_of() { return reinterpret_cast<const void*>(&mkx_megakernel<H
 const void* pick_kernel(int H, int I) {
   if (H == 768 && I == 3072) return kernel_of<768, 3072>();
   if (H == 1024 && I == 4096) return kernel_of<1024, 4096>();
-  if (H == 128 && I == 256) return kernel_of<128, 256>();
-  if (H == 256 && I == 1024) return kernel_of<256, 1024>();
+  if (H == 256 && I == 512) return kernel_of<256, 512>();
   return nullptr;
 }
 
 int lds_of(int H, int I) {
   if (H == 768 && I == 3072) return Shape<768, 3072>::LDS;
   if (H == 1024 && I == 4096) return Shape<1024, 4096>::LDS;
-  if (H == 128 && I == 256) return Shape<128, 256>::LDS;
-  if (H == 256 && I == 1024) return Shape<256, 1024>::LDS;
+  if (H == 256 && I == 512) return Shape<256, 512>::LDS;
   return 0;
 }
 
@@ -77,8 +75,7 @@ inline int ceil4(int a) { return (a + 3) / 4 * 4; }
 long long frame_bytes(int H, int I, int nrp) {
   if (H == 768 && I == 3072) return Shape<768, 3072>::frame_bytes(nrp);
   if (H == 1024 && I == 4096) return Shape<1024, 4096>::frame_bytes(nrp);
-  if (H == 128 && I == 256) return Shape<128, 256>::frame_bytes(nrp);
-  if (H == 256 && I == 1024) return Shape<256, 1024>::frame_bytes(nrp);
+  if (H == 256 && I == 512) return Shape<256, 512>::frame_bytes(nrp);
   return 0;
 }
 long long step_bytes(int H, int nrp, int nxrows, int A) { return (long long)nrp * H * 4 + (long long)((nxrows * A * 4 + 255) / 256 * 256); }
@@ -263,7 +260,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   const int L = d.L, H = d.H, I = d.I;
   if (a->n_steps < 1) return fail(MKX_EINVAL, "n_steps must be >= 1");
-  if ((long long)a->B * a->T_act * a->action_dim * 4 > 72 * 1024) return fail(MKX_EUNSUPPORTED, "B * T_act * action_dim too large for the step tail");
+  if ((long long)a->B * a->T_act * a->action_dim * 4 > 88 * 1024) return fail(MKX_EUNSUPPORTED, "B * T_act * action_dim too large for the step tail");
   if (a->B < 1 || a->B > d.max_batch) return fail(MKX_EINVAL, "B out of range");
   if (a->T_act < 1 || a->R_reg < 0) return fail(MKX_EINVAL, "T_act must be >= 1 and R_reg >= 0");
   const int Mq = a->T_act + a->R_reg;
@@ -283,9 +280,13 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   const int NR = a->B * Mqp;
   const int NRP = ceil16(NR);
   if (NRP > MAX_ROWS_PADDED) return fail(MKX_EUNSUPPORTED, "B * (T_act + R_reg) too large for this build");
-  const int nown = ceil16(Mq), pmp = ceil16(a->PM);
-  if (2 * nown * 128 + ceil32(pmp + nown) * 128 + 4096 > 72 * 1024)
-    return fail(MKX_EUNSUPPORTED, "self-attention working set (memory + own rows) does not fit LDS");
+  // LDS working sets (layout in mkx_kernel.h): self-attention keeps own-row Q/K (hi + lo) and V^T (hi + lo)
+  // beside per-wave staging in the 88 KB activation region; the GEMM stages stage every sample's
+  // modulation slice (2 H floats) in 56 KB.
+  const int nown = ceil16(Mq), nown32 = ceil32(Mq);
+  if (4 * nown * 128 + 2 * nown32 * 128 + 4096 > 88 * 1024)
+    return fail(MKX_EUNSUPPORTED, "self-attention working set (own rows) does not fit LDS");
+  if ((long long)a->B * 2 * H * 4 > 56 * 1024) return fail(MKX_EUNSUPPORTED, "batch too large to stage its modulation slices in LDS");
   if (h->profile && 1 + a->n_steps * (8LL * L + 1) + 1 > h->prof_len) return fail(MKX_EINVAL, "profile buffer shorter than barriers + 1");
   // scratch: one frame per (step, layer), one step area per step; grown on demand
   const long long fb = frame_bytes(H, I, NRP);

@@ -7,7 +7,7 @@ import torch
 from mkx import synthetic as SY
 from oracle import expert_ref as ER
 
-TINY = SY.ExpertConfig(L=2, H=128, NH=2, I=256, T_act=5, R_reg=3, PM=16, kv_start=4, S=40, SP=48, ctx_dim=96,
+TINY = SY.ExpertConfig(L=2, H=256, NH=4, I=512, T_act=5, R_reg=3, PM=16, kv_start=4, S=40, SP=48, ctx_dim=96,
                        tdim=32, num_steps=4)
 
 

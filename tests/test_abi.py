@@ -45,7 +45,7 @@ def _dims(**over):
     (dict(L=0), _lib.EINVAL), (dict(L=33), _lib.EINVAL), (dict(HD=128), _lib.EUNSUPPORTED),
     (dict(NH=10), _lib.EINVAL), (dict(A=16), _lib.EUNSUPPORTED), (dict(weight_dtype=7), _lib.EUNSUPPORTED),
     (dict(activation=5), _lib.EINVAL), (dict(max_batch=0), _lib.EINVAL), (dict(max_rows=200), _lib.EINVAL),
-    (dict(max_mem_rows=300), _lib.EINVAL), (dict(H=512, NH=8), _lib.EUNSUPPORTED),
+    (dict(max_mem_rows=300), _lib.EINVAL), (dict(H=512, NH=8), _lib.EUNSUPPORTED), (dict(H=128, NH=2, I=256), _lib.EUNSUPPORTED),
 ])
 def test_create_validates_dims_before_touching_the_device(over, status):
     L = _lib.lib()
