@@ -29,10 +29,11 @@ int fail(int code, const std::string& msg) {
 constexpr unsigned SPIN_LIMIT = 1u << 20;
 constexpr int MAX_ROWS_PADDED = 512;
 
-// W [L][N][K] row-major -> chunks (l, t, kb): dst[l*dls + (t*tstride + toff + kb)*512 + lane*8 + j] =
-// W[l][t*16 + lane%16][kb*32 + 8(lane/16) + j] (the MFMA 16x16x32 operand layout).
+// W [L][N][K] row-major -> chunks (l, t, kb): dst[l*dls + (t'*tstride + toff + kb)*512 + lane*8 + j] =
+// W[l][t*16 + lane%16][kb*32 + 8(lane/16) + j] (the MFMA 16x16x32 operand layout). t' = t, or with `pairs`
+// the 16-column tiles of each 64-column head reordered 0, 2, 1, 3 (a task's d and d + 32 tiles adjacent).
 __global__ void pack_tiles(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst, int L, int N, int K,
-                           long long dls, int tstride, int toff) {
+                           long long dls, int tstride, int toff, int pairs) {
   const long long total = (long long)L * (N / 16) * (K / 32) * 64;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
@@ -43,7 +44,8 @@ __global__ void pack_tiles(const bf16_t* __restrict__ src, bf16_t* __restrict__ 
   const int t = (int)(r % (N / 16));
   const int l = (int)(r / (N / 16));
   const bf16_t* s = src + ((long long)l * N + t * 16 + lane % 16) * K + kb * 32 + 8 * (lane / 16);
-  bf16_t* d = dst + (long long)l * dls + ((long long)t * tstride + toff + kb) * 512 + lane * 8;
+  const int tp = pairs ? ((t & ~3) | ((t & 1) << 1) | ((t >> 1) & 1)) : t;
+  bf16_t* d = dst + (long long)l * dls + ((long long)tp * tstride + toff + kb) * 512 + lane * 8;
   *reinterpret_cast<u32x4*>(d) = *reinterpret_cast<const u32x4*>(s);
 }
 
@@ -70,7 +72,6 @@ int lds_of(int H, int I) {
 
 inline int ceil16(int a) { return (a + 15) / 16 * 16; }
 inline int ceil32(int a) { return (a + 31) / 32 * 32; }
-inline int ceil4(int a) { return (a + 3) / 4 * 4; }
 
 long long frame_bytes(int H, int I, int nrp) {
   if (H == 768 && I == 3072) return Shape<768, 3072>::frame_bytes(nrp);
@@ -78,7 +79,13 @@ long long frame_bytes(int H, int I, int nrp) {
   if (H == 256 && I == 512) return Shape<256, 512>::frame_bytes(nrp);
   return 0;
 }
-long long step_bytes(int H, int nrp, int nxrows, int A) { return (long long)nrp * H * 4 + (long long)((nxrows * A * 4 + 255) / 256 * 256); }
+long long step_bytes(int H, int I, int nrp, int nxrows, int A) {
+  long long x_off = 0;
+  if (H == 768 && I == 3072) x_off = Shape<768, 3072>::step_x_off(nrp);
+  if (H == 1024 && I == 4096) x_off = Shape<1024, 4096>::step_x_off(nrp);
+  if (H == 256 && I == 512) x_off = Shape<256, 512>::step_x_off(nrp);
+  return x_off + (long long)((nxrows * A * 4 + 255) / 256 * 256);
+}
 
 }  // namespace
 
@@ -96,6 +103,8 @@ struct mkx_handle {
   size_t frames_cap = 0;
   char* steps = nullptr;
   size_t steps_cap = 0;
+  bf16_t* vts = nullptr;  // per-launch V^T copies of the memory and cross-attention V caches
+  size_t vts_cap = 0;
   unsigned* dcnt = nullptr;
   BarState* bar = nullptr;
   long long* prof = nullptr;
@@ -109,7 +118,7 @@ struct mkx_handle {
 static void free_handle(mkx_handle* h) {
   if (!h) return;
   void* ptrs[] = {h->wqkv, h->wo, h->wqca, h->woca, h->wgu, h->wd, h->qn, h->kn, h->qcan, h->win, h->bin,
-                  h->wout, h->bout, h->frames, h->steps, h->dcnt, h->bar};
+                  h->wout, h->bout, h->frames, h->steps, h->vts, h->dcnt, h->bar};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete h;
@@ -202,18 +211,18 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   HCHK(alloc((void**)&h->woca, so * 2));
   HCHK(alloc((void**)&h->wgu, sgu * 2));
   HCHK(alloc((void**)&h->wd, sd * 2));
-  auto pack = [&](const void* src, bf16_t* dst, int N, int K, long long dls, int tstride, int toff) {
+  auto pack = [&](const void* src, bf16_t* dst, int N, int K, long long dls, int tstride, int toff, int pairs) {
     const long long total = (long long)L * (N / 16) * (K / 32) * 64;
     hipLaunchKernelGGL(pack_tiles, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)src, dst,
-                       L, N, K, dls, tstride, toff);
+                       L, N, K, dls, tstride, toff, pairs);
   };
-  pack(w->wqkv, h->wqkv, 3 * H, H, 3LL * H * H, H / 32, 0);
-  pack(w->wo, h->wo, H, H, (long long)H * H, H / 32, 0);
-  pack(w->wqca, h->wqca, H, H, (long long)H * H, H / 32, 0);
-  pack(w->woca, h->woca, H, H, (long long)H * H, H / 32, 0);
-  pack(w->wg, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), 0);
-  pack(w->wu, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), H / 32);
-  pack(w->wd, h->wd, H, I, (long long)H * I, I / 32, 0);
+  pack(w->wqkv, h->wqkv, 3 * H, H, 3LL * H * H, H / 32, 0, 1);
+  pack(w->wo, h->wo, H, H, (long long)H * H, H / 32, 0, 0);
+  pack(w->wqca, h->wqca, H, H, (long long)H * H, H / 32, 0, 1);
+  pack(w->woca, h->woca, H, H, (long long)H * H, H / 32, 0, 0);
+  pack(w->wg, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), 0, 0);
+  pack(w->wu, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), H / 32, 0);
+  pack(w->wd, h->wd, H, I, (long long)H * I, I / 32, 0, 0);
   HCHK(hipGetLastError());
   h->weight_bytes = (long long)(sq + 3 * so + sgu + sd) * 2;
   HCHK(alloc((void**)&h->qn, (size_t)L * HD * 2));
@@ -260,7 +269,9 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   const int L = d.L, H = d.H, I = d.I;
   if (a->n_steps < 1) return fail(MKX_EINVAL, "n_steps must be >= 1");
-  if ((long long)a->B * a->T_act * a->action_dim * 4 > 88 * 1024) return fail(MKX_EUNSUPPORTED, "B * T_act * action_dim too large for the step tail");
+  // step tail: x' of the real action dims (32 KB) and Wout's real-dim rows (64 KB) are staged in LDS
+  if ((long long)a->B * a->T_act * a->action_dim * 4 > 32 * 1024) return fail(MKX_EUNSUPPORTED, "B * T_act * action_dim too large for the step tail");
+  if ((long long)a->action_dim * H * 4 > 64 * 1024) return fail(MKX_EUNSUPPORTED, "action_dim * H too large for the step tail");
   if (a->B < 1 || a->B > d.max_batch) return fail(MKX_EINVAL, "B out of range");
   if (a->T_act < 1 || a->R_reg < 0) return fail(MKX_EINVAL, "T_act must be >= 1 and R_reg >= 0");
   const int Mq = a->T_act + a->R_reg;
@@ -276,29 +287,33 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   for (int l = 0; l < L; ++l)
     if (!a->memk[l] || !a->memv[l] || !a->kca[l] || !a->vca[l]) return fail(MKX_EINVAL, "null per-layer cache pointer");
   if (a->mods_stride_step < 9LL * L * H + 2 * H) return fail(MKX_EINVAL, "mods_stride_step is smaller than MODW = 9 L H + 2 H");
-  const int Mqp = ceil4(Mq);
+  const int Mqp = ceil16(Mq);  // each sample's rows start on a 16-row tile
   const int NR = a->B * Mqp;
   const int NRP = ceil16(NR);
   if (NRP > MAX_ROWS_PADDED) return fail(MKX_EUNSUPPORTED, "B * (T_act + R_reg) too large for this build");
-  // LDS working sets (layout in mkx_kernel.h): self-attention keeps own-row Q/K (hi + lo) and V^T (hi + lo)
-  // beside per-wave staging in the 88 KB activation region; the GEMM stages stage every sample's
-  // modulation slice (2 H floats) in 56 KB.
-  const int nown = ceil16(Mq), nown32 = ceil32(Mq);
-  if (4 * nown * 128 + 2 * nown32 * 128 + 4096 > 88 * 1024)
-    return fail(MKX_EUNSUPPORTED, "self-attention working set (own rows) does not fit LDS");
+  // LDS working sets (layout in mkx_kernel.h): self-attention keeps one query tile, the own rows' K and
+  // V^T (hi + lo, 32-key blocks, at most 128 rows) and the wave-merge area in the 88 KB activation region;
+  // the GEMM stages stage every sample's modulation slices (2 H floats) in 56 KB.
   if ((long long)a->B * 2 * H * 4 > 56 * 1024) return fail(MKX_EUNSUPPORTED, "batch too large to stage its modulation slices in LDS");
   if (h->profile && 1 + a->n_steps * (8LL * L + 1) + 1 > h->prof_len) return fail(MKX_EINVAL, "profile buffer shorter than barriers + 1");
+#ifdef MKX_TRACE
+  if (h->profile && mkx::TRACE_BASE + (2 + a->n_steps * (8LL * L + 1)) * h->G * 8 > h->prof_len)
+    return fail(MKX_EINVAL, "trace buffer too short");
+#endif
   // scratch: one frame per (step, layer), one step area per step; grown on demand
   const long long fb = frame_bytes(H, I, NRP);
-  const long long sb = step_bytes(H, NRP, a->B * a->T_act, d.A);
+  const long long sb = step_bytes(H, I, NRP, a->B * a->T_act, d.A);
   const size_t need_f = (size_t)fb * a->n_steps * L, need_s = (size_t)sb * a->n_steps;
-  if (need_f > h->frames_cap || need_s > h->steps_cap) {
+  const int PMP = ceil32(a->PM), SPP = ceil32(a->SP);
+  const size_t need_v = (size_t)L * a->B * (H / 64) * (PMP + SPP) * 128;
+  if (need_f > h->frames_cap || need_s > h->steps_cap || need_v > h->vts_cap) {
     HIPCHK(hipStreamSynchronize(stream));
     if (need_f > h->frames_cap) {
       if (h->frames) HIPCHK(hipFree(h->frames));
       h->frames = nullptr;
       h->frames_cap = 0;
       if (hipMalloc(&h->frames, need_f) != hipSuccess) return fail(MKX_ENOMEM, "activation frames");
+      HIPCHK(hipMemsetAsync(h->frames, 0, need_f, stream));  // operand slots no stage writes stay finite
       h->frames_cap = need_f;
     }
     if (need_s > h->steps_cap) {
@@ -306,7 +321,15 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
       h->steps = nullptr;
       h->steps_cap = 0;
       if (hipMalloc(&h->steps, need_s) != hipSuccess) return fail(MKX_ENOMEM, "step areas");
+      HIPCHK(hipMemsetAsync(h->steps, 0, need_s, stream));
       h->steps_cap = need_s;
+    }
+    if (need_v > h->vts_cap) {
+      if (h->vts) HIPCHK(hipFree(h->vts));
+      h->vts = nullptr;
+      h->vts_cap = 0;
+      if (hipMalloc(&h->vts, need_v) != hipSuccess) return fail(MKX_ENOMEM, "V^T copies");
+      h->vts_cap = need_v;
     }
   }
   Params p;
@@ -327,6 +350,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.sa_cos = a->sa_cos; p.sa_sin = a->sa_sin; p.ca_cos = a->ca_cos; p.ca_sin = a->ca_sin;
   p.reg_tok = (const bf16_t*)a->reg_tok; p.cur_k = (bf16_t*)a->cur_k; p.cur_v = (bf16_t*)a->cur_v;
   p.n_steps = a->n_steps; p.action_dim = a->action_dim; p.T = a->T_act; p.R = a->R_reg; p.B = a->B;
+  p.memvt = h->vts; p.cavt = h->vts + (size_t)L * a->B * (H / 64) * PMP * 64; p.SPP = SPP;
   p.PM = a->PM; p.SP = a->SP; p.L = L; p.Mq = Mq; p.Mqp = Mqp; p.NR = NR; p.NRP = NRP; p.A = d.A;
   p.act = d.activation == MKX_ACT_GELU_TANH ? 1 : 0;
   p.eps = d.eps; p.qk_eps = d.qk_eps; p.sm_scale = 1.0f / 8.0f;

@@ -55,6 +55,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
 __device__ __forceinline__ void st_sc1(void* base, uint32_t byte_off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, rsrc(base), byte_off, 0, CPOL_SC1);
 }
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_sc1_b64(void* base, uint32_t byte_off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, rsrc(base), byte_off, 0, CPOL_SC1);
+}
 __device__ __forceinline__ void st_sc1_b32(void* base, uint32_t byte_off, uint32_t v) {
   __builtin_amdgcn_raw_buffer_store_b32(v, rsrc(base), byte_off, 0, CPOL_SC1);
 }

@@ -2,8 +2,12 @@
 //
 // Schedule (mirrors expert_megakernel, src/mk_expert.py:302-426): an in-projection tail, then for each
 // step and layer eight stages (QKV, self-attention, out-proj + gated residual, cross-attention query,
-// cross-attention, out-proj + gated residual, gate/up, down + gated residual) and a step tail, each
-// followed by a grid barrier: 1 + n_steps * (8 L + 1) barriers.
+// cross-attention, out-proj + gated residual, gate/up, down + gated residual) and a step tail. Every stage
+// is followed by one grid barrier: 1 + n_steps * (8 L + 1) barriers.
+//
+// Code layout: the kernel is one flat loop over stages, and each kind of stage (GEMM, self-attention,
+// cross-attention, tail) is a single inlined body driven by a runtime descriptor. The whole loop stays
+// resident in the instruction cache; a stage never waits on instruction fetch.
 //
 // Work decomposition for 256 CUs: every linear layer is cut into 16-column output tiles (one task per
 // workgroup, K = H per task; the down projection is split over K into I/H tasks per tile whose fp32
@@ -12,10 +16,24 @@
 // and the per-sample modulation slices (or, for attention, the cached K/V). After the barrier only the
 // activations are loaded, straight into VGPRs.
 //
+// Activation frames are fragment-major: a buffer of C columns and NRP rows is cut into 2 KB blocks
+// (32-column block kb, 16-row tile rt) at ((kb * RT + rt) * 2) KB, lane-major inside (lane = row % 16 +
+// 16 * (8-column group)). "fp32" buffers hold columns 0-3 of each 8-column group in the first 1 KB and 4-7
+// in the second; "split" buffers hold an MFMA operand fragment directly: 8 bf16 high parts per lane in the
+// first 1 KB and the 8 bf16 residuals in the second. A wave loads one split operand fragment (16 rows x 32
+// columns, hi and lo) with two contiguous 1 KB loads and feeds it to the MFMA unchanged.
+//
 // Numerics ("split-bf16"): weights are bf16; every activation operand of an MFMA is split into a bf16 high
 // part and a bf16 residual (a = hi + lo, |lo| <= ulp(hi)/2), and both are multiplied, so the products are
 // those of the fp32 activation to ~2^-17 relative. Activations, softmax probabilities and the residual
-// stream stay fp32 between stages. The kernel therefore reproduces the fp32 eager expert (not the bf16
+// stream stay fp32 between stages. The split is done once, by the producer of an operand: attention writes
+// its output split; the residual stages write h (fp32, for the next residual add), y = h * (1 + scale) of
+// the next AdaRMS (split) and per-tile partial sums of squares of h; the AdaRMS GEMM then computes
+// rstd(h) * (y W^T) + shift W^T (src/mk_expert.py:93-122 rearranged), with shift W^T taken by the MFMA as
+// one extra row tile of per-sample shift rows. The QKV and cross-attention query projections are computed
+// per (head, d-quarter pair) so their epilogue holds d and d + 32 of a row: it applies the q/k norm weight
+// and RoPE and writes the attention operands split (V directly in the transposed P V layout), leaving only
+// the per-row RMS factor, which attention folds into the scores. The kernel therefore reproduces the fp32 eager expert (not the bf16
 // rounding points of the reference's Triton kernel, src/mk_expert.py:119, 169-172, 220): a bf16-activation
 // kernel sits at the bf16 rounding-noise floor of the model (~1.5e-3 mean |delta| at full depth), which
 // is most of the 2e-3 parity budget.
@@ -39,11 +57,14 @@ struct Params {
   const int* kv_start; const int* ca_len;
   const float* sa_cos; const float* sa_sin; const float* ca_cos; const float* ca_sin;
   const bf16_t* reg_tok; bf16_t* cur_k; bf16_t* cur_v;
+  // V^T copies of the memory / cross-attention V caches, made once per launch:
+  // [L][B][NH][PMP/32 or SPP/32 key blocks][4 d-slices][512 bf16]
+  bf16_t* memvt; bf16_t* cavt; int SPP;
   int n_steps, action_dim, T, R, B, PM, SP, L, Mq, Mqp, NR, NRP, A, act;
   float eps, qk_eps, sm_scale;
   // scratch
   char* frames; long long frame_bytes;   // [n_steps * L] layer frames
-  char* steps; long long step_bytes;     // [n_steps] step areas: h0 (fp32, tile-major) + x (fp32)
+  char* steps; long long step_bytes;     // [n_steps] step areas: h0 (fp32, fragment-major) + x (fp32)
   unsigned* dcnt;                        // [H/16] split-K arrival counters
   BarState* bar; unsigned nx[MAX_XCD]; unsigned xmask;
   long long* prof; int profile;
@@ -66,44 +87,95 @@ struct Shape {
   static constexpr int MODS = ABUF + RED_BYTES, MODS_BYTES = 56 * 1024;  // per-sample modulation slices
   static constexpr int SMALL = ABUF + ABUF_BYTES, SMALL_BYTES = 4 * 1024;
   static constexpr int LDS = SMALL + SMALL_BYTES;
-  static constexpr int RB_FIT = 144 / (KPW * 8);  // row tiles per GEMM pass held in VGPRs (fp32)
-  static constexpr int RBMAX = RB_FIT > 4 ? 4 : RB_FIT;
-  static constexpr int MAXKT = (256 + 128) / 16;  // self-attention key tiles (PM <= 256, M_q <= 128)
-  static constexpr int MAX_MOD_SAMPLES = MODS_BYTES / (2 * H * 4);
+  static constexpr int RB_FIT = 144 / (KPW * 8);  // row tiles per GEMM pass held in VGPRs (hi + lo)
+  static constexpr int RBMAX = RB_FIT > 3 ? 3 : RB_FIT;
   static_assert(H % 256 == 0 && I % H == 0, "H must be a multiple of 256 and I a multiple of H");
   static_assert(KPW >= 1 && RBMAX >= 1, "tile does not fit registers");
   static_assert(NKB * 1024 * 2 <= WBUF_BYTES, "gate/up weight tile pair must fit the weight buffer");
-  static_assert(NWAVES * RBMAX * 2 * 1024 <= RED_BYTES, "cross-wave reduction must fit LDS");
+  static_assert(NWAVES * (RBMAX + 1) * 2 * 1024 <= RED_BYTES, "cross-wave reduction must fit LDS");
   static_assert(LDS <= 160 * 1024 - 256, "LDS budget");
-  // frame layout (bytes), tile-major fp32 buffers [cols/16][NRP][16]
-  __host__ __device__ static long long qkv_off(int) { return 0; }
-  __host__ __device__ static long long ysa_off(int nrp) { return (long long)nrp * 3 * H * 4; }
-  __host__ __device__ static long long h2_off(int nrp) { return ysa_off(nrp) + (long long)nrp * H * 4; }
-  __host__ __device__ static long long qca_off(int nrp) { return h2_off(nrp) + (long long)nrp * H * 4; }
-  __host__ __device__ static long long yca_off(int nrp) { return qca_off(nrp) + (long long)nrp * H * 4; }
-  __host__ __device__ static long long h3_off(int nrp) { return yca_off(nrp) + (long long)nrp * H * 4; }
-  __host__ __device__ static long long g_off(int nrp) { return h3_off(nrp) + (long long)nrp * H * 4; }
-  __host__ __device__ static long long hl_off(int nrp) { return g_off(nrp) + (long long)nrp * I * 4; }
-  __host__ __device__ static long long part_off(int nrp) { return hl_off(nrp) + (long long)nrp * H * 4; }
-  __host__ __device__ static long long frame_bytes(int nrp) { return part_off(nrp) + (long long)SK * nrp * H * 4; }
+  // frame layout (bytes), buffers of NRP rows; HB = NRP * H * 4:
+  //   qs, ks: split q / k (roped, not normed) | vt: split V^T blocks per (sample, head) (2 HB) | ysa split |
+  //   h2 fp32 | y2 split | qcas split | yca split | h3 fp32 | y3 split | g split (I columns) | hl fp32 |
+  //   yl split | part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ssca [NH][2][NRP] | ss2, ss3, ssl [HT][NRP]
+  __host__ __device__ static long long hb(int nrp) { return (long long)nrp * H * 4; }
+  __host__ __device__ static long long qs_off(int) { return 0; }
+  __host__ __device__ static long long ks_off(int nrp) { return hb(nrp); }
+  __host__ __device__ static long long vtb_off(int nrp) { return 2 * hb(nrp); }
+  __host__ __device__ static long long ysa_off(int nrp) { return 4 * hb(nrp); }
+  __host__ __device__ static long long h2_off(int nrp) { return 5 * hb(nrp); }
+  __host__ __device__ static long long y2_off(int nrp) { return 6 * hb(nrp); }
+  __host__ __device__ static long long qcas_off(int nrp) { return 7 * hb(nrp); }
+  __host__ __device__ static long long yca_off(int nrp) { return 8 * hb(nrp); }
+  __host__ __device__ static long long h3_off(int nrp) { return 9 * hb(nrp); }
+  __host__ __device__ static long long y3_off(int nrp) { return 10 * hb(nrp); }
+  __host__ __device__ static long long g_off(int nrp) { return 11 * hb(nrp); }
+  __host__ __device__ static long long hl_off(int nrp) { return (11 + SK) * hb(nrp); }
+  __host__ __device__ static long long yl_off(int nrp) { return (12 + SK) * hb(nrp); }
+  __host__ __device__ static long long part_off(int nrp) { return (13 + SK) * hb(nrp); }
+  __host__ __device__ static long long ssqk_off(int nrp) { return (13 + 2 * SK) * hb(nrp); }
+  __host__ __device__ static long long ssca_off(int nrp) { return ssqk_off(nrp) + 4LL * NH * nrp * 4; }
+  __host__ __device__ static long long ss2_off(int nrp) { return ssca_off(nrp) + 2LL * NH * nrp * 4; }
+  __host__ __device__ static long long ss3_off(int nrp) { return ss2_off(nrp) + (long long)HT * nrp * 4; }
+  __host__ __device__ static long long ssl_off(int nrp) { return ss3_off(nrp) + (long long)HT * nrp * 4; }
+  __host__ __device__ static long long frame_bytes(int nrp) { return ssl_off(nrp) + (long long)HT * nrp * 4; }
+  // step area: h0 fp32 | y0 split | ss0 [HT][NRP] | x [B*T][A] fp32
+  __host__ __device__ static long long step_x_off(int nrp) { return 2 * hb(nrp) + (long long)HT * nrp * 4; }
 };
 
+// byte offset of the 4-float piece (row r, columns c .. c+3; c % 4 == 0) of a fragment-major fp32 buffer
+__host__ __device__ __forceinline__ uint32_t fpiece(int r, int c, int RT) {
+  return (uint32_t)((((c >> 5) * RT + (r >> 4)) * 2 + ((c >> 2) & 1)) * 1024 + ((r & 15) + 16 * ((c & 31) >> 3)) * 16);
+}
+// byte offset of the 4 high parts (row r, columns c .. c+3) of a split buffer; the residuals are 1 KB later
+__host__ __device__ __forceinline__ uint32_t spiece(int r, int c, int RT) {
+  return (uint32_t)(((c >> 5) * RT + (r >> 4)) * 2048 + ((r & 15) + 16 * ((c & 31) >> 3)) * 16 + (c & 4) * 2);
+}
+
 enum Stage { ST_QKV = 0, ST_SA, ST_O, ST_CAQ, ST_CA, ST_CAO, ST_GU, ST_DOWN, ST_TAIL };
+enum { K_QKV = 0, K_RES = 1, K_GU = 2, K_SPLIT = 3 };
+
+// Optional per-workgroup phase trace (diagnostic builds with MKX_TRACE): clock of phase `slot` of the
+// interval after barrier ep, at prof[TRACE_BASE + (ep * G + wg) * 8 + slot].
+constexpr long long TRACE_BASE = 8192;
+#ifdef MKX_TRACE
+#define MKX_TR(c, slot)                                                                                          \
+  do {                                                                                                           \
+    if ((c).tid == 0 && (c).p.profile) (c).p.prof[TRACE_BASE + ((long long)(c).ep * (c).G + (c).wg) * 8 + (slot)] = clock100(); \
+  } while (0)
+#else
+#define MKX_TR(c, slot) \
+  do {                  \
+  } while (0)
+#endif
 
 template <class S>
 struct Ctx {
   CP& p;
   char* smem;
-  int wg, G, wave, lane, tid;
+  int wg, G, wave, lane, tid, RT;
+  unsigned ep = 0;  // barriers passed so far in this launch
   float dt;
   __device__ Ctx(CP& p_, char* smem_) : p(p_), smem(smem_) {
-    wg = blockIdx.x; G = gridDim.x; tid = threadIdx.x; wave = tid >> 6; lane = tid & 63;
+    wg = blockIdx.x; G = gridDim.x; tid = threadIdx.x; lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so offsets built from it stay scalar
+    RT = p.NRP >> 4;
   }
   __device__ char* frame(int s, int l) const { return p.frames + (long long)(s * p.L + l) * p.frame_bytes; }
-  __device__ float* h0(int s) const { return (float*)(p.steps + (long long)s * p.step_bytes); }
-  __device__ float* xstep(int s) const { return (float*)(p.steps + (long long)s * p.step_bytes + (long long)p.NRP * S::H * 4); }
+  __device__ char* step(int s) const { return p.steps + (long long)s * p.step_bytes; }
+  __device__ float* h0(int s) const { return (float*)step(s); }
+  __device__ float* y0(int s) const { return (float*)(step(s) + S::hb(p.NRP)); }
+  __device__ float* ss0(int s) const { return (float*)(step(s) + 2 * S::hb(p.NRP)); }
+  __device__ float* xstep(int s) const { return (float*)(step(s) + S::step_x_off(p.NRP)); }
+  // layer inputs: the residual stream h (fp32), its AdaRMS operand y (split) and sums of squares
   __device__ const float* h_in(int s, int l) const {
     return l == 0 ? h0(s) : (const float*)(frame(s, l - 1) + S::hl_off(p.NRP));
+  }
+  __device__ const float* y_in(int s, int l) const {
+    return l == 0 ? y0(s) : (const float*)(frame(s, l - 1) + S::yl_off(p.NRP));
+  }
+  __device__ const float* ss_in(int s, int l) const {
+    return l == 0 ? ss0(s) : (const float*)(frame(s, l - 1) + S::ssl_off(p.NRP));
   }
   __device__ const float* modrow(int b, int s) const {
     return p.mods + (long long)b * p.mods_sb + (long long)(p.mod_row0 + s) * p.mods_ss;
@@ -117,6 +189,12 @@ struct Ctx {
 // ------------------------------------------------------------------------------------------------
 // helpers
 
+__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ f32x4 as_f4(u32x4 v) { return __builtin_bit_cast(f32x4, v); }
+__device__ __forceinline__ u32x4 as_u4(f32x4 v) { return __builtin_bit_cast(u32x4, v); }
+
 template <class S>
 __device__ __forceinline__ void dma_w(Ctx<S>& c, char* dst, const bf16_t* src, int nchunks) {
   for (int k = c.wave; k < nchunks; k += NWAVES) dma16(src + (long long)k * 512 + c.lane * 8, dst + k * 1024);
@@ -127,6 +205,23 @@ __device__ __forceinline__ void dma_f32(Ctx<S>& c, char* dst, const float* src, 
   for (int k = c.wave; k < nfloats / 256; k += NWAVES) dma16(src + (long long)k * 256 + c.lane * 4, dst + k * 1024);
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+// split 8 fp32 values into bf16 high parts and bf16 residuals
+__device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h[j] = cvt_pk(f[2 * j], f[2 * j + 1]);
+    l[j] = cvt_pk(f[2 * j] - __uint_as_float(h[j] << 16), f[2 * j + 1] - __uint_as_float(h[j] & 0xffff0000u));
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
+}
 __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -134,33 +229,20 @@ __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
     f[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
   }
 }
-__device__ __forceinline__ u32x4 pack8(const float* f) {
-  u32x4 v;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = pack2(f[2 * j], f[2 * j + 1]);
-  return v;
-}
-// split 8 fp32 values into bf16 high parts and bf16 residuals
-__device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
-  float r[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = f[j] - rbf(f[j]);
-  const u32x4 h = pack8(f), l = pack8(r);
-  hi = *reinterpret_cast<const bf16x8*>(&h);
-  lo = *reinterpret_cast<const bf16x8*>(&l);
+// 4 fp32 values -> hi and lo bf16 pairs at off and off + 1024 of a split buffer, written through
+__device__ __forceinline__ void st_split4(void* base, uint32_t off, f32x4 v) {
+  u32x2 h, l;
+  h[0] = cvt_pk(v[0], v[1]);
+  h[1] = cvt_pk(v[2], v[3]);
+  l[0] = cvt_pk(v[0] - __uint_as_float(h[0] << 16), v[1] - __uint_as_float(h[0] & 0xffff0000u));
+  l[1] = cvt_pk(v[2] - __uint_as_float(h[1] << 16), v[3] - __uint_as_float(h[1] & 0xffff0000u));
+  st_sc1_b64(base, off, h);
+  st_sc1_b64(base, off + 1024, l);
 }
 __device__ __forceinline__ u32x4 lds16(const char* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void sts16(char* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ bf16x8 ldsfrag(const char* p) { return *reinterpret_cast<const bf16x8*>(p); }
-__device__ __forceinline__ void load8f(const float* p, float* f) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
-  f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3]; f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
-}
-// 8 fp32 values (32 bytes) at element offset `off` of a frame buffer, written through (sc1)
-__device__ __forceinline__ void st8f_sc1(float* base, long long off, const float* v) {
-  st_sc1(base, (uint32_t)(off * 4), u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
-  st_sc1(base, (uint32_t)(off * 4 + 16), u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
-}
+__device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
 __device__ __forceinline__ float act_fn(float x, int gelu) {
   if (gelu) {
@@ -169,777 +251,939 @@ __device__ __forceinline__ float act_fn(float x, int gelu) {
   }
   return x / (1.0f + __expf(-x));
 }
-
-// ------------------------------------------------------------------------------------------------
-// GEMM stage: out tile (16 columns, all rows) = A @ W_tile^T for each task of this workgroup.
-//   ADARMS: A = h * rstd(h) * (1 + scale) + shift from the fp32 residual stream (src/mk_expert.py:93-122;
-//           the per-sample scale/shift slices were staged in LDS by the prefetch); otherwise A is an fp32
-//           activation frame.
-//   KIND PLAIN: fp32 store (qkv, cross-attention query); RES: h_out = res + acc * gate (:162-172);
-//   GU: act(gate) * up (:404-413); SPLIT: K-split partial, the last split of a tile sums the partials in
-//   split order and applies RES.
-// K (= H per task) is split over the 4 waves; the wave partials are summed through LDS.
-enum { K_PLAIN = 0, K_RES = 1, K_GU = 2, K_SPLIT = 3 };
-
-template <class S, int NT>
-__device__ __forceinline__ void red_sum8(Ctx<S>& c, int r, int nt, int half, float* out) {
-  const float* red = (const float*)(c.smem + S::RED);
-  const int rt = r >> 4, rr = r & 15;
+__device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) out[j] = 0.f;
-#pragma unroll
-  for (int w = 0; w < NWAVES; ++w) {
-    const float* src = red + ((w * S::RBMAX + rt) * NT + nt) * 256 + rr * 16 + half * 8;
-    const f32x4 a = *reinterpret_cast<const f32x4*>(src), b = *reinterpret_cast<const f32x4*>(src + 4);
-    out[0] += a[0]; out[1] += a[1]; out[2] += a[2]; out[3] += a[3];
-    out[4] += b[0]; out[5] += b[1]; out[6] += b[2]; out[7] += b[3];
-  }
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
 }
 
-// staged per-sample modulation slice: ADARMS stages hold [scale | shift] (2H), RES stages hold gate (H)
+// staged per-sample modulation slice: AdaRMS stages hold [scale | shift] (2H), gated-residual stages hold gate (H)
 template <class S>
 __device__ __forceinline__ const float* mods_lds(Ctx<S>& c, int b, int width) {
   return (const float*)(c.smem + S::MODS) + (long long)b * width;
 }
 
-template <class S, int NT, int KIND, bool ADARMS>
-__device__ void gemm_stage(Ctx<S>& c, int s, int ntask, const bf16_t* wbase, long long wtask_stride, const float* asrc,
-                           float* out, const float* res, float* part, int split_tiles) {
+// ------------------------------------------------------------------------------------------------
+// Stage descriptor: what one stage computes, where its operands live, and what to prefetch for it.
+
+struct Desc {
+  int st, s, l;
+  bool first, last;
+  // GEMM stages
+  const bf16_t* w; long long wstride;  // packed weight chunks; task t's tile at w + t * wstride (not split)
+  const float* a;                      // split operand frame
+  float* out; const float* res; float* part;
+  float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
+  const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][NRP]
+  int ntask, tiles, kind, nt;
+  int qmode;                           // K_QKV: 0 = self-attention q/k/v, 1 = cross-attention query
+  // staged modulation slices (H floats each, per sample): AdaRMS stages: shift; residual stages: gate, then
+  // the scale of the next AdaRMS
+  int mod_off, mod_off2;
+};
+
+template <class S>
+__device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
+  CP& p = c.p;
+  Desc d;
+  d.first = g == 0;
+  d.last = false;
+  d.w = nullptr; d.wstride = 0; d.a = nullptr; d.out = nullptr; d.res = nullptr; d.part = nullptr;
+  d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr;
+  d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.qmode = 0; d.mod_off = 0; d.mod_off2 = 0;
+  if (g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
+  const int per_step = 8 * p.L + 1;
+  const int h = g - 1;
+  d.s = h / per_step;
+  const int j = h - d.s * per_step;
+  if (j == 8 * p.L) {
+    d.st = ST_TAIL; d.l = p.L - 1; d.last = d.s + 1 == p.n_steps;
+    return d;
+  }
+  d.l = j >> 3;
+  d.st = j & 7;
+  const int NRP = p.NRP, l = d.l;
+  char* fr = c.frame(d.s, l);
+  // AdaRMS slices of a layer's mods row (src/mk_expert.py:302-426): [scale | shift | gate] for self-attention,
+  // cross-attention and the MLP; the next layer's (or the final) AdaRMS scale follows at 9 (l + 1) H
+  const int m_sa = 9 * l * S::H, m_ca = m_sa + 3 * S::H, m_mlp = m_sa + 6 * S::H, m_next = m_sa + 9 * S::H;
+  d.wstride = (long long)S::NKB * 512;
+  switch (d.st) {
+    case ST_QKV:  // task ((kind * NH + head) * 2 + j): columns 16 j + [0, 16) and 16 j + 32 + [0, 16) of the head
+      d.w = p.wqkv + l * p.s_qkv; d.wstride = 2LL * S::NKB * 512; d.a = c.y_in(d.s, l); d.ssin = c.ss_in(d.s, l);
+      d.out = (float*)(fr + S::qs_off(NRP)); d.yout = (float*)(fr + S::ks_off(NRP)); d.part = (float*)(fr + S::vtb_off(NRP));
+      d.ssout = (float*)(fr + S::ssqk_off(NRP)); d.ntask = d.tiles = 6 * S::NH; d.nt = 2; d.mod_off = m_sa + S::H;
+      break;
+    case ST_O:
+      d.w = p.wo + l * p.s_o; d.a = (const float*)(fr + S::ysa_off(NRP)); d.out = (float*)(fr + S::h2_off(NRP));
+      d.yout = (float*)(fr + S::y2_off(NRP)); d.ssout = (float*)(fr + S::ss2_off(NRP));
+      d.res = c.h_in(d.s, l); d.ntask = d.tiles = S::HT; d.kind = K_RES; d.mod_off = m_sa + 2 * S::H; d.mod_off2 = m_ca;
+      break;
+    case ST_CAQ:
+      d.w = p.wqca + l * p.s_o; d.wstride = 2LL * S::NKB * 512; d.a = (const float*)(fr + S::y2_off(NRP));
+      d.ssin = (const float*)(fr + S::ss2_off(NRP)); d.out = (float*)(fr + S::qcas_off(NRP));
+      d.ssout = (float*)(fr + S::ssca_off(NRP)); d.ntask = d.tiles = 2 * S::NH; d.nt = 2; d.qmode = 1; d.mod_off = m_ca + S::H;
+      break;
+    case ST_CAO:
+      d.w = p.woca + l * p.s_o; d.a = (const float*)(fr + S::yca_off(NRP)); d.out = (float*)(fr + S::h3_off(NRP));
+      d.yout = (float*)(fr + S::y3_off(NRP)); d.ssout = (float*)(fr + S::ss3_off(NRP));
+      d.res = (const float*)(fr + S::h2_off(NRP)); d.ntask = d.tiles = S::HT; d.kind = K_RES;
+      d.mod_off = m_ca + 2 * S::H; d.mod_off2 = m_mlp;
+      break;
+    case ST_GU:
+      d.w = p.wgu + l * p.s_gu; d.wstride = 2LL * S::NKB * 512; d.a = (const float*)(fr + S::y3_off(NRP));
+      d.ssin = (const float*)(fr + S::ss3_off(NRP)); d.out = (float*)(fr + S::g_off(NRP));
+      d.ntask = d.tiles = S::IT; d.kind = K_GU; d.nt = 2; d.mod_off = m_mlp + S::H;
+      break;
+    case ST_DOWN:
+      d.w = p.wd + l * p.s_d; d.a = (const float*)(fr + S::g_off(NRP)); d.out = (float*)(fr + S::hl_off(NRP));
+      d.yout = (float*)(fr + S::yl_off(NRP)); d.ssout = (float*)(fr + S::ssl_off(NRP));
+      d.res = (const float*)(fr + S::h3_off(NRP)); d.part = (float*)(fr + S::part_off(NRP));
+      d.tiles = S::HT; d.ntask = S::HT * S::SK; d.kind = K_SPLIT; d.mod_off = m_mlp + 2 * S::H; d.mod_off2 = m_next;
+      break;
+    default:
+      break;
+  }
+  return d;
+}
+
+template <class S>
+__device__ __forceinline__ const bf16_t* wtile(const Desc& d, int t) {
+  if (d.kind == K_SPLIT) return d.w + ((long long)(t % d.tiles) * S::SK + t / d.tiles) * S::NKB * 512;
+  return d.w + (long long)t * d.wstride;
+}
+
+// ------------------------------------------------------------------------------------------------
+// GEMM stage: out tile (16 columns, all rows) of A @ W^T for each task of this workgroup, computed
+// transposed (D^T = W_tile A^T) so that each lane's accumulator is 4 consecutive output columns of one row:
+// one 16-byte piece of the fragment-major output. A is a split operand frame (hi and lo both multiplied).
+//   AdaRMS stages (K_QKV: q/k/v, cross-attention query; K_GU): A = y = h * (1 + scale) was written by the
+//     producer of h, so out = rstd(h) * (y W^T) + shift W^T (src/mk_expert.py:93-122); rstd comes from the
+//     producer's per-tile sums of squares, shift W^T from an extra MFMA row tile whose rows are the
+//     samples' shift slices. K_QKV: see qk_piece / the V^T epilogue; K_GU stores act(gate) * up split
+//     (:404-413).
+//   K_RES: h_out = res + acc * gate (:162-172), stored fp32, plus y = h_out * (1 + next scale) split and
+//     the tile's sums of squares of h_out; K_SPLIT: K-split partial, the last split of a tile sums the
+//     partials in split order and applies K_RES.
+// K (= H per task) is split over the 4 waves; the wave partials are summed through LDS.
+
+// residual epilogue of one 4-column piece: h = res + v * gate; stores h, y = h (1 + next scale) and the
+// piece's share of the row's sum of squares (lanes L, L^16, L^32, L^48 hold one row's 16 columns)
+template <class S>
+__device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, int row, int col, int L, f32x4 v) {
+  const uint32_t off = fpiece(row, col, c.RT);
+  const float* ml = mods_lds(c, c.sample_of(row), 2 * S::H);
+  const f32x4 h = as_f4(ld16((const char*)d.res + off)) + v * ldf4(ml + col);
+  st_sc1(d.out, off, as_u4(h));
+  st_split4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)));
+  float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  if (L < 16) st_sc1_b32(d.ssout, (uint32_t)(((long long)tile * c.p.NRP + row) * 4), __float_as_uint(ss));
+}
+
+// q/k epilogue of one row: xa, xb = columns d0 .. d0+3 and d0+32 .. d0+35 of head hd (kind 0 = q, 1 = k;
+// qmode 1 = cross-attention query). Stores the row's share of the head's sum of squares (lanes L, L^16,
+// L^32, L^48 hold the task's 32 columns) and u = rope(x (1 + w)) split (src/mk_expert.py:175-193; the RMS
+// factor is applied to the scores).
+template <class S>
+__device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int hd, int j, int row, int L, f32x4 xa, f32x4 xb) {
+  CP& p = c.p;
+  float ss = xa[0] * xa[0] + xa[1] * xa[1] + xa[2] * xa[2] + xa[3] * xa[3] + xb[0] * xb[0] + xb[1] * xb[1] + xb[2] * xb[2] + xb[3] * xb[3];
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  if (L < 16) st_sc1_b32(d.ssout, (uint32_t)((((long long)(kind * S::NH + hd) * 2 + j) * p.NRP + row) * 4), __float_as_uint(ss));
+  const int d0 = 16 * j + 4 * (L >> 4);
+  const bf16_t* nw = (d.qmode ? p.qcan : kind == 0 ? p.qn : p.kn) + d.l * HD;
+  const uint2 wa = *reinterpret_cast<const uint2*>(nw + d0), wb = *reinterpret_cast<const uint2*>(nw + d0 + 32);
+  const f32x4 ga = {1.0f + __uint_as_float(wa.x << 16), 1.0f + __uint_as_float(wa.x & 0xffff0000u),
+                    1.0f + __uint_as_float(wa.y << 16), 1.0f + __uint_as_float(wa.y & 0xffff0000u)};
+  const f32x4 gb = {1.0f + __uint_as_float(wb.x << 16), 1.0f + __uint_as_float(wb.x & 0xffff0000u),
+                    1.0f + __uint_as_float(wb.y << 16), 1.0f + __uint_as_float(wb.y & 0xffff0000u)};
+  const int pos = min(row - c.sample_of(row) * p.Mqp, p.Mq - 1);
+  const float* cs = (d.qmode ? p.ca_cos : p.sa_cos) + pos * HD + d0;
+  const float* sn = (d.qmode ? p.ca_sin : p.sa_sin) + pos * HD + d0;
+  const f32x4 za = xa * ga, zb = xb * gb;
+  const f32x4 ua = za * ldf4(cs) - zb * ldf4(sn);
+  const f32x4 ub = zb * ldf4(cs + 32) + za * ldf4(sn + 32);
+  float* buf = kind == 0 ? d.out : d.yout;
+  st_split4(buf, spiece(row, hd * HD + d0, c.RT), ua);
+  st_split4(buf, spiece(row, hd * HD + d0 + 32, c.RT), ub);
+}
+
+template <class S>
+__device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
   constexpr int KPW = S::KPW, RB = S::RBMAX;
-  const int NRP = c.p.NRP;
-  const int RT = NRP / 16;
-  for (int t = c.wg; t < ntask; t += c.G) {
-    int tile = t, split = 0;
-    if (KIND == K_SPLIT) { tile = t % split_tiles; split = t / split_tiles; }
+  CP& p = c.p;
+  const int RT = c.RT, NRP = p.NRP;
+  const bool ada = d.kind == K_QKV || d.kind == K_GU;
+  const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
+  const uint32_t vlane = (uint32_t)c.lane * 16;
+  float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
+  char* red = c.smem + S::RED;                // [wave][RB + 1][2][64 lanes] x 16 bytes
+  for (int t = c.wg; t < d.ntask; t += c.G) {
+    const int tile = t % d.tiles, split = t / d.tiles;
+    // QKV tasks: kind (q, k, v), head, quarter pair j; v is computed untransposed (D = A W^T) so that each
+    // lane holds 4 consecutive keys of one d: 8 bytes of the V^T layout
+    const int qkind = d.kind == K_QKV ? t / (2 * S::NH) : 0, qhd = (t >> 1) % S::NH, qj = t & 1;
+    const bool vtask = qkind == 2;
     if (t != c.wg) {  // later tasks of this workgroup: load their weights now (the first was prefetched)
+      wait_vm0();
       __syncthreads();
-      const long long woff = KIND == K_SPLIT ? ((long long)tile * S::SK + split) * S::NKB * 512 : (long long)t * wtask_stride;
-      dma_w(c, c.smem + S::WBUF, wbase + woff, NT * S::NKB);
+      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
     }
-    const int k0 = split * S::H;
+    const int kb0 = split * S::NKB;
     for (int rt0 = 0; rt0 < RT; rt0 += RB) {
       const int nrt = min(RB, RT - rt0);
-      const int row0 = rt0 * 16;
-      bf16x8 ahi[RB][KPW], alo[RB][KPW];
-      {
-        float x[RB][KPW][8];
-        // rows beyond the pass are clamped to the pass's last row: every load is unconditional (one batch)
-#pragma unroll
-        for (int rt = 0; rt < RB; ++rt)
-#pragma unroll
-          for (int i = 0; i < KPW; ++i) {
-            const int row = row0 + min(rt, nrt - 1) * 16 + (c.lane & 15);
-            const int col = k0 + (c.wave + NWAVES * i) * 32 + 8 * (c.lane >> 4);
-            load8f(asrc + ((long long)(col >> 4) * NRP + row) * 16 + (col & 15), x[rt][i]);
-          }
-        if (ADARMS) {
-          float* ssq = (float*)(c.smem + S::SMALL);  // [4][RB*16]
-#pragma unroll
-          for (int rt = 0; rt < RB; ++rt) {
-            float ss = 0.f;
-#pragma unroll
-            for (int i = 0; i < KPW; ++i)
-#pragma unroll
-              for (int j = 0; j < 8; ++j) ss += x[rt][i][j] * x[rt][i][j];
-            ss += __shfl_xor(ss, 16);
-            ss += __shfl_xor(ss, 32);
-            if (c.lane < 16) ssq[c.wave * RB * 16 + rt * 16 + c.lane] = ss;
-          }
-          wait_vm0();  // staged weights and modulation slices have landed
-          __syncthreads();
-#pragma unroll
-          for (int rt = 0; rt < RB; ++rt) {
-            const int r = rt * 16 + (c.lane & 15);
-            float tot = 0.f;
-#pragma unroll
-            for (int w = 0; w < NWAVES; ++w) tot += ssq[w * RB * 16 + r];
-            const float rs = rsqrtf(tot / (float)S::H + c.p.eps);
-            const float* ml = mods_lds(c, c.sample_of(row0 + r), 2 * S::H);
-#pragma unroll
-            for (int i = 0; i < KPW; ++i) {
-              const int col = (c.wave + NWAVES * i) * 32 + 8 * (c.lane >> 4);
-              float sc[8], sh[8], v[8];
-              load8f(ml + col, sc);
-              load8f(ml + S::H + col, sh);
-#pragma unroll
-              for (int j = 0; j < 8; ++j) v[j] = x[rt][i][j] * rs * (1.0f + sc[j]) + sh[j];
-              split8(v, ahi[rt][i], alo[rt][i]);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int rt = 0; rt < RB; ++rt)
-#pragma unroll
-            for (int i = 0; i < KPW; ++i) split8(x[rt][i], ahi[rt][i], alo[rt][i]);
-          wait_vm0();
-          __syncthreads();
-        }
-      }
-      f32x4 acc[RB][NT];
+      bf16x8 ah[RB][KPW], al[RB][KPW];
+      // row tiles beyond the pass repeat its last tile: every load is unconditional (one batch)
 #pragma unroll
       for (int rt = 0; rt < RB; ++rt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < KPW; ++i) {
-        const int kb = c.wave + NWAVES * i;
-        bf16x8 w[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) w[nt] = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
-#pragma unroll
-        for (int rt = 0; rt < RB; ++rt)
-          if (rt < nrt) {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              acc[rt][nt] = mfma16(ahi[rt][i], w[nt], acc[rt][nt]);
-              acc[rt][nt] = mfma16(alo[rt][i], w[nt], acc[rt][nt]);
-            }
-          }
-      }
-      // cross-wave reduction through LDS: red[w][rt][nt][16 rows][16 cols]
-      float* red = (float*)(c.smem + S::RED);
-#pragma unroll
-      for (int rt = 0; rt < RB; ++rt)
-        if (rt < nrt) {
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            float* base = red + ((c.wave * RB + rt) * NT + nt) * 256;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) base[(4 * (c.lane >> 4) + i) * 16 + (c.lane & 15)] = acc[rt][nt][i];
-          }
+        for (int i = 0; i < KPW; ++i) {
+          const uint32_t blk = (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + min(rt, nrt - 1)) * 2048);
+          ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
+          al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
         }
+      float ssp = 0.f;
+      if (ada) {  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
+        const int row = min(rt0 * 16 + c.lane, NRP - 1);
+#pragma unroll
+        for (int i = 0; i < S::HT / NWAVES; ++i) ssp += d.ssin[(long long)(c.wave + NWAVES * i) * NRP + row];
+      }
+      wait_vm0();  // activations, and the staged weights and modulation slices, have landed
       __syncthreads();
-      // epilogue: one item = (row, 8 columns) of the task's 16-column tile
-      for (int it = c.tid; it < nrt * 16 * 2; it += NTHREADS) {
-        const int r = it >> 1, half = it & 1;
-        const int grow = row0 + r;
-        const long long ooff = ((long long)tile * NRP + grow) * 16 + half * 8;  // elements
-        float v[8];
-        red_sum8<S, NT>(c, r, 0, half, v);
-        if (KIND == K_GU) {
-          float u[8];
-          red_sum8<S, NT>(c, r, NT - 1, half, u);
+      MKX_TR(c, 1);
+      if (ada) ssw[c.wave * 64 + c.lane] = ssp;
+      f32x4 acc[RB + 1][2];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = act_fn(v[j], c.p.act) * u[j];
-          st8f_sc1(out, ooff, v);
-        } else if (KIND == K_PLAIN) {
-          st8f_sc1(out, ooff, v);
-        } else if (KIND == K_RES) {
-          float rv[8], g[8];
-          load8f(res + ooff, rv);
-          load8f(mods_lds(c, c.sample_of(grow), S::H) + tile * 16 + half * 8, g);
+      for (int rt = 0; rt <= RB; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (vtask) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = rv[j] + v[j] * g[j];
-          st8f_sc1(out, ooff, v);
-        } else {
-          st8f_sc1(part, (((long long)split * split_tiles + tile) * NRP + grow) * 16 + half * 8, v);
+        for (int i = 0; i < KPW; ++i) {
+          const int kb = c.wave + NWAVES * i;
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            const bf16x8 wf = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
+#pragma unroll
+            for (int rt = 0; rt < RB; ++rt) {
+              acc[rt][nt] = mfma16(ah[rt][i], wf, acc[rt][nt]);
+              acc[rt][nt] = mfma16(al[rt][i], wf, acc[rt][nt]);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < KPW; ++i) {
+          const int kb = c.wave + NWAVES * i;
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            if (nt < d.nt) {
+              const bf16x8 wf = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
+#pragma unroll
+              for (int rt = 0; rt < RB; ++rt) {
+                acc[rt][nt] = mfma16(wf, ah[rt][i], acc[rt][nt]);
+                acc[rt][nt] = mfma16(wf, al[rt][i], acc[rt][nt]);
+              }
+            }
+          }
         }
       }
-      __syncthreads();  // red and ssq are reused by the next pass
+      if (ada) {
+        // shift W^T: row tile whose row b is sample b's shift slice (rows >= B are zero)
+        const int b = c.lane & 15;
+        const float* sh = mods_lds(c, min(b, p.B - 1), S::H);
+#pragma unroll
+        for (int i = 0; i < KPW; ++i) {
+          const int kb = c.wave + NWAVES * i;
+          const int col = kb * 32 + 8 * (c.lane >> 4);
+          const f32x4 s0 = ldf4(sh + col), s1 = ldf4(sh + col + 4);
+          const bool okb = b < p.B;
+          float v[8] = {okb ? s0[0] : 0.f, okb ? s0[1] : 0.f, okb ? s0[2] : 0.f, okb ? s0[3] : 0.f,
+                        okb ? s1[0] : 0.f, okb ? s1[1] : 0.f, okb ? s1[2] : 0.f, okb ? s1[3] : 0.f};
+          bf16x8 sh_h, sh_l;
+          split8(v, sh_h, sh_l);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            if (nt < d.nt) {
+              const bf16x8 wf = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
+              acc[RB][nt] = mfma16(wf, sh_h, acc[RB][nt]);
+              acc[RB][nt] = mfma16(wf, sh_l, acc[RB][nt]);
+            }
+          }
+        }
+      }
+      // cross-wave reduction through LDS
+#pragma unroll
+      for (int rt = 0; rt <= RB; ++rt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          if (nt < d.nt && (rt < nrt || (rt == RB && ada)))
+            sts16(red + (((c.wave * (RB + 1) + rt) * 2 + nt) * 64 + c.lane) * 16, as_u4(acc[rt][nt]));
+      __syncthreads();
+      MKX_TR(c, 2);
+      // epilogue: one (row tile, lane) item per thread: row (rt0 + rt) * 16 + L % 16, columns tile*16 + 4 (L / 16) + 0..3
+      {
+        const int rt = c.tid >> 6, L = c.tid & 63;
+        if (rt < nrt) {
+          auto wsum = [&](int r, int nt, int lane) {
+            f32x4 v = ldf4((const float*)(red + ((r * 2 + nt) * 64 + lane) * 16));
+#pragma unroll
+            for (int w = 1; w < NWAVES; ++w) v += ldf4((const float*)(red + (((w * (RB + 1) + r) * 2 + nt) * 64 + lane) * 16));
+            return v;
+          };
+          const int row = (rt0 + rt) * 16 + (L & 15);
+          const int col = tile * 16 + 4 * (L >> 4);
+          f32x4 v = wsum(rt, 0, L);
+          if (vtask) {
+            // lane L: d = 16 j + 32 nt + L % 16, rows (keys) 4 (L / 16) + e of a 16-row tile of one sample
+            const int row0 = (rt0 + rt) * 16, b = c.sample_of(row0);
+            const int ib = row0 - b * p.Mqp + 4 * (L >> 4);
+            const int KBO = ceil_to(p.Mq, 32) / 32;
+            float rs[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = rt * 16 + 4 * (L >> 4) + e;
+              rs[e] = rsqrtf((ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r]) / (float)S::H + p.eps);
+            }
+            const uint32_t vo = (uint32_t)(((b * S::NH + qhd) * KBO + (ib >> 5)) * 8192 + L * 16 + ((ib >> 4) & 1) * 8);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+              const f32x4 a = wsum(rt, nt, L);
+              const int cl = L & 15, bl = b + 16 * (cl >> 2);
+              float bias = 0.f;
+#pragma unroll
+              for (int w = 0; w < NWAVES; ++w) bias += ((const float*)(red + (((w * (RB + 1) + RB) * 2 + nt) * 64 + bl) * 16))[cl & 3];
+              f32x4 x;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[e] = ib + e < p.Mq ? a[e] * rs[e] + bias : 0.f;
+              st_split4(d.part, vo + (uint32_t)((qj + 2 * nt) * 2048), x);
+            }
+          } else if (d.kind == K_SPLIT) {
+            st_sc1(d.part, (uint32_t)((((split * d.tiles + tile) * RT + rt0 + rt) * 64 + L) * 16), as_u4(v));
+          } else if (d.kind == K_RES) {
+            res_piece(c, d, tile, row, col, L, v);
+          } else {
+            const int r = rt * 16 + (L & 15);
+            const float tot = ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r];
+            const float rs = rsqrtf(tot / (float)S::H + p.eps);
+            const int bl = c.sample_of(row) + 16 * (L >> 4);
+            v = v * rs + wsum(RB, 0, bl);
+            const f32x4 u = wsum(rt, 1, L) * rs + wsum(RB, 1, bl);
+            if (d.kind == K_GU) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) v[j] = act_fn(v[j], p.act) * u[j];
+              st_split4(d.out, spiece(row, col, RT), v);
+            } else {
+              qk_piece(c, d, qkind, qhd, qj, row, L, v, u);
+            }
+          }
+        }
+      }
+      __syncthreads();  // red and ssw are reused by the next pass
+      MKX_TR(c, 3);
     }
-    if (KIND == K_SPLIT) {
+    if (d.kind == K_SPLIT) {
       // the last-arriving split task of this tile sums the partials in split order and applies the residual
-      const int SK = ntask / split_tiles;
-      int* flag = (int*)(c.smem + S::SMALL + 3 * 1024);
+      int* flag = (int*)(c.smem + S::SMALL + 3 * 1024 + 512);
       wait_vm0();
       __syncthreads();
       if (c.tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(&c.p.dcnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = (old == (unsigned)(SK - 1));
-        if (last) __hip_atomic_store(&c.p.dcnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(&p.dcnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = (old == (unsigned)(S::SK - 1));
+        if (last) __hip_atomic_store(&p.dcnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *flag = last;
       }
       __syncthreads();
       if (*flag) {
-        for (int it = c.tid; it < NRP * 2; it += NTHREADS) {
-          const int grow = it >> 1, half = it & 1;
-          float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-          u32x4 xp[2 * 8];
+        for (int it = c.tid; it < RT * 64; it += NTHREADS) {
+          const int rtg = it >> 6, L = it & 63;
+          u32x4 xp[S::SK];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {  // up to 8 splits, loads batched
-            if (j < SK) {
-              const long long poff = (((long long)j * split_tiles + tile) * NRP + grow) * 16 + half * 8;
-              xp[2 * j] = ld_sc1(part, (uint32_t)(poff * 4));
-              xp[2 * j + 1] = ld_sc1(part, (uint32_t)(poff * 4 + 16));
-            }
-          }
-          const long long ooff = ((long long)tile * NRP + grow) * 16 + half * 8;
-          float rv[8], g[8];
-          load8f(res + ooff, rv);
-          load8f(mods_lds(c, c.sample_of(grow), S::H) + tile * 16 + half * 8, g);
+          for (int j = 0; j < S::SK; ++j) xp[j] = ld_sc1(d.part, (uint32_t)((((j * d.tiles + tile) * RT + rtg) * 64 + L) * 16));
+          f32x4 v = as_f4(xp[0]);
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            if (j < SK) {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) { v[q] += __uint_as_float(xp[2 * j][q]); v[4 + q] += __uint_as_float(xp[2 * j + 1][q]); }
-            }
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = rv[j] + v[j] * g[j];
-          st8f_sc1(out, ooff, v);
+          for (int j = 1; j < S::SK; ++j) v += as_f4(xp[j]);
+          res_piece(c, d, tile, rtg * 16 + (L & 15), tile * 16 + 4 * (L >> 4), L, v);
         }
+        MKX_TR(c, 7);
       }
     }
   }
 }
 
 // ------------------------------------------------------------------------------------------------
-// Attention. Q/K chunk layout (rows x 64 d) -> chunk (rt, db) 1 KB, lane l = row rt*16 + l%16,
-// d = db*32 + 8(l/16). Vt chunk (kb, dt): lane l holds V[key kb*32 + 8(l/16) + j][d = dt*16 + l%16], j < 8.
+// Attention. One task per (sample, head, 16-query tile); its 4 waves take the 32-key blocks round-robin
+// and merge their online-softmax states through LDS at the end.
+// K chunk (key tile kt, d-block db), 1 KB: lane l holds K[kt*16 + l%16][db*32 + 8(l/16) + j] (the split
+// frame's hi or lo half, so own-row Q/K chunks are DMA'd straight from the projection's output). Vt chunk
+// (32-key block kb, 16-d slice dt), 1 KB: lane l = d%16 + 16 g holds V[kb*32 + key_j][dt*16 + d%16] for
+// key_j = (j/4)*16 + 4g + j%4, j < 8. Scores are computed transposed (S^T = K Q^T), so a lane holds, for
+// its query l%16, exactly the 8 keys its P operand of P V needs in that order: the probabilities never
+// leave registers. The own-row q and k arrive un-normalised (u = rope(x (1 + w))); their RMS factors
+// multiply the scores (src/mk_expert.py:175-222 rearranged: rms(x) is a per-row scalar and RoPE is linear).
 
-__device__ __forceinline__ int qk_chunk_off(int row, int d) {  // byte offset of 8 d-values (d % 8 == 0)
+__device__ __forceinline__ int kchunk_off(int row, int d) {  // byte offset of 8 d-values (d % 8 == 0)
   return ((row >> 4) * 2 + (d >> 5)) * 1024 + ((row & 15) + 16 * ((d & 31) >> 3)) * 16;
 }
 __device__ __forceinline__ int vt_off(int key, int d) {  // byte offset of one bf16
-  return ((key >> 5) * 4 + (d >> 4)) * 1024 + ((d & 15) + 16 * ((key & 31) >> 3)) * 16 + (key & 7) * 2;
+  const int kk = key & 31, g = (kk & 15) >> 2, j = (kk >> 4) * 4 + (kk & 3);
+  return ((key >> 5) * 4 + (d >> 4)) * 1024 + ((d & 15) + 16 * g) * 16 + j * 2;
 }
 
-// q/k head row, 8 lanes per row (lane j of the group holds d = 8j .. 8j+7 of x): RMSNorm with weight 1 + w,
-// then rotate-half RoPE (src/mk_expert.py:175-193), in fp32.
-__device__ __forceinline__ void norm_rope8(float* x, const bf16_t* w, const float* cs, const float* sn, float eps, int j) {
-  float ss = 0.f;
+struct AttnState {
+  f32x4 acc[4];
+  float m, den;
+  bf16x8 qh[2], ql[2];
+};
+
+// One block of 32 keys (K: 4 chunks, Vt: 4 chunks; Kl/Vl: bf16 residual parts or null) for the wave's
+// query tile; keys [klo, khi) of the block are valid (invalid keys hold finite values). Scores are scaled
+// by qs (softmax scale x query RMS factor) and, when rk is set, by the key RMS factors rk[key]. Online
+// fp32 softmax (src/mk_expert.py:196-251).
+__device__ __forceinline__ void attn_block(AttnState& A, int lane, const char* K, const char* Kl, const char* V, const char* Vl,
+                                           int klo, int khi, float qs, const float* rk) {
+  f32x4 s[2];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) ss += x[q] * x[q];
-  ss += __shfl_xor(ss, 1);
-  ss += __shfl_xor(ss, 2);
-  ss += __shfl_xor(ss, 4);
-  const float r = rsqrtf(ss / 64.f + eps);
-  float wv[8], c8[8], s8[8];
-  unpack8(ld16(w + 8 * j), wv);
-  load8f(cs + 8 * j, c8);
-  load8f(sn + 8 * j, s8);
-  float xn[8];
+  for (int h = 0; h < 2; ++h) {
+    s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int q = 0; q < 8; ++q) xn[q] = x[q] * r * (1.0f + wv[q]);
-  const float sgn = j < 4 ? -1.0f : 1.0f;
+    for (int db = 0; db < 2; ++db) {
+      const bf16x8 kf = ldsfrag(K + (h * 2 + db) * 1024 + lane * 16);
+      s[h] = mfma16(kf, A.qh[db], s[h]);
+      s[h] = mfma16(kf, A.ql[db], s[h]);
+      if (Kl) s[h] = mfma16(ldsfrag(Kl + (h * 2 + db) * 1024 + lane * 16), A.qh[db], s[h]);
+    }
+  }
+  float pv[8];
+  float mb = -INFINITY;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const float partner = __shfl_xor(xn[q], 4);  // d +- 32
-    x[q] = xn[q] * c8[q] + sgn * partner * s8[q];
+  for (int j = 0; j < 8; ++j) {
+    const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+    float sc = qs;
+    if (rk) sc *= rk[key];
+    pv[j] = s[j >> 2][j & 3] * sc + ((key >= klo && key < khi) ? 0.f : -INFINITY);
+    mb = fmaxf(mb, pv[j]);
+  }
+  mb = fmaxf(mb, __shfl_xor(mb, 16));
+  mb = fmaxf(mb, __shfl_xor(mb, 32));
+  const float mn = fmaxf(A.m, mb);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float alpha = __expf(A.m - mu);
+  A.m = mn;
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    pv[j] = __expf(pv[j] - mu);
+    ps += pv[j];
+  }
+  A.den = A.den * alpha + ps;
+  bf16x8 ph, pl;
+  split8(pv, ph, pl);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const bf16x8 vf = ldsfrag(V + dt * 1024 + lane * 16);
+    f32x4 a = A.acc[dt] * alpha;
+    a = mfma16(vf, ph, a);
+    a = mfma16(vf, pl, a);
+    if (Vl) a = mfma16(ldsfrag(Vl + dt * 1024 + lane * 16), ph, a);
+    A.acc[dt] = a;
   }
 }
 
-// 8 fp32 values of row `grow`, columns [col, col+8) of a tile-major fp32 buffer
-template <class S>
-__device__ __forceinline__ void load_frag8(Ctx<S>& c, const float* buf, int grow, int col, float* x) {
-  load8f(buf + ((long long)(col >> 4) * c.p.NRP + grow) * 16 + (col & 15), x);
+__device__ __forceinline__ void attn_begin(AttnState& A, const char* Qh, const char* Ql, int lane) {
+#pragma unroll
+  for (int db = 0; db < 2; ++db) {
+    A.qh[db] = ldsfrag(Qh + db * 1024 + lane * 16);
+    A.ql[db] = ldsfrag(Ql + db * 1024 + lane * 16);
+  }
+  A.m = -INFINITY;
+  A.den = 0.f;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) A.acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
+// merges the 4 waves' states (mrg: 18 KB of LDS) and stores the tile's output rows of head hd of sample b
+// (split, written through; query rows >= M get zeros). Wave w finishes the 16-d slice dt = w.
 template <class S>
-__device__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd) {
+__device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float* mrg, float* y, int b, int hd, int qt) {
+  float* me = mrg + (c.wave * 64 + c.lane) * 18;
+  me[0] = A.m;
+  me[1] = A.den;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4*>(me + 2 + 4 * dt) = A.acc[dt];
+  __syncthreads();
+  float mw[NWAVES], M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NWAVES; ++w) {
+    mw[w] = mrg[(w * 64 + c.lane) * 18];
+    M = fmaxf(M, mw[w]);
+  }
+  float den = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < NWAVES; ++w) {
+    const float* o = mrg + (w * 64 + c.lane) * 18;
+    const float f = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - M);
+    den += o[1] * f;
+    acc += ldf4(o + 2 + 4 * c.wave) * f;
+  }
+  den += __shfl_xor(den, 16);
+  den += __shfl_xor(den, 32);
+  const int q = qt * 16 + (c.lane & 15);
+  const f32x4 out = (den > 0.f && q < c.p.Mq) ? acc * (1.0f / den) : f32x4{0.f, 0.f, 0.f, 0.f};
+  st_split4(y, spiece(b * c.p.Mqp + q, hd * HD + c.wave * 16 + 4 * (c.lane >> 4), c.RT), out);
+}
+
+// Attention tasks: virtual workgroup v -> (sample-head hh, query tile qt), arranged so that the query
+// tiles of one head run on workgroups of one XCD (v % 8 is the XCD class) and share its L2.
+struct AttnTask {
+  int hh, qt;
+  bool ok;
+};
+__device__ __forceinline__ AttnTask attn_task(int v, int nqt, int nhb) {
+  AttnTask a;
+  const int k = v >> 3;
+  a.qt = k % nqt;
+  a.hh = (v & 7) + 8 * (k / nqt);
+  a.ok = a.hh < nhb;
+  return a;
+}
+__device__ __forceinline__ int attn_vcount(int nqt, int nhb) { return 8 * nqt * ((nhb + 7) / 8); }
+
+template <class S>
+__device__ __forceinline__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd, int kvs) {
   const int PM = c.p.PM, PMP = ceil_to(PM, 32);
   char* memK = c.smem + S::WBUF;
-  char* memV = memK + PMP * 128;
+  char* memVt = memK + PMP * 128;
   const bf16_t* mk = c.p.memk[l] + (long long)b * c.p.mem_sb;
-  const bf16_t* mv = c.p.memv[l] + (long long)b * c.p.mem_sb;
+  const bf16_t* mvt = c.p.memvt + ((long long)(l * c.p.B + b) * S::NH + hd) * PMP * 64;
   const int nk = (PMP / 16) * 2, nv = PMP / 8;
   for (int k = c.wave; k < nk + nv; k += NWAVES) {
     if (k < nk) {
+      // rows outside [kv_start, PM) are replaced by valid rows (they are masked): every operand is finite
       const int kt = k >> 1, db = k & 1;
-      const int key = min(kt * 16 + (c.lane & 15), PM - 1);
+      const int key = min(max(kt * 16 + (c.lane & 15), kvs), PM - 1);
       dma16(mk + ((long long)key * S::NH + hd) * HD + db * 32 + 8 * (c.lane >> 4), memK + k * 1024);
     } else {
       const int i = k - nk;
-      const int key = min(i * 8 + (c.lane >> 3), PM - 1);
-      dma16(mv + ((long long)key * S::NH + hd) * HD + (c.lane & 7) * 8, memV + i * 1024);
+      dma16(mvt + (long long)i * 512 + c.lane * 8, memVt + i * 1024);
     }
   }
 }
 
-// In-place transpose of nkeys raw V rows (key-major [key][64] bf16) into Vt chunks at the same address.
-// Keys outside [lo, hi) become zero. nkeys <= 256 (8 pieces of 16 bytes per thread).
-__device__ __forceinline__ void transpose_v_inplace(char* buf, int nkeys, int lo, int hi, int tid) {
-  u32x4 v[8];
+// Per-launch V^T copies of the memory and cross-attention V caches (the caches are constant over the
+// Euler loop). Task (l, b, head, 32-key block): rows outside the valid range are replaced by valid rows.
+template <class S>
+__device__ __forceinline__ void transpose_caches(Ctx<S>& c, const int* s_ks) {
+  CP& p = c.p;
+  const int PMP = ceil_to(p.PM, 32), nmb = PMP / 32, ncb = p.SPP / 32;
+  const int nm = p.L * p.B * S::NH * nmb, ntot = nm + p.L * p.B * S::NH * ncb;
+  char* raw = c.smem + S::ABUF;  // [4 tasks][32 keys][64 d] bf16
+  for (int t0 = c.wg * 4; t0 < ntot; t0 += c.G * 4) {
+    __syncthreads();
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int it = tid + u * NTHREADS;
-    if (it < nkeys * 8) v[u] = lds16(buf + it * 16);
-  }
-  __syncthreads();
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u;
+      if (t < ntot) {
+        const bool mem = t < nm;
+        const int tt = mem ? t : t - nm, nb = mem ? nmb : ncb;
+        const int kb = tt % nb, lbh = tt / nb, hd = lbh % S::NH, lb = lbh / S::NH, b = lb % p.B, l = lb / p.B;
+        const int r = kb * 32 + (c.tid >> 3);
+        int key;
+        const bf16_t* src;
+        if (mem) {
+          key = min(max(r, s_ks[b]), p.PM - 1);
+          src = p.memv[l] + (long long)b * p.mem_sb;
+        } else {
+          key = max(min(r, s_ks[MAX_BATCH + b] - 1), 0);
+          src = p.vca[l] + (long long)b * p.src_sb;
+        }
+        *reinterpret_cast<u32x4*>(raw + u * 4096 + c.tid * 16) = ld16(src + ((long long)key * S::NH + hd) * HD + (c.tid & 7) * 8);
+      }
+    }
+    __syncthreads();
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int it = tid + u * NTHREADS;
-    if (it < nkeys * 8) {
-      const int key = it >> 3, dg = (it & 7) * 8;
-      const bool ok = key >= lo && key < hi;
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u;
+      if (t < ntot) {
+        const bool mem = t < nm;
+        const int tt = mem ? t : t - nm;
+        bf16_t* dst = (mem ? p.memvt : p.cavt) + (long long)tt * 2048;  // (l, b, head, block) blocks of 4 KB
+        const int dt = c.tid >> 6, ln = c.tid & 63, dd = dt * 16 + (ln & 15), g = ln >> 4;
+        u32x4 v;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t w = ok ? v[u][q] : 0u;
-        *reinterpret_cast<bf16_t*>(buf + vt_off(key, dg + 2 * q)) = (bf16_t)(w & 0xffffu);
-        *reinterpret_cast<bf16_t*>(buf + vt_off(key, dg + 2 * q + 1)) = (bf16_t)(w >> 16);
+        for (int q = 0; q < 4; ++q) {
+          const int k0 = ((2 * q) >> 2) * 16 + 4 * g + ((2 * q) & 3), k1 = ((2 * q + 1) >> 2) * 16 + 4 * g + ((2 * q + 1) & 3);
+          const uint32_t lo = *reinterpret_cast<const bf16_t*>(raw + u * 4096 + k0 * 128 + dd * 2);
+          const uint32_t hi = *reinterpret_cast<const bf16_t*>(raw + u * 4096 + k1 * 128 + dd * 2);
+          v[q] = lo | (hi << 16);
+        }
+        st_sc1(dst, (uint32_t)((dt * 64 + ln) * 16), v);
       }
     }
   }
 }
 
-// Self-attention of one (sample, head): queries = own rows; keys = memory rows [kv_start, PM) (bf16 cache,
-// pre-normed and rotated) || own rows (normed and rotated here). Two-pass fp32 softmax
-// (src/mk_expert.py:196-222). The own-row Q, K and V are split into bf16 hi + lo.
+// Self-attention stage: task (sample b, head hd, query tile qt). Queries = the tile's own rows; keys =
+// memory rows [kv_start, PM) (bf16 cache, pre-normed and rotated, DMA'd during the barrier) || the
+// sample's own rows (split q/k/v written by the QKV stage).
 template <class S>
-__device__ void sa_task(Ctx<S>& c, int s, int l, int b, int hd, const float* qkv, float* y, int kvs) {
+__device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
-  const int M = p.Mq, PM = p.PM, PMP = ceil_to(PM, 32), NOWN = ceil_to(M, 16), NOWN32 = ceil_to(M, 32);
+  const int M = p.Mq, Mqp = p.Mqp, PM = p.PM, PMP = ceil_to(PM, 32), NOWN32 = ceil_to(M, 32);
+  const int NQT = Mqp / 16, NKT = NOWN32 / 16, KBO = NOWN32 / 32, NRP = p.NRP, RT = c.RT;
+  const int l = d.l;
+  char* fr = c.frame(d.s, l);
+  const char* qs = fr + S::qs_off(NRP);
+  const char* ks = fr + S::ks_off(NRP);
+  const char* vt = fr + S::vtb_off(NRP);
+  const float* ssqk = (const float*)(fr + S::ssqk_off(NRP));
+  float* ysa = (float*)(fr + S::ysa_off(NRP));
   char* memK = c.smem + S::WBUF;
   char* memVt = memK + PMP * 128;
-  char* Qhi = c.smem + S::ABUF;
-  char* Qlo = Qhi + NOWN * 128;
-  char* Khi = Qlo + NOWN * 128;
-  char* Klo = Khi + NOWN * 128;
-  char* Vhi = Klo + NOWN * 128;
-  char* Vlo = Vhi + NOWN32 * 128;
-  char* Pst = Vlo + NOWN32 * 128 + c.wave * 1024;
-  const bool want_kv = (s == 0 && p.cur_k != nullptr && p.R > 0);
-  // memory V rows -> Vt (rows below kv_start and beyond PM are zero)
-  transpose_v_inplace(memVt, PMP, kvs, PM, c.tid);
-  // own rows: 8 lanes per (kind, row); kind 0 = q, 1 = k, 2 = v
-  const int j = c.tid & 7;
-  for (int g0 = 0; g0 < 3 * NOWN32; g0 += NTHREADS / 8) {
-    const int g = g0 + (c.tid >> 3);
-    if (g < 3 * NOWN32) {
-      const int kind = g / NOWN32, i = g % NOWN32;
-      const bool valid = i < M;
-      const int grow = b * p.Mqp + min(i, M - 1);
-      float x[8];
-      load_frag8(c, qkv, grow, kind * S::H + hd * HD + 8 * j, x);
-      if (kind < 2) {
-        norm_rope8(x, (kind == 0 ? p.qn : p.kn) + l * HD, p.sa_cos + min(i, M - 1) * HD, p.sa_sin + min(i, M - 1) * HD, p.qk_eps, j);
-        if (i < NOWN) {
-          bf16x8 hi, lo;
-          split8(x, hi, lo);
-          char* dh = kind == 0 ? Qhi : Khi;
-          char* dl = kind == 0 ? Qlo : Klo;
-          *reinterpret_cast<bf16x8*>(dh + qk_chunk_off(i, 8 * j)) = hi;
-          *reinterpret_cast<bf16x8*>(dl + qk_chunk_off(i, 8 * j)) = lo;
-        }
-        if (kind == 1 && want_kv && valid && i >= p.T) {
-          bf16_t* o = p.cur_k + ((((long long)l * p.B + b) * p.R + (i - p.T)) * S::NH + hd) * HD + 8 * j;
-          *reinterpret_cast<u32x4*>(o) = pack8(x);
-        }
+  char* Qh = c.smem + S::ABUF;
+  char* Ql = Qh + 2048;
+  char* Kh = Ql + 2048;
+  char* Kl = Kh + NOWN32 * 128;
+  char* Vh = Kl + NOWN32 * 128;
+  char* Vl = Vh + NOWN32 * 128;
+  float* rk = (float*)(Vl + NOWN32 * 128);
+  float* mrg = rk + 128;
+  const int NHB = p.B * S::NH;
+  const bool want_kv = (d.s == 0 && p.cur_k != nullptr && p.R > 0);
+  for (int v = c.wg; v < attn_vcount(NQT, NHB); v += c.G) {
+    const AttnTask at = attn_task(v, NQT, NHB);
+    if (!at.ok) continue;
+    const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
+    const int kvs = s_ks[b];
+    if (v != c.wg) {
+      wait_vm0();
+      __syncthreads();
+      sa_prefetch(c, l, b, hd, kvs);
+    }
+    // own-row operands: Q tile (hi, lo), K tiles of all own keys, V^T blocks (all DMA, one batch)
+    const int rt0 = b * Mqp / 16;
+    for (int k = c.wave; k < 4 + 4 * NKT + 8 * KBO; k += NWAVES) {
+      if (k < 4) {
+        const int db = k >> 1, part = k & 1;
+        dma16(qs + ((long long)((2 * hd + db) * RT + rt0 + qt) * 2 + part) * 1024 + c.lane * 16, (part ? Ql : Qh) + db * 1024);
+      } else if (k < 4 + 4 * NKT) {
+        const int kk = k - 4, kt = kk >> 2, db = (kk >> 1) & 1, part = kk & 1;
+        const int rtk = rt0 + min(kt, NQT - 1);
+        dma16(ks + ((long long)((2 * hd + db) * RT + rtk) * 2 + part) * 1024 + c.lane * 16, (part ? Kl : Kh) + (kt * 2 + db) * 1024);
       } else {
-        if (want_kv && valid && i >= p.T) {
-          bf16_t* o = p.cur_v + ((((long long)l * p.B + b) * p.R + (i - p.T)) * S::NH + hd) * HD + 8 * j;
-          *reinterpret_cast<u32x4*>(o) = pack8(x);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float v = valid ? x[q] : 0.f;
-          const float vh = rbf(v);
-          *reinterpret_cast<bf16_t*>(Vhi + vt_off(i, 8 * j + q)) = f2bf(vh);
-          *reinterpret_cast<bf16_t*>(Vlo + vt_off(i, 8 * j + q)) = f2bf(v - vh);
-        }
+        const int vv = k - 4 - 4 * NKT;
+        dma16(vt + ((long long)at.hh * KBO * 8 + vv) * 1024 + c.lane * 16, ((vv & 1) ? Vl : Vh) + (vv >> 1) * 1024);
       }
     }
-  }
-  __syncthreads();
-  const float scale = p.sm_scale;
-  const int mt = PMP / 16, nkt = mt + NOWN / 16, mb = PMP / 32, nkb = mb + NOWN32 / 32;
-  for (int qt = c.wave; qt < NOWN / 16; qt += NWAVES) {
-    bf16x8 qh[2], ql[2];
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      qh[db] = ldsfrag(Qhi + (qt * 2 + db) * 1024 + c.lane * 16);
-      ql[db] = ldsfrag(Qlo + (qt * 2 + db) * 1024 + c.lane * 16);
+    // RMS factors: query row of this lane, and (threads < NOWN32) own keys
+    const int q = qt * 16 + (c.lane & 15);
+    const float ssq = ssqk[(long long)(hd * 2) * NRP + b * Mqp + q] + ssqk[(long long)(hd * 2 + 1) * NRP + b * Mqp + q];
+    float ssk = 0.f;
+    if (c.tid < NOWN32) {
+      const int rowk = b * Mqp + min(c.tid, Mqp - 1);
+      ssk = ssqk[(long long)((S::NH + hd) * 2) * NRP + rowk] + ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + rowk];
     }
-    f32x4 sreg[S::MAXKT];
-    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-    for (int kt = 0; kt < S::MAXKT; ++kt) {
-      if (kt < nkt) {
-        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-        if (kt < mt) {
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const bf16x8 kf = ldsfrag(memK + (kt * 2 + db) * 1024 + c.lane * 16);
-            sc = mfma16(qh[db], kf, sc);
-            sc = mfma16(ql[db], kf, sc);
-          }
-        } else {
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const int off = ((kt - mt) * 2 + db) * 1024 + c.lane * 16;
-            const bf16x8 kh = ldsfrag(Khi + off), kl = ldsfrag(Klo + off);
-            sc = mfma16(qh[db], kh, sc);
-            sc = mfma16(ql[db], kh, sc);
-            sc = mfma16(qh[db], kl, sc);
-          }
-        }
-        const int key = kt * 16 + (c.lane & 15);
-        const bool valid = kt < mt ? (key >= kvs && key < PM) : (key - PMP < M);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[i] = valid ? sc[i] * scale : -INFINITY;
-          mx[i] = fmaxf(mx[i], sc[i]);
-        }
-        sreg[kt] = sc;
+    wait_vm0();  // memory K/V (prefetched) and the own-row operands have landed
+    __syncthreads();
+    if (c.tid < NOWN32) rk[c.tid] = rsqrtf(ssk / 64.f + p.qk_eps);
+    // own keys beyond the sample's rows have no producer: zero their V
+    for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
+      const int key = Mqp + it / HD, dd = it % HD;
+      *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
+      *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
+    }
+    __syncthreads();
+    MKX_TR(c, 1);
+    AttnState A;
+    attn_begin(A, Qh, Ql, c.lane);
+    const float qsc = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
+    const int mb0 = kvs >> 5, nmb = PMP / 32 - mb0;
+    for (int beta = c.wave; beta < nmb + KBO; beta += NWAVES) {
+      if (beta < nmb) {
+        const int kb = mb0 + beta;
+        attn_block(A, c.lane, memK + kb * 4096, nullptr, memVt + kb * 4096, nullptr, kvs - kb * 32, PM - kb * 32, qsc, nullptr);
+      } else {
+        const int kb = beta - nmb;
+        attn_block(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
       }
     }
+    MKX_TR(c, 2);
+    attn_merge_store(c, A, mrg, ysa, b, hd, qt);
+    if (want_kv && qt == 0) {
+      // register rows' k (normed, rotated) and v of step 1, bf16 [L][B][R][NH][64] (src/mk_expert.py:440-470)
+      for (int it = c.tid; it < p.R * 8; it += NTHREADS) {
+        const int i = p.T + it / 8, dd = (it % 8) * 8;
+        bf16x8 kh = ldsfrag(Kh + kchunk_off(i, dd)), kl = ldsfrag(Kl + kchunk_off(i, dd));
+        const u32x4 khu = __builtin_bit_cast(u32x4, kh), klu = __builtin_bit_cast(u32x4, kl);
+        float kf[8], kr[8], vf[8];
+        unpack8(khu, kf);
+        unpack8(klu, kr);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o));
-    float den[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kt = 0; kt < S::MAXKT; ++kt)
-      if (kt < nkt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __expf(sreg[kt][i] - mx[i]);
-          sreg[kt][i] = e;
-          den[i] += e;
+        for (int e = 0; e < 8; ++e) {
+          kf[e] = (kf[e] + kr[e]) * rk[i];
+          vf[e] = bf2f(*reinterpret_cast<const bf16_t*>(Vh + vt_off(i, dd + e))) +
+                  bf2f(*reinterpret_cast<const bf16_t*>(Vl + vt_off(i, dd + e)));
         }
-      }
+        const long long o = ((((long long)l * p.B + b) * p.R + (i - p.T)) * S::NH + hd) * HD + dd;
+        u32x4 wk, wv;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) den[i] += __shfl_xor(den[i], o);
-    f32x4 acc[4];
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < S::MAXKT / 2; ++kb) {
-      if (kb < nkb) {
-        // P (fp32) of key tiles 2kb, 2kb+1 -> bf16 hi then lo, through the wave's 1 KB staging tile
-        bf16x8 pf[2];
-#pragma unroll
-        for (int part = 0; part < 2; ++part) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int kt = 2 * kb + h;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float pv = kt < nkt ? sreg[kt][i] : 0.f;
-              const float ph = rbf(pv);
-              *reinterpret_cast<bf16_t*>(Pst + (4 * (c.lane >> 4) + i) * 64 + (h * 16 + (c.lane & 15)) * 2) =
-                  f2bf(part == 0 ? ph : pv - ph);
-            }
-          }
-          pf[part] = ldsfrag(Pst + (c.lane & 15) * 64 + (c.lane >> 4) * 16);
+        for (int e = 0; e < 4; ++e) {
+          wk[e] = cvt_pk(kf[2 * e], kf[2 * e + 1]);
+          wv[e] = cvt_pk(vf[2 * e], vf[2 * e + 1]);
         }
-        if (kb < mb) {
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const bf16x8 vf = ldsfrag(memVt + (kb * 4 + dt) * 1024 + c.lane * 16);
-            acc[dt] = mfma16(pf[0], vf, acc[dt]);
-            acc[dt] = mfma16(pf[1], vf, acc[dt]);
-          }
-        } else {
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const int off = ((kb - mb) * 4 + dt) * 1024 + c.lane * 16;
-            const bf16x8 vh = ldsfrag(Vhi + off), vl = ldsfrag(Vlo + off);
-            acc[dt] = mfma16(pf[0], vh, acc[dt]);
-            acc[dt] = mfma16(pf[1], vh, acc[dt]);
-            acc[dt] = mfma16(pf[0], vl, acc[dt]);
-          }
-        }
+        *reinterpret_cast<u32x4*>(p.cur_k + o) = wk;
+        *reinterpret_cast<u32x4*>(p.cur_v + o) = wv;
       }
     }
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = qt * 16 + 4 * (c.lane >> 4) + i;
-        if (q < M) {
-          const long long off = ((long long)(hd * 4 + dt) * p.NRP + b * p.Mqp + q) * 16 + (c.lane & 15);
-          st_sc1_b32(y, (uint32_t)(off * 4), __float_as_uint(acc[dt][i] / den[i]));
-        }
-      }
+    __syncthreads();
   }
 }
 
-// Cross-attention: K/V streamed in blocks of 64 source rows through a 4-slot LDS ring (16 KB per slot:
-// K chunks, then raw V rows transposed in place), online fp32 softmax (src/mk_expert.py:225-251).
+// Cross-attention: K and V^T of the source rows streamed in chunks of 128 rows through a 4-slot LDS ring
+// (32 KB per slot: 16 K chunks, then 16 V^T chunks from the per-launch copy); the first four chunks are
+// DMA'd during the barrier. Wave w takes the chunk's 32-row block w (src/mk_expert.py:225-251). The query
+// rows arrive split and un-normalised from the query projection.
 template <class S>
-__device__ void ca_dma_block(Ctx<S>& c, int l, int b, int hd, int jb) {
-  const int SP = c.p.SP;
-  char* slot = c.smem + S::WBUF + (jb & 3) * 16384;
+__device__ __forceinline__ char* ca_slot(Ctx<S>& c, int cc) {
+  const int sl = cc & 3;
+  return c.smem + (sl < 2 ? S::WBUF + sl * 32768 : S::ABUF + (sl - 2) * 32768);
+}
+
+template <class S>
+__device__ __forceinline__ void ca_dma_chunk(Ctx<S>& c, int l, int b, int hd, int cc, int S_len) {
+  char* slot = ca_slot(c, cc);
   const bf16_t* kb_ = c.p.kca[l] + (long long)b * c.p.src_sb;
-  const bf16_t* vb_ = c.p.vca[l] + (long long)b * c.p.src_sb;
-  for (int k = c.wave; k < 16; k += NWAVES) {
-    if (k < 8) {
+  const int ncb = c.p.SPP / 32;
+  const bf16_t* vt = c.p.cavt + ((long long)(l * c.p.B + b) * S::NH + hd) * ncb * 2048;
+  for (int k = c.wave; k < 32; k += NWAVES) {
+    if (k < 16) {
+      // rows beyond the valid length are replaced by the last valid row (they are masked)
       const int kt = k >> 1, db = k & 1;
-      const int key = min(jb * 64 + kt * 16 + (c.lane & 15), SP - 1);
+      const int key = min(cc * 128 + kt * 16 + (c.lane & 15), S_len - 1);
       dma16(kb_ + ((long long)key * S::NH + hd) * HD + db * 32 + 8 * (c.lane >> 4), slot + k * 1024);
     } else {
-      const int i = k - 8;
-      const int key = min(jb * 64 + i * 8 + (c.lane >> 3), SP - 1);
-      dma16(vb_ + ((long long)key * S::NH + hd) * HD + (c.lane & 7) * 8, slot + 8192 + i * 1024);
+      const int i = k - 16, kb = min(cc * 4 + (i >> 2), ncb - 1);
+      dma16(vt + ((long long)kb * 4 + (i & 3)) * 512 + c.lane * 8, slot + 16384 + i * 1024);
     }
   }
 }
 
 template <class S>
-__device__ void ca_prefetch(Ctx<S>& c, int l, int b, int hd, int S_len) {
-  const int nblk = (S_len + 63) / 64;
-  for (int jb = 0; jb < min(nblk, 4); ++jb) ca_dma_block(c, l, b, hd, jb);
+__device__ __forceinline__ void ca_prefetch(Ctx<S>& c, int l, int b, int hd, int S_len) {
+  const int nch = (S_len + 127) / 128;
+  for (int cc = 0; cc < min(nch, 4); ++cc) ca_dma_chunk(c, l, b, hd, cc, S_len);
 }
 
-__device__ __forceinline__ void wait_vm_blocks(int younger) {
-  // each ring block is 4 DMA instructions per wave
-  switch (younger) {
+// waits until at most n ring chunks (8 DMA instructions per wave each) are outstanding
+__device__ __forceinline__ void wait_vm_chunks(int n) {
+  switch (n) {
     case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
   }
 }
 
 template <class S>
-__device__ void ca_task(Ctx<S>& c, int s, int l, int b, int hd, const float* qca, float* y, int S_len) {
+__device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
-  const int M = p.Mq, NOWN = ceil_to(M, 16);
-  char* Qhi = c.smem + S::ABUF;
-  char* Qlo = Qhi + NOWN * 128;
-  char* Pst = Qlo + NOWN * 128 + c.wave * 1024;
-  const int j = c.tid & 7;
-  for (int g0 = 0; g0 < NOWN; g0 += NTHREADS / 8) {
-    const int i = g0 + (c.tid >> 3);
-    if (i < NOWN) {
-      const int ic = min(i, M - 1);
-      float x[8];
-      load_frag8(c, qca, b * p.Mqp + ic, hd * HD + 8 * j, x);
-      norm_rope8(x, p.qcan + l * HD, p.ca_cos + ic * HD, p.ca_sin + ic * HD, p.qk_eps, j);
-      bf16x8 hi, lo;
-      split8(x, hi, lo);
-      *reinterpret_cast<bf16x8*>(Qhi + qk_chunk_off(i, 8 * j)) = hi;
-      *reinterpret_cast<bf16x8*>(Qlo + qk_chunk_off(i, 8 * j)) = lo;
+  const int Mqp = p.Mqp, NQT = Mqp / 16, NRP = p.NRP, RT = c.RT;
+  const int l = d.l;
+  char* fr = c.frame(d.s, l);
+  const char* qcas = fr + S::qcas_off(NRP);
+  const float* ssca = (const float*)(fr + S::ssca_off(NRP));
+  float* yca = (float*)(fr + S::yca_off(NRP));
+  char* Qh = c.smem + S::ABUF + 65536;
+  char* Ql = Qh + 2048;
+  float* mrg = (float*)(Ql + 2048);
+  const int NHB = p.B * S::NH;
+  for (int v = c.wg; v < attn_vcount(NQT, NHB); v += c.G) {
+    const AttnTask at = attn_task(v, NQT, NHB);
+    if (!at.ok) continue;
+    const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
+    const int S_len = s_ks[MAX_BATCH + b];
+    const int nch = (S_len + 127) / 128;
+    if (v != c.wg) {
+      wait_vm0();
+      __syncthreads();
+      ca_prefetch(c, l, b, hd, S_len);
     }
+    const int rt0 = b * Mqp / 16;
+    if (c.wave == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int db = k >> 1, part = k & 1;
+        dma16(qcas + ((long long)((2 * hd + db) * RT + rt0 + qt) * 2 + part) * 1024 + c.lane * 16, (part ? Ql : Qh) + db * 1024);
+      }
+    }
+    const int q = qt * 16 + (c.lane & 15);
+    const float ssq = ssca[(long long)(hd * 2) * NRP + b * Mqp + q] + ssca[(long long)(hd * 2 + 1) * NRP + b * Mqp + q];
+    wait_vm0();  // the prefetched chunks and the query tile have landed
+    __syncthreads();
+    MKX_TR(c, 1);
+    AttnState A;
+    attn_begin(A, Qh, Ql, c.lane);
+    const float qsc = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
+    for (int cc = 0; cc < nch; ++cc) {
+      if (cc >= 4) {
+        wait_vm_chunks(min(nch - 1 - cc, 3));
+        __syncthreads();
+      }
+      char* slot = ca_slot(c, cc);
+      const int k0 = cc * 128 + c.wave * 32;
+      if (k0 < S_len)
+        attn_block(A, c.lane, slot + c.wave * 4096, nullptr, slot + 16384 + c.wave * 4096, nullptr, 0, S_len - k0, qsc, nullptr);
+      if (cc + 4 < nch) {
+        __syncthreads();
+        ca_dma_chunk(c, l, b, hd, cc + 4, S_len);
+      }
+    }
+    MKX_TR(c, 2);
+    attn_merge_store(c, A, mrg, yca, b, hd, qt);
+    __syncthreads();
   }
-  const int nblk = (S_len + 63) / 64;
-  constexpr int MAXQT = 2;  // query tiles per wave (M_q <= 128)
-  float mrun[MAXQT][4], den[MAXQT][4];
-  f32x4 acc[MAXQT][4];
-#pragma unroll
-  for (int u = 0; u < MAXQT; ++u)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { mrun[u][i] = -INFINITY; den[u][i] = 0.f; acc[u][i] = f32x4{0.f, 0.f, 0.f, 0.f}; }
-  const float scale = p.sm_scale;
-  for (int jb = 0; jb < nblk; ++jb) {
-    wait_vm_blocks(min(nblk, jb + 4) - jb - 1);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Step tail (src/mk_expert.py:254-299): o = AdaRMS_final(h_L); v = o Wout^T + bout; x' = x + dt v;
+// h0' = x'_real Win + bin (action rows), register tokens (register rows), all fp32; with h0' its layer-0
+// AdaRMS operand y0' = h0' (1 + scale) (split) and sums of squares. Tasks [0, H/16):
+// in-projection tiles (each recomputes the velocity of the real action dims); tasks [H/16, H/16 + A):
+// one output dim each. One wave per action row; lane owns the 4-column pieces 4 (lane + 64 q).
+// The final modulation rows and Wout's real-dim rows were staged in LDS by the prefetch.
+template <class S>
+__device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
+  CP& p = c.p;
+  constexpr int NP = S::H / 256;  // pieces per lane
+  const int nin = d.last ? 0 : S::HT;
+  const int nout = d.first ? 0 : p.A;
+  const int nrows = p.B * p.T;
+  const int adim = p.action_dim;
+  const float* xcur = (d.first || d.s == 0) ? p.x_in : c.xstep(d.s);
+  const float* hL = d.first ? p.x_in : (const float*)(c.frame(d.s, p.L - 1) + S::hl_off(p.NRP));
+  float* xp = (float*)(c.smem + S::ABUF);           // [nrows][adim] x' of the real dims
+  const float* wo_l = (const float*)(c.smem + S::WBUF);  // Wout rows [adim][H]
+  float* win_t = (float*)(c.smem + S::SMALL);        // Win tile [adim][16]
+  for (int t = c.wg; t < nin + nout; t += c.G) {
     __syncthreads();
-    char* slot = c.smem + S::WBUF + (jb & 3) * 16384;
-    transpose_v_inplace(slot + 8192, 64, 0, S_len - jb * 64, c.tid);
-    __syncthreads();
+    const bool inproj = t < nin;
+    const int a_out = t - nin;
+    if (!d.first) {
+      f32x4 wa[NP];
+      if (!inproj) {
 #pragma unroll
-    for (int u = 0; u < MAXQT; ++u) {
-      const int qt = c.wave + NWAVES * u;
-      if (qt < NOWN / 16) {
-        bf16x8 qh[2], ql[2];
+        for (int q = 0; q < NP; ++q) wa[q] = ldf4(p.wout + (long long)a_out * S::H + 4 * (c.lane + 64 * q));
+      }
+      const __amdgpu_buffer_rsrc_t rh = rsrc(hL);
+      for (int ri = c.wave; ri < nrows; ri += NWAVES) {
+        const int b = ri / p.T, i = ri - b * p.T;
+        const int grow = b * p.Mqp + i;
+        f32x4 x[NP];
 #pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          qh[db] = ldsfrag(Qhi + (qt * 2 + db) * 1024 + c.lane * 16);
-          ql[db] = ldsfrag(Qlo + (qt * 2 + db) * 1024 + c.lane * 16);
+        for (int q = 0; q < NP; ++q) x[q] = as_f4(bload(rh, fpiece(grow, 4 * (c.lane + 64 * q), c.RT), 0));
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < NP; ++q) ss += x[q][0] * x[q][0] + x[q][1] * x[q][1] + x[q][2] * x[q][2] + x[q][3] * x[q][3];
+        const float rs = rsqrtf(wave_sum(ss) / (float)S::H + p.eps);
+        const float* ml = mods_lds(c, b, 2 * S::H);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          const int col = 4 * (c.lane + 64 * q);
+          x[q] = x[q] * rs * (1.0f + ldf4(ml + col)) + ldf4(ml + S::H + col);
         }
-        f32x4 sb[4];
-        float mb[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (inproj) {
+          for (int a = 0; a < adim; ++a) {
+            float dd = 0.f;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const bf16x8 kf = ldsfrag(slot + (kt * 2 + db) * 1024 + c.lane * 16);
-            sc = mfma16(qh[db], kf, sc);
-            sc = mfma16(ql[db], kf, sc);
+            for (int q = 0; q < NP; ++q) {
+              const f32x4 w = ldf4(wo_l + a * S::H + 4 * (c.lane + 64 * q));
+              dd += x[q][0] * w[0] + x[q][1] * w[1] + x[q][2] * w[2] + x[q][3] * w[3];
+            }
+            dd = wave_sum(dd);
+            if (c.lane == 0) xp[ri * adim + a] = xcur[(long long)ri * p.A + a] + c.dt * (dd + p.bout[a]);
           }
-          const bool valid = jb * 64 + kt * 16 + (c.lane & 15) < S_len;
+        } else {
+          float dd = 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            sc[i] = valid ? sc[i] * scale : -INFINITY;
-            mb[i] = fmaxf(mb[i], sc[i]);
-          }
-          sb[kt] = sc;
-        }
-        float alpha[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) mb[i] = fmaxf(mb[i], __shfl_xor(mb[i], o));
-          const float mn = fmaxf(mrun[u][i], mb[i]);
-          alpha[i] = __expf(mrun[u][i] - mn);
-          mrun[u][i] = mn;
-        }
-        float ps[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __expf(sb[kt][i] - mrun[u][i]);
-            sb[kt][i] = e;
-            ps[i] += e;
-          }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) ps[i] += __shfl_xor(ps[i], o);
-          den[u][i] = den[u][i] * alpha[i] + ps[i];
-        }
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[u][dt][i] *= alpha[i];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          bf16x8 pf[2];
-#pragma unroll
-          for (int part = 0; part < 2; ++part) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const float pv = sb[2 * kb + h][i];
-                const float ph = rbf(pv);
-                *reinterpret_cast<bf16_t*>(Pst + (4 * (c.lane >> 4) + i) * 64 + (h * 16 + (c.lane & 15)) * 2) =
-                    f2bf(part == 0 ? ph : pv - ph);
-              }
-            pf[part] = ldsfrag(Pst + (c.lane & 15) * 64 + (c.lane >> 4) * 16);
-          }
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const bf16x8 vf = ldsfrag(slot + 8192 + (kb * 4 + dt) * 1024 + c.lane * 16);
-            acc[u][dt] = mfma16(pf[0], vf, acc[u][dt]);
-            acc[u][dt] = mfma16(pf[1], vf, acc[u][dt]);
+          for (int q = 0; q < NP; ++q) dd += x[q][0] * wa[q][0] + x[q][1] * wa[q][1] + x[q][2] * wa[q][2] + x[q][3] * wa[q][3];
+          dd = wave_sum(dd);
+          if (c.lane == 0) {
+            float* xn = d.last ? p.x_out : c.xstep(d.s + 1);
+            const float xa = a_out < adim ? xcur[(long long)ri * p.A + a_out] : 0.f;
+            st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + a_out) * 4), __float_as_uint(xa + c.dt * (dd + p.bout[a_out])));
           }
         }
       }
+    } else if (inproj) {
+      for (int it = c.tid; it < nrows * adim; it += NTHREADS) {
+        const int ri = it / adim, a = it - ri * adim;
+        xp[it] = xcur[(long long)ri * p.A + a];
+      }
     }
-    __syncthreads();
-    if (jb + 4 < nblk) ca_dma_block(c, l, b, hd, jb + 4);
-  }
-#pragma unroll
-  for (int u = 0; u < MAXQT; ++u) {
-    const int qt = c.wave + NWAVES * u;
-    if (qt < NOWN / 16) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int q = qt * 16 + 4 * (c.lane >> 4) + i;
-          if (q < M) {
-            const long long off = ((long long)(hd * 4 + dt) * p.NRP + b * p.Mqp + q) * 16 + (c.lane & 15);
-            const float o = den[u][i] > 0.f ? acc[u][dt][i] / den[u][i] : 0.f;
-            st_sc1_b32(y, (uint32_t)(off * 4), __float_as_uint(o));
-          }
+    if (inproj) {
+      if (c.tid < adim * 4) {
+        const int a = c.tid >> 2, q = c.tid & 3;
+        *reinterpret_cast<f32x4*>(win_t + a * 16 + 4 * q) = ldf4(p.win + (long long)a * S::H + t * 16 + 4 * q);
+      }
+      __syncthreads();
+      MKX_TR(c, 1);
+      const int sn = d.first ? 0 : d.s + 1;
+      float* h0n = c.h0(sn);
+      for (int it = c.tid; it < p.NRP * 4; it += NTHREADS) {
+        const int row = it >> 2, q = it & 3;
+        const int b = row / p.Mqp, i = row - b * p.Mqp;
+        const int col = t * 16 + 4 * q;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 sc = ldf4(c.modrow(min(b, p.B - 1), sn) + col);  // layer 0 self-attention AdaRMS scale
+        if (b < p.B && i < p.T) {
+          v = ldf4(p.bin + col);
+          const float* xr = xp + (b * p.T + i) * adim;
+          for (int a = 0; a < adim; ++a) v += xr[a] * ldf4(win_t + a * 16 + 4 * q);
+        } else if (b < p.B && i < p.Mq) {
+          const uint2 r = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
+          v = f32x4{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                    __uint_as_float(r.y & 0xffff0000u)};
         }
+        st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
+        st_split4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc));
+        float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        if (q == 0) st_sc1_b32(c.ss0(sn), (uint32_t)(((long long)t * p.NRP + row) * 4), __float_as_uint(ss));
+      }
     }
   }
 }
 
 // ------------------------------------------------------------------------------------------------
-// Step tail (src/mk_expert.py:254-299): o = AdaRMS_final(h_L); v = o Wout^T + bout; x' = x_pad + dt v;
-// h0' = x'_pad Win + bin, all fp32. Tasks [0, H/16): in-projection tiles (they recompute the velocity of
-// the real action dims); tasks [H/16, H/16 + A): one output dim each. One wave per action row; lane < H/16
-// owns 16 columns; every constant a lane needs is loaded in one batch before use.
-constexpr int TAIL_AG = 8;  // output dims per batched group
-
+// DMA of the constant operands of this workgroup's first task of stage d (weight tile or cached K/V, Wout
+// rows) and of the stage's per-sample modulation slices.
 template <class S>
-__device__ void tail_velocity8(Ctx<S>& c, const float* hL, int grow, const float* mrow, int a0, int na, float* v) {
-  const int lane = c.lane;
-  const int lc = min(lane, S::HT - 1);
-  float x[16], sc[16], sh[16], w[TAIL_AG][16];
-  load8f(hL + ((long long)lc * c.p.NRP + grow) * 16, x);
-  load8f(hL + ((long long)lc * c.p.NRP + grow) * 16 + 8, x + 8);
-  load8f(mrow + lc * 16, sc);
-  load8f(mrow + lc * 16 + 8, sc + 8);
-  load8f(mrow + S::H + lc * 16, sh);
-  load8f(mrow + S::H + lc * 16 + 8, sh + 8);
-#pragma unroll
-  for (int a = 0; a < TAIL_AG; ++a) {
-    const float* wr = c.p.wout + (long long)min(a0 + a, c.p.A - 1) * S::H + lc * 16;
-    load8f(wr, w[a]);
-    load8f(wr + 8, w[a] + 8);
-  }
-  float ss = 0.f;
-  if (lane < S::HT) {
-#pragma unroll
-    for (int q = 0; q < 16; ++q) ss += x[q] * x[q];
-  }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
-  const float r = rsqrtf(ss / (float)S::H + c.p.eps);
-  float o16[16];
-#pragma unroll
-  for (int q = 0; q < 16; ++q) o16[q] = lane < S::HT ? x[q] * r * (1.0f + sc[q]) + sh[q] : 0.f;
-#pragma unroll
-  for (int a = 0; a < TAIL_AG; ++a) {
-    float d = 0.f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) d += o16[q] * w[a][q];
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) d += __shfl_xor(d, o);
-    v[a] = d + (a < na ? c.p.bout[a0 + a] : 0.f);
-  }
-}
-
-template <class S>
-__device__ void tail_stage(Ctx<S>& c, int s, bool first, bool last, const float* hL) {
+__device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
-  const int nin = last ? 0 : S::HT;
-  const int nout = first ? 0 : p.A;
-  const int nrows = p.B * p.T;
-  const int adim = p.action_dim;
-  const float* xcur = (first || s == 0) ? p.x_in : c.xstep(s);
-  float* xp = (float*)(c.smem + S::ABUF);  // [nrows][action_dim] x' of the real dims
-  for (int t = c.wg; t < nin + nout; t += c.G) {
-    __syncthreads();
-    if (t < nin) {
-      for (int ri = c.wave; ri < nrows; ri += NWAVES) {
-        const int b = ri / p.T, i = ri % p.T;
-        if (first) {
-          if (c.lane < adim) xp[ri * adim + c.lane] = xcur[(long long)ri * p.A + c.lane];
-        } else {
-          const float* mrow = c.modrow(b, s) + 9 * p.L * S::H;
-          for (int a0 = 0; a0 < adim; a0 += TAIL_AG) {
-            float v[TAIL_AG];
-            tail_velocity8(c, hL, b * p.Mqp + i, mrow, a0, min(TAIL_AG, adim - a0), v);
-            if (c.lane < TAIL_AG && a0 + c.lane < adim) {
-              float vv = v[0];
-#pragma unroll
-              for (int a = 1; a < TAIL_AG; ++a) vv = c.lane == a ? v[a] : vv;
-              xp[ri * adim + a0 + c.lane] = xcur[(long long)ri * p.A + a0 + c.lane] + c.dt * vv;
-            }
-          }
-        }
-      }
-      __syncthreads();
-      float* h0n = c.h0(first ? 0 : s + 1);
-      const int col0 = t * 16;
-      for (int it = c.tid; it < p.NRP * 2; it += NTHREADS) {
-        const int grow = it >> 1, half = it & 1;
-        const int b = grow / p.Mqp, i = grow % p.Mqp;
-        const int col = col0 + half * 8;
-        float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (b < p.B && i < p.T) {
-          load8f(p.bin + col, v);
-          const float* xr = xp + (b * p.T + i) * adim;
-          for (int a0 = 0; a0 < adim; a0 += TAIL_AG) {
-            float w[TAIL_AG][8];
-#pragma unroll
-            for (int a = 0; a < TAIL_AG; ++a) load8f(p.win + (long long)min(a0 + a, p.A - 1) * S::H + col, w[a]);
-#pragma unroll
-            for (int a = 0; a < TAIL_AG; ++a)
-              if (a0 + a < adim) {
-                const float xa = xr[a0 + a];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) v[q] += xa * w[a][q];
-              }
-          }
-        } else if (b < p.B && i < p.Mq) {
-          unpack8(ld16(p.reg_tok + (long long)(i - p.T) * S::H + col), v);
-        }
-        st8f_sc1(h0n, ((long long)t * p.NRP + grow) * 16 + half * 8, v);
-      }
-    } else {
-      const int a = t - nin;
-      float* xn = last ? p.x_out : c.xstep(s + 1);
-      for (int ri = c.wave; ri < nrows; ri += NWAVES) {
-        const int b = ri / p.T, i = ri % p.T;
-        const float* mrow = c.modrow(b, s) + 9 * p.L * S::H;
-        float v[TAIL_AG];
-        tail_velocity8(c, hL, b * p.Mqp + i, mrow, a, 1, v);
-        if (c.lane == 0) {
-          const float xa = a < adim ? xcur[(long long)ri * p.A + a] : 0.f;
-          st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + a) * 4), __float_as_uint(xa + c.dt * v[0]));
-        }
-      }
+  const int t = c.wg;
+  char* mb = c.smem + S::MODS;
+  if (d.st == ST_SA || d.st == ST_CA) {
+    const AttnTask at = attn_task(t, p.Mqp / 16, p.B * S::NH);
+    if (at.ok) {
+      const int b = at.hh / S::NH, hd = at.hh % S::NH;
+      if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
+      else ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);
+    }
+  } else if (d.st == ST_TAIL) {
+    if (!d.first && t < (d.last ? 0 : S::HT) + p.A) {
+      for (int b = 0; b < p.B; ++b) dma_f32(c, mb + b * 2 * S::H * 4, c.modrow(b, d.s) + 9 * p.L * S::H, 2 * S::H);
+      dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
+    }
+  } else if (t < d.ntask) {
+    dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
+    const bool two = d.kind == K_RES || d.kind == K_SPLIT;  // gate and the next AdaRMS scale
+    for (int b = 0; b < p.B; ++b) {
+      const float* mr = c.modrow(b, d.s);
+      dma_f32(c, mb + b * (two ? 2 : 1) * S::H * 4, mr + d.mod_off, S::H);
+      if (two) dma_f32(c, mb + (b * 2 + 1) * S::H * 4, mr + d.mod_off2, S::H);
     }
   }
 }
@@ -951,8 +1195,9 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   __shared__ __attribute__((aligned(1024))) char smem[S::LDS];
   CP& p = *(CP*)(__builtin_amdgcn_kernarg_segment_ptr());
   Ctx<S> c(p, smem);
-  c.dt = p.dt[0];
-  int* s_ks = (int*)(smem + S::SMALL + 3 * 1024 + 64);  // kv_start[B], ca_len[B]
+  const float dt = p.dt[0];
+  c.dt = dt;
+  int* s_ks = (int*)(smem + S::SMALL + 3 * 1024);  // kv_start[MAX_BATCH], ca_len[MAX_BATCH]
   if (c.tid < p.B) {
     s_ks[c.tid] = min(max(p.kv_start[c.tid], 0), p.PM);
     s_ks[MAX_BATCH + c.tid] = min(max(p.ca_len[c.tid], 0), p.SP);
@@ -969,116 +1214,38 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (c.wg == 0 && c.tid < S::HT) __hip_atomic_store(&p.dcnt[c.tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  const int NRP = p.NRP;
-  const int NBH = p.B * S::NH;
-  unsigned long long e = 0;
   if (p.profile && c.wg == 0 && c.tid == 0) p.prof[0] = clock100() * 10;
 
-  // DMA of the constant operands of this workgroup's first task in a stage (weight tile or cached K/V)
-  // and of the stage's per-sample modulation slices
-  auto prefetch = [&](int s, int l, int st) {
-    char* wb = smem + S::WBUF;
-    char* mb = smem + S::MODS;
-    const int t = c.wg;
-    const int m_sa = 9 * l * H, m_ca = m_sa + 3 * H, m_mlp = m_sa + 6 * H;
-    auto stage_mods = [&](int off, int width) {
-      for (int b = 0; b < p.B; ++b) dma_f32(c, mb + b * width * 4, c.modrow(b, s) + off, width);
-    };
-    switch (st) {
-      case ST_QKV:
-        if (t < 3 * S::HT) { dma_w(c, wb, p.wqkv + l * p.s_qkv + (long long)t * S::NKB * 512, S::NKB); stage_mods(m_sa, 2 * H); }
-        break;
-      case ST_SA: if (t < NBH) sa_prefetch(c, l, t / S::NH, t % S::NH); break;
-      case ST_O:
-        if (t < S::HT) { dma_w(c, wb, p.wo + l * p.s_o + (long long)t * S::NKB * 512, S::NKB); stage_mods(m_sa + 2 * H, H); }
-        break;
-      case ST_CAQ:
-        if (t < S::HT) { dma_w(c, wb, p.wqca + l * p.s_o + (long long)t * S::NKB * 512, S::NKB); stage_mods(m_ca, 2 * H); }
-        break;
-      case ST_CA: if (t < NBH) ca_prefetch(c, l, t / S::NH, t % S::NH, s_ks[MAX_BATCH + t / S::NH]); break;
-      case ST_CAO:
-        if (t < S::HT) { dma_w(c, wb, p.woca + l * p.s_o + (long long)t * S::NKB * 512, S::NKB); stage_mods(m_ca + 2 * H, H); }
-        break;
-      case ST_GU:
-        if (t < S::IT) { dma_w(c, wb, p.wgu + l * p.s_gu + (long long)t * 2 * S::NKB * 512, 2 * S::NKB); stage_mods(m_mlp, 2 * H); }
-        break;
-      case ST_DOWN:
-        if (t < S::HT * S::SK) {
-          const int tile = t % S::HT, split = t / S::HT;
-          dma_w(c, wb, p.wd + l * p.s_d + ((long long)tile * S::SK + split) * S::NKB * 512, S::NKB);
-          stage_mods(m_mlp + 2 * H, H);
-        }
-        break;
-      default: break;
+  const int total = 1 + p.n_steps * (8 * p.L + 1);
+  for (int g = 0; g < total; ++g) {
+    {
+      // parameters are re-read from the kernarg segment in every stage instead of being kept live (and
+      // spilled) across the whole loop
+      CP* pl = (CP*)__builtin_amdgcn_kernarg_segment_ptr();
+      asm volatile("" : "+s"(pl));
+      Ctx<S> c(*pl, smem);
+      c.dt = dt;
+      c.ep = (unsigned)g;
+      const Desc cur = describe(c, g);
+      if (cur.st == ST_SA) sa_stage(c, cur, s_ks);
+      else if (cur.st == ST_CA) ca_stage(c, cur, s_ks);
+      else if (cur.st == ST_TAIL) tail_stage(c, cur);
+      else gemm_stage(c, cur);
+      if (g == 0) transpose_caches(c, s_ks);
     }
-  };
-  auto sync_next = [&](int s, int l, int st) {
-    bar_arrive(bc, ++e);
-    if (st >= 0) prefetch(s, l, st);
-    bar_wait(bc, e);
-    if (p.profile && c.wg == 0 && c.tid == 0) p.prof[e] = clock100() * 10;
-  };
-
-  // in-projection of the incoming x (src/mk_expert.py:326-327)
-  tail_stage(c, 0, true, false, nullptr);
-  sync_next(0, 0, ST_QKV);
-  for (int s = 0; s < p.n_steps; ++s) {
-    for (int l = 0; l < p.L; ++l) {
-      char* fr = c.frame(s, l);
-      const float* hin = c.h_in(s, l);
-      float* qkv = (float*)(fr + S::qkv_off(NRP));
-      float* ysa = (float*)(fr + S::ysa_off(NRP));
-      float* h2 = (float*)(fr + S::h2_off(NRP));
-      float* qca = (float*)(fr + S::qca_off(NRP));
-      float* yca = (float*)(fr + S::yca_off(NRP));
-      float* h3 = (float*)(fr + S::h3_off(NRP));
-      float* g = (float*)(fr + S::g_off(NRP));
-      float* hl = (float*)(fr + S::hl_off(NRP));
-      float* part = (float*)(fr + S::part_off(NRP));
-      // 1. qkv = AdaRMS(h) @ Wqkv^T
-      gemm_stage<S, 1, K_PLAIN, true>(c, s, 3 * S::HT, p.wqkv + l * p.s_qkv, S::NKB * 512, hin, qkv, nullptr, nullptr, 0);
-      sync_next(s, l, ST_SA);
-      // 2. self-attention per (sample, head)
-      for (int t = c.wg; t < NBH; t += c.G) {
-        if (t != c.wg) { __syncthreads(); sa_prefetch(c, l, t / S::NH, t % S::NH); }
-        wait_vm0();
-        __syncthreads();
-        sa_task(c, s, l, t / S::NH, t % S::NH, qkv, ysa, s_ks[t / S::NH]);
-        __syncthreads();
-      }
-      sync_next(s, l, ST_O);
-      // 3. h2 = h + (y @ Wo^T) * gate_sa
-      gemm_stage<S, 1, K_RES, false>(c, s, S::HT, p.wo + l * p.s_o, S::NKB * 512, ysa, h2, hin, nullptr, 0);
-      sync_next(s, l, ST_CAQ);
-      // 4. qca = AdaRMS_ca(h2) @ Wqca^T
-      gemm_stage<S, 1, K_PLAIN, true>(c, s, S::HT, p.wqca + l * p.s_o, S::NKB * 512, h2, qca, nullptr, nullptr, 0);
-      sync_next(s, l, ST_CA);
-      // 5. cross-attention per (sample, head)
-      for (int t = c.wg; t < NBH; t += c.G) {
-        if (t != c.wg) { __syncthreads(); ca_prefetch(c, l, t / S::NH, t % S::NH, s_ks[MAX_BATCH + t / S::NH]); }
-        __syncthreads();
-        ca_task(c, s, l, t / S::NH, t % S::NH, qca, yca, s_ks[MAX_BATCH + t / S::NH]);
-        __syncthreads();
-      }
-      sync_next(s, l, ST_CAO);
-      // 6. h3 = h2 + (y @ Woca^T) * gate_ca
-      gemm_stage<S, 1, K_RES, false>(c, s, S::HT, p.woca + l * p.s_o, S::NKB * 512, yca, h3, h2, nullptr, 0);
-      sync_next(s, l, ST_GU);
-      // 7. g = act(A Wg^T) * (A Wu^T), A = AdaRMS_mlp(h3)
-      gemm_stage<S, 2, K_GU, true>(c, s, S::IT, p.wgu + l * p.s_gu, 2 * S::NKB * 512, h3, g, nullptr, nullptr, 0);
-      sync_next(s, l, ST_DOWN);
-      // 8. h = h3 + (g @ Wd^T) * gate_mlp, K split in I/H parts
-      gemm_stage<S, 1, K_SPLIT, false>(c, s, S::HT * S::SK, p.wd + l * p.s_d, 0, g, hl, h3, part, S::HT);
-      if (l + 1 < p.L) sync_next(s, l + 1, ST_QKV);
-      else sync_next(s, 0, -1);
-    }
-    // step tail
-    const float* hL = (const float*)(c.frame(s, p.L - 1) + S::hl_off(NRP));
-    tail_stage(c, s, false, s + 1 == p.n_steps, hL);
-    if (s + 1 < p.n_steps) sync_next(s + 1, 0, ST_QKV);
-    else sync_next(s, 0, -1);
+    // barrier; the next stage's constant operands are DMA'd while it completes
+    c.ep = (unsigned)g;
+    MKX_TR(c, 4);
+    bar_arrive(bc, (unsigned long long)g + 1);
+    MKX_TR(c, 5);
+    if (g + 1 < total) prefetch(c, describe(c, g + 1), s_ks);
+    MKX_TR(c, 6);
+    bar_wait(bc, (unsigned long long)g + 1);
+    c.ep = (unsigned)(g + 1);
+    MKX_TR(c, 0);
+    if (p.profile && c.wg == 0 && c.tid == 0) p.prof[g + 1] = clock100() * 10;
   }
-  if (c.wg == 0 && c.tid == 0) __hip_atomic_store(&p.bar->gen, bc.base + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (c.wg == 0 && c.tid == 0) __hip_atomic_store(&p.bar->gen, bc.base + (unsigned long long)total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace mkx
