@@ -55,6 +55,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--stage-profile", action="store_true", help="also print per-stage barrier timestamps (stderr)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 device copies of MIB MiB (reference kernel for the HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the megakernel runs on a single MI355X (batch samples would shard "
@@ -63,6 +65,16 @@ def main() -> int:
 
     import torch
     from mkx import ExpertMegakernel, synthetic as SY
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read": n, "bytes_written": n, "launches": 5}}), flush=True)
+        return 0
 
     torch.set_grad_enabled(False)
     cfg = SY.WORKLOADS[args.workload]
@@ -170,7 +182,12 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out))
+    print(json.dumps(out), flush=True)
+    # release device memory before interpreter teardown (profilers finalise at exit)
+    torch.cuda.synchronize()
+    del plan
+    mk.close()
+    torch.cuda.synchronize()
     return 0
 
 

@@ -125,7 +125,10 @@ typedef enum {
 } mkx_query_key;
 
 /* ExpertMegakernel.__init__ (src/mk_expert.py:436-481). Validates dims, copies and repacks the weights
- * on `stream` (synchronised before return), allocates scratch, checks co-residency. */
+ * on `stream` (synchronised before return), allocates scratch, checks co-residency. Launches are
+ * cooperative; with the environment variable MKX_PLAIN_LAUNCH=1 set at creation they are plain launches
+ * of the same grid (one workgroup per CU, co-resident when the GPU runs nothing else), which some
+ * profilers require. */
 int mkx_create(const mkx_dims* dims, const mkx_weights* weights, void* stream, mkx_handle** out);
 
 /* ExpertMegakernel.run (src/mk_expert.py:483-515): one persistent launch on `stream` (a hipStream_t;

@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -110,6 +111,7 @@ struct mkx_handle {
   long long* prof = nullptr;
   int prof_len = 0;
   int profile = 0;
+  int plain_launch = 0;  // MKX_PLAIN_LAUNCH=1 at creation: hipLaunchKernel instead of the cooperative launch
   unsigned long long gen_before = 0;
   long long last_nbar = 0;
   long long weight_bytes = 0;
@@ -181,6 +183,10 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NTHREADS, 0));
   if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel does not fit one workgroup per CU"));
   h->G = prop.multiProcessorCount;
+  {
+    const char* pl = std::getenv("MKX_PLAIN_LAUNCH");
+    h->plain_launch = (pl && pl[0] == '1') ? 1 : 0;
+  }
   // XCD of each workgroup of a G-workgroup launch; the barrier's per-XCD counts come from it
   unsigned* dx = nullptr;
   HCHK(hipMalloc(&dx, sizeof(unsigned) * h->G));
@@ -297,7 +303,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   if ((long long)a->B * 2 * H * 4 > 56 * 1024) return fail(MKX_EUNSUPPORTED, "batch too large to stage its modulation slices in LDS");
   if (h->profile && 1 + a->n_steps * (8LL * L + 1) + 1 > h->prof_len) return fail(MKX_EINVAL, "profile buffer shorter than barriers + 1");
 #ifdef MKX_TRACE
-  if (h->profile && mkx::TRACE_BASE + (2 + a->n_steps * (8LL * L + 1)) * h->G * 8 > h->prof_len)
+  if (h->profile && mkx::TRACE_BASE + (2 + a->n_steps * (8LL * L + 1)) * h->G * mkx::TRACE_SLOTS > h->prof_len)
     return fail(MKX_EINVAL, "trace buffer too short");
 #endif
   // scratch: one frame per (step, layer), one step area per step; grown on demand
@@ -363,7 +369,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   void* args[] = {&p};
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   HIPCHK(hipStreamIsCapturing(stream, &cs));
-  if (cs == hipStreamCaptureStatusActive) {
+  if (cs == hipStreamCaptureStatusActive || h->plain_launch) {
     // co-residency was established at creation (one workgroup per CU fits); capture a plain launch
     HIPCHK(hipLaunchKernel(h->kernel, dim3(h->G), dim3(NTHREADS), args, 0, stream));
   } else {

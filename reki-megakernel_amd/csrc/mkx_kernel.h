@@ -97,7 +97,9 @@ struct Shape {
   // frame layout (bytes), buffers of NRP rows; HB = NRP * H * 4:
   //   qs, ks: split q / k (roped, not normed) | vt: split V^T blocks per (sample, head) (2 HB) | ysa split |
   //   h2 fp32 | y2 split | qcas split | yca split | h3 fp32 | y3 split | g split (I columns) | hl fp32 |
-  //   yl split | part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ssca [NH][2][NRP] | ss2, ss3, ssl [HT][NRP]
+  //   yl split | part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ssca [NH][2][NRP] | ss2, ss3, ssl [NRP][HT]
+  // (sums of squares of h per 16-column tile t, at row * HT + (t % 4) * HT / 4 + t / 4: wave w of a consumer
+  // reads its tiles w + 4 i as one contiguous run)
   __host__ __device__ static long long hb(int nrp) { return (long long)nrp * H * 4; }
   __host__ __device__ static long long qs_off(int) { return 0; }
   __host__ __device__ static long long ks_off(int nrp) { return hb(nrp); }
@@ -119,7 +121,7 @@ struct Shape {
   __host__ __device__ static long long ss3_off(int nrp) { return ss2_off(nrp) + (long long)HT * nrp * 4; }
   __host__ __device__ static long long ssl_off(int nrp) { return ss3_off(nrp) + (long long)HT * nrp * 4; }
   __host__ __device__ static long long frame_bytes(int nrp) { return ssl_off(nrp) + (long long)HT * nrp * 4; }
-  // step area: h0 fp32 | y0 split | ss0 [HT][NRP] | x [B*T][A] fp32
+  // step area: h0 fp32 | y0 split | ss0 [NRP][HT] | x [B*T][A] fp32
   __host__ __device__ static long long step_x_off(int nrp) { return 2 * hb(nrp) + (long long)HT * nrp * 4; }
 };
 
@@ -136,16 +138,23 @@ enum Stage { ST_QKV = 0, ST_SA, ST_O, ST_CAQ, ST_CA, ST_CAO, ST_GU, ST_DOWN, ST_
 enum { K_QKV = 0, K_RES = 1, K_GU = 2, K_SPLIT = 3 };
 
 // Optional per-workgroup phase trace (diagnostic builds with MKX_TRACE): clock of phase `slot` of the
-// interval after barrier ep, at prof[TRACE_BASE + (ep * G + wg) * 8 + slot].
-constexpr long long TRACE_BASE = 8192;
+// interval after barrier ep, at prof[TRACE_BASE + (ep * G + wg) * TRACE_SLOTS + slot].
+constexpr long long TRACE_BASE = 8192, TRACE_SLOTS = 16;
 #ifdef MKX_TRACE
 #define MKX_TR(c, slot)                                                                                          \
   do {                                                                                                           \
-    if ((c).tid == 0 && (c).p.profile) (c).p.prof[TRACE_BASE + ((long long)(c).ep * (c).G + (c).wg) * 8 + (slot)] = clock100(); \
+    if ((c).tid == 0 && (c).p.profile) (c).p.prof[TRACE_BASE + ((long long)(c).ep * (c).G + (c).wg) * TRACE_SLOTS + (slot)] = clock100(); \
+  } while (0)
+#define MKX_TRW(c, slot)                                                                                         \
+  do {                                                                                                           \
+    if ((c).tid == 64 && (c).p.profile) (c).p.prof[TRACE_BASE + ((long long)(c).ep * (c).G + (c).wg) * TRACE_SLOTS + (slot)] = clock100(); \
   } while (0)
 #else
 #define MKX_TR(c, slot) \
   do {                  \
+  } while (0)
+#define MKX_TRW(c, slot) \
+  do {                   \
   } while (0)
 #endif
 
@@ -154,12 +163,15 @@ struct Ctx {
   CP& p;
   char* smem;
   int wg, G, wave, lane, tid, RT;
+  int dw, dn;  // DMA issue: this wave's index among the dn issuing waves (all 4, or waves 1-3 in a barrier)
   unsigned ep = 0;  // barriers passed so far in this launch
   float dt;
   __device__ Ctx(CP& p_, char* smem_) : p(p_), smem(smem_) {
     wg = blockIdx.x; G = gridDim.x; tid = threadIdx.x; lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so offsets built from it stay scalar
     RT = p.NRP >> 4;
+    dw = wave;
+    dn = NWAVES;
   }
   __device__ char* frame(int s, int l) const { return p.frames + (long long)(s * p.L + l) * p.frame_bytes; }
   __device__ char* step(int s) const { return p.steps + (long long)s * p.step_bytes; }
@@ -197,12 +209,12 @@ __device__ __forceinline__ u32x4 as_u4(f32x4 v) { return __builtin_bit_cast(u32x
 
 template <class S>
 __device__ __forceinline__ void dma_w(Ctx<S>& c, char* dst, const bf16_t* src, int nchunks) {
-  for (int k = c.wave; k < nchunks; k += NWAVES) dma16(src + (long long)k * 512 + c.lane * 8, dst + k * 1024);
+  for (int k = c.dw; k < nchunks; k += c.dn) dma16(src + (long long)k * 512 + c.lane * 8, dst + k * 1024);
 }
 // nfloats (a multiple of 256) contiguous fp32 values into LDS
 template <class S>
 __device__ __forceinline__ void dma_f32(Ctx<S>& c, char* dst, const float* src, int nfloats) {
-  for (int k = c.wave; k < nfloats / 256; k += NWAVES) dma16(src + (long long)k * 256 + c.lane * 4, dst + k * 1024);
+  for (int k = c.dw; k < nfloats / 256; k += c.dn) dma16(src + (long long)k * 256 + c.lane * 4, dst + k * 1024);
 }
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -367,6 +379,11 @@ __device__ __forceinline__ const bf16_t* wtile(const Desc& d, int t) {
 //     partials in split order and applies K_RES.
 // K (= H per task) is split over the 4 waves; the wave partials are summed through LDS.
 
+// byte offset of the sum of squares of (row, 16-column tile t) in an [NRP][HT] array
+__device__ __forceinline__ uint32_t ss_slot(int row, int t, int HT) {
+  return (uint32_t)((row * HT + (t & 3) * (HT / 4) + (t >> 2)) * 4);
+}
+
 // residual epilogue of one 4-column piece: h = res + v * gate; stores h, y = h (1 + next scale) and the
 // piece's share of the row's sum of squares (lanes L, L^16, L^32, L^48 hold one row's 16 columns)
 template <class S>
@@ -379,7 +396,7 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
   float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
   ss += __shfl_xor(ss, 16);
   ss += __shfl_xor(ss, 32);
-  if (L < 16) st_sc1_b32(d.ssout, (uint32_t)(((long long)tile * c.p.NRP + row) * 4), __float_as_uint(ss));
+  if (L < 16) st_sc1_b32(d.ssout, ss_slot(row, tile, S::HT), __float_as_uint(ss));
 }
 
 // q/k epilogue of one row: xa, xb = columns d0 .. d0+3 and d0+32 .. d0+35 of head hd (kind 0 = q, 1 = k;
@@ -445,16 +462,25 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
           ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
           al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
         }
-      float ssp = 0.f;
-      if (ada) {  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
-        const int row = min(rt0 * 16 + c.lane, NRP - 1);
+      u32x4 ssv[S::HT / 16];  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
+      if (ada) {
+        const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
+        const uint32_t so = (uint32_t)((min(rt0 * 16 + c.lane, NRP - 1) * S::HT + c.wave * (S::HT / 4)) * 4);
 #pragma unroll
-        for (int i = 0; i < S::HT / NWAVES; ++i) ssp += d.ssin[(long long)(c.wave + NWAVES * i) * NRP + row];
+        for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
       }
       wait_vm0();  // activations, and the staged weights and modulation slices, have landed
       __syncthreads();
       MKX_TR(c, 1);
-      if (ada) ssw[c.wave * 64 + c.lane] = ssp;
+      if (ada) {
+        float ssp = 0.f;
+#pragma unroll
+        for (int i = 0; i < S::HT / 16; ++i) {
+          const f32x4 x = as_f4(ssv[i]);
+          ssp += (x[0] + x[1]) + (x[2] + x[3]);
+        }
+        ssw[c.wave * 64 + c.lane] = ssp;
+      }
       f32x4 acc[RB + 1][2];
 #pragma unroll
       for (int rt = 0; rt <= RB; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -759,7 +785,7 @@ __device__ __forceinline__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd, int
   const bf16_t* mk = c.p.memk[l] + (long long)b * c.p.mem_sb;
   const bf16_t* mvt = c.p.memvt + ((long long)(l * c.p.B + b) * S::NH + hd) * PMP * 64;
   const int nk = (PMP / 16) * 2, nv = PMP / 8;
-  for (int k = c.wave; k < nk + nv; k += NWAVES) {
+  for (int k = c.dw; k < nk + nv; k += c.dn) {
     if (k < nk) {
       // rows outside [kv_start, PM) are replaced by valid rows (they are masked): every operand is finite
       const int kt = k >> 1, db = k & 1;
@@ -957,7 +983,7 @@ __device__ __forceinline__ void ca_dma_chunk(Ctx<S>& c, int l, int b, int hd, in
   const bf16_t* kb_ = c.p.kca[l] + (long long)b * c.p.src_sb;
   const int ncb = c.p.SPP / 32;
   const bf16_t* vt = c.p.cavt + ((long long)(l * c.p.B + b) * S::NH + hd) * ncb * 2048;
-  for (int k = c.wave; k < 32; k += NWAVES) {
+  for (int k = c.dw; k < 32; k += c.dn) {
     if (k < 16) {
       // rows beyond the valid length are replaced by the last valid row (they are masked)
       const int kt = k >> 1, db = k & 1;
@@ -1151,7 +1177,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
         ss += __shfl_xor(ss, 1);
         ss += __shfl_xor(ss, 2);
-        if (q == 0) st_sc1_b32(c.ss0(sn), (uint32_t)(((long long)t * p.NRP + row) * 4), __float_as_uint(ss));
+        if (q == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, t, S::HT), __float_as_uint(ss));
       }
     }
   }
@@ -1161,10 +1187,11 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
 // DMA of the constant operands of this workgroup's first task of stage d (weight tile or cached K/V, Wout
 // rows) and of the stage's per-sample modulation slices.
 template <class S>
-__device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_ks) {
+__device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
   const int t = c.wg;
   char* mb = c.smem + S::MODS;
+  MKX_TRW(c, 8);
   if (d.st == ST_SA || d.st == ST_CA) {
     const AttnTask at = attn_task(t, p.Mqp / 16, p.B * S::NH);
     if (at.ok) {
@@ -1179,6 +1206,7 @@ __device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_
     }
   } else if (t < d.ntask) {
     dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
+    MKX_TRW(c, 9);
     const bool two = d.kind == K_RES || d.kind == K_SPLIT;  // gate and the next AdaRMS scale
     for (int b = 0; b < p.B; ++b) {
       const float* mr = c.modrow(b, d.s);
@@ -1186,6 +1214,18 @@ __device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_
       if (two) dma_f32(c, mb + (b * 2 + 1) * S::H * 4, mr + d.mod_off2, S::H);
     }
   }
+}
+
+// the prefetch of the next stage is issued by waves 1-3 while wave 0 completes the barrier
+template <class S>
+__device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_ks) {
+  if (c.wave == 0) return;
+  c.dw = c.wave - 1;
+  c.dn = NWAVES - 1;
+  prefetch_body(c, d, s_ks);
+  MKX_TRW(c, 10);
+  c.dw = c.wave;
+  c.dn = NWAVES;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1236,9 +1276,12 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
     // barrier; the next stage's constant operands are DMA'd while it completes
     c.ep = (unsigned)g;
     MKX_TR(c, 4);
+    wait_vm0();  // (bar_arrive waits for the stores too; separated here so a trace can time it)
+    MKX_TR(c, 11);
     bar_arrive(bc, (unsigned long long)g + 1);
     MKX_TR(c, 5);
-    if (g + 1 < total) prefetch(c, describe(c, g + 1), s_ks);
+    MKX_TRW(c, 12);
+    if (g + 1 < total && c.wave != 0) prefetch(c, describe(c, g + 1), s_ks);
     MKX_TR(c, 6);
     bar_wait(bc, (unsigned long long)g + 1);
     c.ep = (unsigned)(g + 1);

@@ -84,14 +84,18 @@ class ExpertMegakernel:
         self.cfg = {"block": int(lib().mkx_query(h, _lib.Q_BLOCK)), "lds_bytes": int(lib().mkx_query(h, _lib.Q_LDS_BYTES)),
                     "grid": self.nprog, "PROFILE": False}
 
-    def __del__(self):
+    def close(self) -> None:
+        """Releases the handle's device memory now (also done at garbage collection)."""
         h = getattr(self, "_h", None)
         if h is not None and h.value:
-            try:
-                lib().mkx_destroy(h)
-            except Exception:  # interpreter shutdown
-                pass
-            self._h = None
+            lib().mkx_destroy(h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown
+            pass
 
     # ------------------------------------------------------------------------------------------
     def _args(self, x_t, mods, dt, past, action_dim, n_steps, mod_row0, first, cur_k=None, cur_v=None):
