@@ -1257,6 +1257,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   if (p.profile && c.wg == 0 && c.tid == 0) p.prof[0] = clock100() * 10;
 
   const int total = 1 + p.n_steps * (8 * p.L + 1);
+  Desc cur = describe(c, 0);
   for (int g = 0; g < total; ++g) {
     {
       // parameters are re-read from the kernarg segment in every stage instead of being kept live (and
@@ -1266,7 +1267,6 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       Ctx<S> c(*pl, smem);
       c.dt = dt;
       c.ep = (unsigned)g;
-      const Desc cur = describe(c, g);
       if (cur.st == ST_SA) sa_stage(c, cur, s_ks);
       else if (cur.st == ST_CA) ca_stage(c, cur, s_ks);
       else if (cur.st == ST_TAIL) tail_stage(c, cur);
@@ -1281,7 +1281,11 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
     bar_arrive(bc, (unsigned long long)g + 1);
     MKX_TR(c, 5);
     MKX_TRW(c, 12);
-    if (g + 1 < total && c.wave != 0) prefetch(c, describe(c, g + 1), s_ks);
+    // the next stage's descriptor, computed while the barrier completes
+    if (g + 1 < total) {
+      cur = describe(c, g + 1);
+      if (c.wave != 0) prefetch(c, cur, s_ks);
+    }
     MKX_TR(c, 6);
     bar_wait(bc, (unsigned long long)g + 1);
     c.ep = (unsigned)(g + 1);
