@@ -311,7 +311,9 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   const long long sb = step_bytes(H, I, NRP, a->B * a->T_act, d.A);
   const size_t need_f = (size_t)fb * a->n_steps * L, need_s = (size_t)sb * a->n_steps;
   const int PMP = ceil32(a->PM), SPP = ceil32(a->SP);
-  const size_t need_v = (size_t)L * a->B * (H / 64) * (PMP + SPP) * 128;
+  // V^T copies (bf16) and the split AdaRMS shift operands (B * H * 4 bytes per step, layer and AdaRMS)
+  const size_t vt_bytes = (size_t)L * a->B * (H / 64) * (PMP + SPP) * 128;
+  const size_t need_v = vt_bytes + (size_t)a->n_steps * L * 3 * a->B * H * 4;
   if (need_f > h->frames_cap || need_s > h->steps_cap || need_v > h->vts_cap) {
     HIPCHK(hipStreamSynchronize(stream));
     if (need_f > h->frames_cap) {
@@ -357,6 +359,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.reg_tok = (const bf16_t*)a->reg_tok; p.cur_k = (bf16_t*)a->cur_k; p.cur_v = (bf16_t*)a->cur_v;
   p.n_steps = a->n_steps; p.action_dim = a->action_dim; p.T = a->T_act; p.R = a->R_reg; p.B = a->B;
   p.memvt = h->vts; p.cavt = h->vts + (size_t)L * a->B * (H / 64) * PMP * 64; p.SPP = SPP;
+  p.shs = (char*)h->vts + vt_bytes;
   p.PM = a->PM; p.SP = a->SP; p.L = L; p.Mq = Mq; p.Mqp = Mqp; p.NR = NR; p.NRP = NRP; p.A = d.A;
   p.act = d.activation == MKX_ACT_GELU_TANH ? 1 : 0;
   p.eps = d.eps; p.qk_eps = d.qk_eps; p.sm_scale = 1.0f / 8.0f;

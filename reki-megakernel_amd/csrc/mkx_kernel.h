@@ -60,6 +60,10 @@ struct Params {
   // V^T copies of the memory / cross-attention V caches, made once per launch:
   // [L][B][NH][PMP/32 or SPP/32 key blocks][4 d-slices][512 bf16]
   bf16_t* memvt; bf16_t* cavt; int SPP;
+  // AdaRMS shift slices split into bf16 hi / lo, made once per launch: [n_steps][L][3: self-attn,
+  // cross-attn, MLP] blocks of B * H * 4 bytes; sample b's 8-column group (k-block kb, group j) is 16 bytes
+  // of hi then 16 bytes of lo at ((b * H/32 + kb) * 4 + j) * 32
+  char* shs;
   int n_steps, action_dim, T, R, B, PM, SP, L, Mq, Mqp, NR, NRP, A, act;
   float eps, qk_eps, sm_scale;
   // scratch
@@ -289,6 +293,7 @@ struct Desc {
   const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][NRP]
   int ntask, tiles, kind, nt;
   int qmode;                           // K_QKV: 0 = self-attention q/k/v, 1 = cross-attention query
+  const char* shs;                     // AdaRMS stages: the split shift fragments of this step and layer
   // staged modulation slices (H floats each, per sample): AdaRMS stages: shift; residual stages: gate, then
   // the scale of the next AdaRMS
   int mod_off, mod_off2;
@@ -301,7 +306,7 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
   d.first = g == 0;
   d.last = false;
   d.w = nullptr; d.wstride = 0; d.a = nullptr; d.out = nullptr; d.res = nullptr; d.part = nullptr;
-  d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr;
+  d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr; d.shs = nullptr;
   d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.qmode = 0; d.mod_off = 0; d.mod_off2 = 0;
   if (g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
   const int per_step = 8 * p.L + 1;
@@ -320,11 +325,12 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
   // cross-attention and the MLP; the next layer's (or the final) AdaRMS scale follows at 9 (l + 1) H
   const int m_sa = 9 * l * S::H, m_ca = m_sa + 3 * S::H, m_mlp = m_sa + 6 * S::H, m_next = m_sa + 9 * S::H;
   d.wstride = (long long)S::NKB * 512;
+  const char* shs = p.shs + (long long)(d.s * p.L + l) * 3 * p.B * S::H * 4;
   switch (d.st) {
     case ST_QKV:  // task ((kind * NH + head) * 2 + j): columns 16 j + [0, 16) and 16 j + 32 + [0, 16) of the head
       d.w = p.wqkv + l * p.s_qkv; d.wstride = 2LL * S::NKB * 512; d.a = c.y_in(d.s, l); d.ssin = c.ss_in(d.s, l);
       d.out = (float*)(fr + S::qs_off(NRP)); d.yout = (float*)(fr + S::ks_off(NRP)); d.part = (float*)(fr + S::vtb_off(NRP));
-      d.ssout = (float*)(fr + S::ssqk_off(NRP)); d.ntask = d.tiles = 6 * S::NH; d.nt = 2; d.mod_off = m_sa + S::H;
+      d.ssout = (float*)(fr + S::ssqk_off(NRP)); d.ntask = d.tiles = 6 * S::NH; d.nt = 2; d.shs = shs;
       break;
     case ST_O:
       d.w = p.wo + l * p.s_o; d.a = (const float*)(fr + S::ysa_off(NRP)); d.out = (float*)(fr + S::h2_off(NRP));
@@ -334,7 +340,8 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
     case ST_CAQ:
       d.w = p.wqca + l * p.s_o; d.wstride = 2LL * S::NKB * 512; d.a = (const float*)(fr + S::y2_off(NRP));
       d.ssin = (const float*)(fr + S::ss2_off(NRP)); d.out = (float*)(fr + S::qcas_off(NRP));
-      d.ssout = (float*)(fr + S::ssca_off(NRP)); d.ntask = d.tiles = 2 * S::NH; d.nt = 2; d.qmode = 1; d.mod_off = m_ca + S::H;
+      d.ssout = (float*)(fr + S::ssca_off(NRP)); d.ntask = d.tiles = 2 * S::NH; d.nt = 2; d.qmode = 1;
+      d.shs = shs + p.B * S::H * 4;
       break;
     case ST_CAO:
       d.w = p.woca + l * p.s_o; d.a = (const float*)(fr + S::yca_off(NRP)); d.out = (float*)(fr + S::h3_off(NRP));
@@ -345,7 +352,7 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
     case ST_GU:
       d.w = p.wgu + l * p.s_gu; d.wstride = 2LL * S::NKB * 512; d.a = (const float*)(fr + S::y3_off(NRP));
       d.ssin = (const float*)(fr + S::ss3_off(NRP)); d.out = (float*)(fr + S::g_off(NRP));
-      d.ntask = d.tiles = S::IT; d.kind = K_GU; d.nt = 2; d.mod_off = m_mlp + S::H;
+      d.ntask = d.tiles = S::IT; d.kind = K_GU; d.nt = 2; d.shs = shs + 2 * p.B * S::H * 4;
       break;
     case ST_DOWN:
       d.w = p.wd + l * p.s_d; d.a = (const float*)(fr + S::g_off(NRP)); d.out = (float*)(fr + S::hl_off(NRP));
@@ -462,8 +469,18 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
           ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
           al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
         }
+      bf16x8 sh_h[KPW], sh_l[KPW];  // the split shift fragments of this wave's k-blocks (rows = samples)
       u32x4 ssv[S::HT / 16];  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
       if (ada) {
+        // lane l reads sample l % 16; the samples >= B fall outside the buffer and read zeros
+        const __amdgpu_buffer_rsrc_t rsh =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(d.shs), (short)0, p.B * S::H * 4, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < KPW; ++i) {
+          const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + c.wave + NWAVES * i) * 4 + (c.lane >> 4)) * 32);
+          sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
+          sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
+        }
         const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
         const uint32_t so = (uint32_t)((min(rt0 * 16 + c.lane, NRP - 1) * S::HT + c.wave * (S::HT / 4)) * 4);
 #pragma unroll
@@ -517,24 +534,15 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
       }
       if (ada) {
         // shift W^T: row tile whose row b is sample b's shift slice (rows >= B are zero)
-        const int b = c.lane & 15;
-        const float* sh = mods_lds(c, min(b, p.B - 1), S::H);
 #pragma unroll
         for (int i = 0; i < KPW; ++i) {
           const int kb = c.wave + NWAVES * i;
-          const int col = kb * 32 + 8 * (c.lane >> 4);
-          const f32x4 s0 = ldf4(sh + col), s1 = ldf4(sh + col + 4);
-          const bool okb = b < p.B;
-          float v[8] = {okb ? s0[0] : 0.f, okb ? s0[1] : 0.f, okb ? s0[2] : 0.f, okb ? s0[3] : 0.f,
-                        okb ? s1[0] : 0.f, okb ? s1[1] : 0.f, okb ? s1[2] : 0.f, okb ? s1[3] : 0.f};
-          bf16x8 sh_h, sh_l;
-          split8(v, sh_h, sh_l);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) {
             if (nt < d.nt) {
               const bf16x8 wf = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
-              acc[RB][nt] = mfma16(wf, sh_h, acc[RB][nt]);
-              acc[RB][nt] = mfma16(wf, sh_l, acc[RB][nt]);
+              acc[RB][nt] = mfma16(wf, sh_h[i], acc[RB][nt]);
+              acc[RB][nt] = mfma16(wf, sh_l[i], acc[RB][nt]);
             }
           }
         }
@@ -794,6 +802,37 @@ __device__ __forceinline__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd, int
     } else {
       const int i = k - nk;
       dma16(mvt + (long long)i * 512 + c.lane * 8, memVt + i * 1024);
+    }
+  }
+}
+
+// Per-launch split of every AdaRMS shift slice (step s, layer l, attention / cross-attention / MLP) into
+// bf16 hi / lo: one lane per (sample, 8-column group).
+template <class S>
+__device__ __forceinline__ void split_shifts(Ctx<S>& c) {
+  CP& p = c.p;
+  const int ngrp = p.n_steps * p.L * 3 * p.B * (S::H / 8);
+  for (int k0 = c.wg * NTHREADS + c.tid; k0 < ngrp; k0 += c.G * NTHREADS * 4) {
+    float v[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = min(k0 + u * c.G * NTHREADS, ngrp - 1);
+      const int grp = k % (S::H / 8), r = k / (S::H / 8), b = r % p.B, r2 = r / p.B, kind = r2 % 3, sl = r2 / 3;
+      const int l = sl % p.L, s = sl / p.L;
+      const float* src = c.modrow(b, s) + 9 * l * S::H + 3 * kind * S::H + S::H + 8 * grp;
+      const f32x4 a0 = ldf4(src), a1 = ldf4(src + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { v[u][j] = a0[j]; v[u][4 + j] = a1[j]; }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = k0 + u * c.G * NTHREADS;
+      if (k < ngrp) {
+        bf16x8 hi, lo;
+        split8(v[u], hi, lo);
+        st_sc1(p.shs, (uint32_t)(k * 32), __builtin_bit_cast(u32x4, hi));
+        st_sc1(p.shs, (uint32_t)(k * 32 + 16), __builtin_bit_cast(u32x4, lo));
+      }
     }
   }
 }
@@ -1207,11 +1246,12 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   } else if (t < d.ntask) {
     dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
     MKX_TRW(c, 9);
-    const bool two = d.kind == K_RES || d.kind == K_SPLIT;  // gate and the next AdaRMS scale
-    for (int b = 0; b < p.B; ++b) {
-      const float* mr = c.modrow(b, d.s);
-      dma_f32(c, mb + b * (two ? 2 : 1) * S::H * 4, mr + d.mod_off, S::H);
-      if (two) dma_f32(c, mb + (b * 2 + 1) * S::H * 4, mr + d.mod_off2, S::H);
+    if (d.kind == K_RES || d.kind == K_SPLIT) {  // gate and the next AdaRMS scale
+      for (int b = 0; b < p.B; ++b) {
+        const float* mr = c.modrow(b, d.s);
+        dma_f32(c, mb + b * 2 * S::H * 4, mr + d.mod_off, S::H);
+        dma_f32(c, mb + (b * 2 + 1) * S::H * 4, mr + d.mod_off2, S::H);
+      }
     }
   }
 }
@@ -1271,7 +1311,10 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       else if (cur.st == ST_CA) ca_stage(c, cur, s_ks);
       else if (cur.st == ST_TAIL) tail_stage(c, cur);
       else gemm_stage(c, cur);
-      if (g == 0) transpose_caches(c, s_ks);
+      if (g == 0) {
+        transpose_caches(c, s_ks);
+        split_shifts(c);
+      }
     }
     // barrier; the next stage's constant operands are DMA'd while it completes
     c.ep = (unsigned)g;
