@@ -260,12 +260,15 @@ __device__ __forceinline__ void sts16(char* p, u32x4 v) { *reinterpret_cast<u32x
 __device__ __forceinline__ bf16x8 ldsfrag(const char* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
+// SiLU, or GELU with the tanh approximation (tanh u = 1 - 2 / (exp(2u) + 1)); hardware exp and reciprocal
 __device__ __forceinline__ float act_fn(float x, int gelu) {
   if (gelu) {
     const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-    return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
+    const float u = k0 * (x + k1 * x * x * x);
+    const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * u) + 1.0f);
+    return 0.5f * x * (1.0f + th);
   }
-  return x / (1.0f + __expf(-x));
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -394,10 +397,10 @@ __device__ __forceinline__ uint32_t ss_slot(int row, int t, int HT) {
 // residual epilogue of one 4-column piece: h = res + v * gate; stores h, y = h (1 + next scale) and the
 // piece's share of the row's sum of squares (lanes L, L^16, L^32, L^48 hold one row's 16 columns)
 template <class S>
-__device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, int row, int col, int L, f32x4 v) {
+__device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, int row, int col, int L, f32x4 v, f32x4 res) {
   const uint32_t off = fpiece(row, col, c.RT);
   const float* ml = mods_lds(c, c.sample_of(row), 2 * S::H);
-  const f32x4 h = as_f4(ld16((const char*)d.res + off)) + v * ldf4(ml + col);
+  const f32x4 h = res + v * ldf4(ml + col);
   st_sc1(d.out, off, as_u4(h));
   st_split4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)));
   float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
@@ -410,26 +413,52 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
 // qmode 1 = cross-attention query). Stores the row's share of the head's sum of squares (lanes L, L^16,
 // L^32, L^48 hold the task's 32 columns) and u = rope(x (1 + w)) split (src/mk_expert.py:175-193; the RMS
 // factor is applied to the scores).
+// The epilogue's constant operands of one (row, 4-column) item, loaded with the activations: RoPE cos/sin of
+// columns d0 and d0 + 32 and the norm weights (q/k tasks), or the residual piece (residual stages).
+struct EpiPre {
+  f32x4 c0, s0, c1, s1;
+  uint2 w0, w1;
+};
+
 template <class S>
-__device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int hd, int j, int row, int L, f32x4 xa, f32x4 xb) {
+__device__ __forceinline__ EpiPre epi_preload(Ctx<S>& c, const Desc& d, int kind, int j, int tile, int row, int L) {
+  CP& p = c.p;
+  EpiPre e;
+  if (d.kind == K_RES) {
+    e.c0 = as_f4(ld16((const char*)d.res + fpiece(row, tile * 16 + 4 * (L >> 4), c.RT)));
+  } else if (d.kind == K_QKV && kind < 2) {
+    const int d0 = 16 * j + 4 * (L >> 4);
+    const bf16_t* nw = (d.qmode ? p.qcan : kind == 0 ? p.qn : p.kn) + d.l * HD;
+    e.w0 = *reinterpret_cast<const uint2*>(nw + d0);
+    e.w1 = *reinterpret_cast<const uint2*>(nw + d0 + 32);
+    const int pos = min(row - c.sample_of(row) * p.Mqp, p.Mq - 1);
+    const float* cs = (d.qmode ? p.ca_cos : p.sa_cos) + pos * HD + d0;
+    const float* sn = (d.qmode ? p.ca_sin : p.sa_sin) + pos * HD + d0;
+    e.c0 = ldf4(cs);
+    e.s0 = ldf4(sn);
+    e.c1 = ldf4(cs + 32);
+    e.s1 = ldf4(sn + 32);
+  }
+  return e;
+}
+
+template <class S>
+__device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int hd, int j, int row, int L, f32x4 xa, f32x4 xb,
+                                         const EpiPre& e) {
   CP& p = c.p;
   float ss = xa[0] * xa[0] + xa[1] * xa[1] + xa[2] * xa[2] + xa[3] * xa[3] + xb[0] * xb[0] + xb[1] * xb[1] + xb[2] * xb[2] + xb[3] * xb[3];
   ss += __shfl_xor(ss, 16);
   ss += __shfl_xor(ss, 32);
   if (L < 16) st_sc1_b32(d.ssout, (uint32_t)((((long long)(kind * S::NH + hd) * 2 + j) * p.NRP + row) * 4), __float_as_uint(ss));
   const int d0 = 16 * j + 4 * (L >> 4);
-  const bf16_t* nw = (d.qmode ? p.qcan : kind == 0 ? p.qn : p.kn) + d.l * HD;
-  const uint2 wa = *reinterpret_cast<const uint2*>(nw + d0), wb = *reinterpret_cast<const uint2*>(nw + d0 + 32);
+  const uint2 wa = e.w0, wb = e.w1;
   const f32x4 ga = {1.0f + __uint_as_float(wa.x << 16), 1.0f + __uint_as_float(wa.x & 0xffff0000u),
                     1.0f + __uint_as_float(wa.y << 16), 1.0f + __uint_as_float(wa.y & 0xffff0000u)};
   const f32x4 gb = {1.0f + __uint_as_float(wb.x << 16), 1.0f + __uint_as_float(wb.x & 0xffff0000u),
                     1.0f + __uint_as_float(wb.y << 16), 1.0f + __uint_as_float(wb.y & 0xffff0000u)};
-  const int pos = min(row - c.sample_of(row) * p.Mqp, p.Mq - 1);
-  const float* cs = (d.qmode ? p.ca_cos : p.sa_cos) + pos * HD + d0;
-  const float* sn = (d.qmode ? p.ca_sin : p.sa_sin) + pos * HD + d0;
   const f32x4 za = xa * ga, zb = xb * gb;
-  const f32x4 ua = za * ldf4(cs) - zb * ldf4(sn);
-  const f32x4 ub = zb * ldf4(cs + 32) + za * ldf4(sn + 32);
+  const f32x4 ua = za * e.c0 - zb * e.s0;
+  const f32x4 ub = zb * e.c1 + za * e.s1;
   float* buf = kind == 0 ? d.out : d.yout;
   st_split4(buf, spiece(row, hd * HD + d0, c.RT), ua);
   st_split4(buf, spiece(row, hd * HD + d0 + 32, c.RT), ub);
@@ -486,6 +515,8 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
 #pragma unroll
         for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
       }
+      const int ert = c.tid >> 6, eL = c.tid & 63;
+      const EpiPre epre = epi_preload(c, d, qkind, qj, tile, (rt0 + min(ert, nrt - 1)) * 16 + (eL & 15), eL);
       wait_vm0();  // activations, and the staged weights and modulation slices, have landed
       __syncthreads();
       MKX_TR(c, 1);
@@ -596,7 +627,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
           } else if (d.kind == K_SPLIT) {
             st_sc1(d.part, (uint32_t)((((split * d.tiles + tile) * RT + rt0 + rt) * 64 + L) * 16), as_u4(v));
           } else if (d.kind == K_RES) {
-            res_piece(c, d, tile, row, col, L, v);
+            res_piece(c, d, tile, row, col, L, v, epre.c0);
           } else {
             const int r = rt * 16 + (L & 15);
             const float tot = ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r];
@@ -609,7 +640,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
               for (int j = 0; j < 4; ++j) v[j] = act_fn(v[j], p.act) * u[j];
               st_split4(d.out, spiece(row, col, RT), v);
             } else {
-              qk_piece(c, d, qkind, qhd, qj, row, L, v, u);
+              qk_piece(c, d, qkind, qhd, qj, row, L, v, u, epre);
             }
           }
         }
@@ -638,7 +669,8 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
           f32x4 v = as_f4(xp[0]);
 #pragma unroll
           for (int j = 1; j < S::SK; ++j) v += as_f4(xp[j]);
-          res_piece(c, d, tile, rtg * 16 + (L & 15), tile * 16 + 4 * (L >> 4), L, v);
+          const int row = rtg * 16 + (L & 15);
+          res_piece(c, d, tile, row, tile * 16 + 4 * (L >> 4), L, v, as_f4(ld16((const char*)d.res + fpiece(row, tile * 16 + 4 * (L >> 4), RT))));
         }
         MKX_TR(c, 7);
       }
