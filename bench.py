@@ -124,12 +124,12 @@ def main() -> int:
         torch.cuda.synchronize()
         ts = mk.barrier_timestamps()[: mk.barriers(n_euler) + 1].tolist()
         d = [(b - a) / 1e3 for a, b in zip(ts[1:-1], ts[2:])]
-        names = ["qkv", "sa_attn", "sa_o", "ca_q", "ca_attn", "ca_o", "gate_up", "down"]
-        per_step = 8 * cfg.L + 1
+        names = ["qkv", "sa_attn", "sa_o", "ca_attn", "ca_o", "gate_up", "down"]
+        per_step = 7 * cfg.L + 1
         buckets = {k: [] for k in names + ["tail"]}
         for i, v in enumerate(d):
             j = i % per_step
-            buckets["tail" if j == per_step - 1 else names[j % 8]].append(v)
+            buckets["tail" if j == per_step - 1 else names[j % 7]].append(v)
         print(json.dumps({"stage_us_median": {k: round(statistics.median(v), 3) for k, v in buckets.items() if v},
                           "stage_us_sum_ms": {k: round(sum(v) / 1e3, 4) for k, v in buckets.items() if v},
                           "first_tail_us": round((ts[1] - ts[0]) / 1e3, 3)}), file=sys.stderr)

@@ -224,7 +224,7 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   };
   pack(w->wqkv, h->wqkv, 3 * H, H, 3LL * H * H, H / 32, 0, 1);
   pack(w->wo, h->wo, H, H, (long long)H * H, H / 32, 0, 0);
-  pack(w->wqca, h->wqca, H, H, (long long)H * H, H / 32, 0, 1);
+  pack(w->wqca, h->wqca, H, H, (long long)H * H, H / 32, 0, 0);
   pack(w->woca, h->woca, H, H, (long long)H * H, H / 32, 0, 0);
   pack(w->wg, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), 0, 0);
   pack(w->wu, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), H / 32, 0);
@@ -257,7 +257,7 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
 
 int64_t mkx_barriers(const mkx_handle* h, int32_t n_steps) {
   if (!h || n_steps < 0) return -1;
-  return 1 + (int64_t)n_steps * (8 * h->d.L + 1);
+  return 1 + (int64_t)n_steps * (mkx::STAGES_PER_LAYER * h->d.L + 1);
 }
 
 int mkx_set_profile(mkx_handle* h, int64_t* buf, int32_t len) {
@@ -301,9 +301,9 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   // V^T (hi + lo, 32-key blocks, at most 128 rows) and the wave-merge area in the 88 KB activation region;
   // the GEMM stages stage every sample's modulation slices (2 H floats) in 56 KB.
   if ((long long)a->B * 2 * H * 4 > 56 * 1024) return fail(MKX_EUNSUPPORTED, "batch too large to stage its modulation slices in LDS");
-  if (h->profile && 1 + a->n_steps * (8LL * L + 1) + 1 > h->prof_len) return fail(MKX_EINVAL, "profile buffer shorter than barriers + 1");
+  if (h->profile && mkx_barriers(h, a->n_steps) + 1 > h->prof_len) return fail(MKX_EINVAL, "profile buffer shorter than barriers + 1");
 #ifdef MKX_TRACE
-  if (h->profile && mkx::TRACE_BASE + (2 + a->n_steps * (8LL * L + 1)) * h->G * mkx::TRACE_SLOTS > h->prof_len)
+  if (h->profile && mkx::TRACE_BASE + (1 + mkx_barriers(h, a->n_steps)) * h->G * mkx::TRACE_SLOTS > h->prof_len)
     return fail(MKX_EINVAL, "trace buffer too short");
 #endif
   // scratch: one frame per (step, layer), one step area per step; grown on demand

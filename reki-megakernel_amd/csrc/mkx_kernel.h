@@ -1,9 +1,10 @@
 // The persistent megakernel: Euler steps of the flow-matching action expert in one launch.
 //
-// Schedule (mirrors expert_megakernel, src/mk_expert.py:302-426): an in-projection tail, then for each
-// step and layer eight stages (QKV, self-attention, out-proj + gated residual, cross-attention query,
-// cross-attention, out-proj + gated residual, gate/up, down + gated residual) and a step tail. Every stage
-// is followed by one grid barrier: 1 + n_steps * (8 L + 1) barriers.
+// Schedule (the stage math of expert_megakernel, src/mk_expert.py:302-426): an in-projection tail, then for
+// each step and layer seven stages (QKV, self-attention, out-proj + gated residual, cross-attention with its
+// own query projection, out-proj + gated residual, gate/up, down + gated residual) and a step tail. Every
+// stage is followed by one grid barrier: 1 + n_steps * (7 L + 1) barriers (the reference runs the
+// cross-attention query projection as a stage of its own: 8 L + 1).
 //
 // Code layout: the kernel is one flat loop over stages, and each kind of stage (GEMM, self-attention,
 // cross-attention, tail) is a single inlined body driven by a runtime descriptor. The whole loop stays
@@ -30,13 +31,14 @@
 // its output split; the residual stages write h (fp32, for the next residual add), y = h * (1 + scale) of
 // the next AdaRMS (split) and per-tile partial sums of squares of h; the AdaRMS GEMM then computes
 // rstd(h) * (y W^T) + shift W^T (src/mk_expert.py:93-122 rearranged), with shift W^T taken by the MFMA as
-// one extra row tile of per-sample shift rows. The QKV and cross-attention query projections are computed
-// per (head, d-quarter pair) so their epilogue holds d and d + 32 of a row: it applies the q/k norm weight
-// and RoPE and writes the attention operands split (V directly in the transposed P V layout), leaving only
-// the per-row RMS factor, which attention folds into the scores. The kernel therefore reproduces the fp32 eager expert (not the bf16
-// rounding points of the reference's Triton kernel, src/mk_expert.py:119, 169-172, 220): a bf16-activation
-// kernel sits at the bf16 rounding-noise floor of the model (~1.5e-3 mean |delta| at full depth), which
-// is most of the 2e-3 parity budget.
+// one extra row tile of per-sample shift rows. The QKV projection is computed per (head, d-quarter pair)
+// so its epilogue holds d and d + 32 of a row: it applies the q/k norm weight and RoPE and writes the
+// attention operands split (V directly in the transposed P V layout), leaving only the per-row RMS factor,
+// which attention folds into the scores. The cross-attention query is projected inside the cross-attention
+// stage, where a workgroup holds whole head rows. The kernel therefore reproduces the fp32 eager expert
+// (not the bf16 rounding points of the reference's Triton kernel, src/mk_expert.py:119, 169-172, 220): a
+// bf16-activation kernel sits at the bf16 rounding-noise floor of the model (~1.5e-3 mean |delta| at full
+// depth), which is most of the 2e-3 parity budget.
 #pragma once
 #include "mkx_device.h"
 
@@ -100,8 +102,8 @@ struct Shape {
   static_assert(LDS <= 160 * 1024 - 256, "LDS budget");
   // frame layout (bytes), buffers of NRP rows; HB = NRP * H * 4:
   //   qs, ks: split q / k (roped, not normed) | vt: split V^T blocks per (sample, head) (2 HB) | ysa split |
-  //   h2 fp32 | y2 split | qcas split | yca split | h3 fp32 | y3 split | g split (I columns) | hl fp32 |
-  //   yl split | part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ssca [NH][2][NRP] | ss2, ss3, ssl [NRP][HT]
+  //   h2 fp32 | y2 split | yca split | h3 fp32 | y3 split | g split (I columns) | hl fp32 | yl split |
+  //   part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ss2, ss3, ssl [NRP][HT]
   // (sums of squares of h per 16-column tile t, at row * HT + (t % 4) * HT / 4 + t / 4: wave w of a consumer
   // reads its tiles w + 4 i as one contiguous run)
   __host__ __device__ static long long hb(int nrp) { return (long long)nrp * H * 4; }
@@ -111,17 +113,15 @@ struct Shape {
   __host__ __device__ static long long ysa_off(int nrp) { return 4 * hb(nrp); }
   __host__ __device__ static long long h2_off(int nrp) { return 5 * hb(nrp); }
   __host__ __device__ static long long y2_off(int nrp) { return 6 * hb(nrp); }
-  __host__ __device__ static long long qcas_off(int nrp) { return 7 * hb(nrp); }
-  __host__ __device__ static long long yca_off(int nrp) { return 8 * hb(nrp); }
-  __host__ __device__ static long long h3_off(int nrp) { return 9 * hb(nrp); }
-  __host__ __device__ static long long y3_off(int nrp) { return 10 * hb(nrp); }
-  __host__ __device__ static long long g_off(int nrp) { return 11 * hb(nrp); }
-  __host__ __device__ static long long hl_off(int nrp) { return (11 + SK) * hb(nrp); }
-  __host__ __device__ static long long yl_off(int nrp) { return (12 + SK) * hb(nrp); }
-  __host__ __device__ static long long part_off(int nrp) { return (13 + SK) * hb(nrp); }
-  __host__ __device__ static long long ssqk_off(int nrp) { return (13 + 2 * SK) * hb(nrp); }
-  __host__ __device__ static long long ssca_off(int nrp) { return ssqk_off(nrp) + 4LL * NH * nrp * 4; }
-  __host__ __device__ static long long ss2_off(int nrp) { return ssca_off(nrp) + 2LL * NH * nrp * 4; }
+  __host__ __device__ static long long yca_off(int nrp) { return 7 * hb(nrp); }
+  __host__ __device__ static long long h3_off(int nrp) { return 8 * hb(nrp); }
+  __host__ __device__ static long long y3_off(int nrp) { return 9 * hb(nrp); }
+  __host__ __device__ static long long g_off(int nrp) { return 10 * hb(nrp); }
+  __host__ __device__ static long long hl_off(int nrp) { return (10 + SK) * hb(nrp); }
+  __host__ __device__ static long long yl_off(int nrp) { return (11 + SK) * hb(nrp); }
+  __host__ __device__ static long long part_off(int nrp) { return (12 + SK) * hb(nrp); }
+  __host__ __device__ static long long ssqk_off(int nrp) { return (12 + 2 * SK) * hb(nrp); }
+  __host__ __device__ static long long ss2_off(int nrp) { return ssqk_off(nrp) + 4LL * NH * nrp * 4; }
   __host__ __device__ static long long ss3_off(int nrp) { return ss2_off(nrp) + (long long)HT * nrp * 4; }
   __host__ __device__ static long long ssl_off(int nrp) { return ss3_off(nrp) + (long long)HT * nrp * 4; }
   __host__ __device__ static long long frame_bytes(int nrp) { return ssl_off(nrp) + (long long)HT * nrp * 4; }
@@ -138,7 +138,8 @@ __host__ __device__ __forceinline__ uint32_t spiece(int r, int c, int RT) {
   return (uint32_t)(((c >> 5) * RT + (r >> 4)) * 2048 + ((r & 15) + 16 * ((c & 31) >> 3)) * 16 + (c & 4) * 2);
 }
 
-enum Stage { ST_QKV = 0, ST_SA, ST_O, ST_CAQ, ST_CA, ST_CAO, ST_GU, ST_DOWN, ST_TAIL };
+enum Stage { ST_QKV = 0, ST_SA, ST_O, ST_CA, ST_CAO, ST_GU, ST_DOWN, ST_TAIL };
+constexpr int STAGES_PER_LAYER = 7;
 enum { K_QKV = 0, K_RES = 1, K_GU = 2, K_SPLIT = 3 };
 
 // Optional per-workgroup phase trace (diagnostic builds with MKX_TRACE): clock of phase `slot` of the
@@ -295,7 +296,6 @@ struct Desc {
   float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
   const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][NRP]
   int ntask, tiles, kind, nt;
-  int qmode;                           // K_QKV: 0 = self-attention q/k/v, 1 = cross-attention query
   const char* shs;                     // AdaRMS stages: the split shift fragments of this step and layer
   // staged modulation slices (H floats each, per sample): AdaRMS stages: shift; residual stages: gate, then
   // the scale of the next AdaRMS
@@ -310,18 +310,18 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
   d.last = false;
   d.w = nullptr; d.wstride = 0; d.a = nullptr; d.out = nullptr; d.res = nullptr; d.part = nullptr;
   d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr; d.shs = nullptr;
-  d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.qmode = 0; d.mod_off = 0; d.mod_off2 = 0;
+  d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.mod_off = 0; d.mod_off2 = 0;
   if (g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
-  const int per_step = 8 * p.L + 1;
+  const int per_step = STAGES_PER_LAYER * p.L + 1;
   const int h = g - 1;
   d.s = h / per_step;
   const int j = h - d.s * per_step;
-  if (j == 8 * p.L) {
+  if (j == STAGES_PER_LAYER * p.L) {
     d.st = ST_TAIL; d.l = p.L - 1; d.last = d.s + 1 == p.n_steps;
     return d;
   }
-  d.l = j >> 3;
-  d.st = j & 7;
+  d.l = j / STAGES_PER_LAYER;
+  d.st = j - d.l * STAGES_PER_LAYER;
   const int NRP = p.NRP, l = d.l;
   char* fr = c.frame(d.s, l);
   // AdaRMS slices of a layer's mods row (src/mk_expert.py:302-426): [scale | shift | gate] for self-attention,
@@ -339,12 +339,6 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
       d.w = p.wo + l * p.s_o; d.a = (const float*)(fr + S::ysa_off(NRP)); d.out = (float*)(fr + S::h2_off(NRP));
       d.yout = (float*)(fr + S::y2_off(NRP)); d.ssout = (float*)(fr + S::ss2_off(NRP));
       d.res = c.h_in(d.s, l); d.ntask = d.tiles = S::HT; d.kind = K_RES; d.mod_off = m_sa + 2 * S::H; d.mod_off2 = m_ca;
-      break;
-    case ST_CAQ:
-      d.w = p.wqca + l * p.s_o; d.wstride = 2LL * S::NKB * 512; d.a = (const float*)(fr + S::y2_off(NRP));
-      d.ssin = (const float*)(fr + S::ss2_off(NRP)); d.out = (float*)(fr + S::qcas_off(NRP));
-      d.ssout = (float*)(fr + S::ssca_off(NRP)); d.ntask = d.tiles = 2 * S::NH; d.nt = 2; d.qmode = 1;
-      d.shs = shs + p.B * S::H * 4;
       break;
     case ST_CAO:
       d.w = p.woca + l * p.s_o; d.a = (const float*)(fr + S::yca_off(NRP)); d.out = (float*)(fr + S::h3_off(NRP));
@@ -379,7 +373,7 @@ __device__ __forceinline__ const bf16_t* wtile(const Desc& d, int t) {
 // GEMM stage: out tile (16 columns, all rows) of A @ W^T for each task of this workgroup, computed
 // transposed (D^T = W_tile A^T) so that each lane's accumulator is 4 consecutive output columns of one row:
 // one 16-byte piece of the fragment-major output. A is a split operand frame (hi and lo both multiplied).
-//   AdaRMS stages (K_QKV: q/k/v, cross-attention query; K_GU): A = y = h * (1 + scale) was written by the
+//   AdaRMS stages (K_QKV: q/k/v; K_GU): A = y = h * (1 + scale) was written by the
 //     producer of h, so out = rstd(h) * (y W^T) + shift W^T (src/mk_expert.py:93-122); rstd comes from the
 //     producer's per-tile sums of squares, shift W^T from an extra MFMA row tile whose rows are the
 //     samples' shift slices. K_QKV: see qk_piece / the V^T epilogue; K_GU stores act(gate) * up split
@@ -409,8 +403,8 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
   if (L < 16) st_sc1_b32(d.ssout, ss_slot(row, tile, S::HT), __float_as_uint(ss));
 }
 
-// q/k epilogue of one row: xa, xb = columns d0 .. d0+3 and d0+32 .. d0+35 of head hd (kind 0 = q, 1 = k;
-// qmode 1 = cross-attention query). Stores the row's share of the head's sum of squares (lanes L, L^16,
+// q/k epilogue of one row: xa, xb = columns d0 .. d0+3 and d0+32 .. d0+35 of head hd (kind 0 = q, 1 = k).
+// Stores the row's share of the head's sum of squares (lanes L, L^16,
 // L^32, L^48 hold the task's 32 columns) and u = rope(x (1 + w)) split (src/mk_expert.py:175-193; the RMS
 // factor is applied to the scores).
 // The epilogue's constant operands of one (row, 4-column) item, loaded with the activations: RoPE cos/sin of
@@ -428,12 +422,12 @@ __device__ __forceinline__ EpiPre epi_preload(Ctx<S>& c, const Desc& d, int kind
     e.c0 = as_f4(ld16((const char*)d.res + fpiece(row, tile * 16 + 4 * (L >> 4), c.RT)));
   } else if (d.kind == K_QKV && kind < 2) {
     const int d0 = 16 * j + 4 * (L >> 4);
-    const bf16_t* nw = (d.qmode ? p.qcan : kind == 0 ? p.qn : p.kn) + d.l * HD;
+    const bf16_t* nw = (kind == 0 ? p.qn : p.kn) + d.l * HD;
     e.w0 = *reinterpret_cast<const uint2*>(nw + d0);
     e.w1 = *reinterpret_cast<const uint2*>(nw + d0 + 32);
     const int pos = min(row - c.sample_of(row) * p.Mqp, p.Mq - 1);
-    const float* cs = (d.qmode ? p.ca_cos : p.sa_cos) + pos * HD + d0;
-    const float* sn = (d.qmode ? p.ca_sin : p.sa_sin) + pos * HD + d0;
+    const float* cs = p.sa_cos + pos * HD + d0;
+    const float* sn = p.sa_sin + pos * HD + d0;
     e.c0 = ldf4(cs);
     e.s0 = ldf4(sn);
     e.c1 = ldf4(cs + 32);
@@ -1038,14 +1032,19 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
   }
 }
 
-// Cross-attention: K and V^T of the source rows streamed in chunks of 128 rows through a 4-slot LDS ring
-// (32 KB per slot: 16 K chunks, then 16 V^T chunks from the per-launch copy); the first four chunks are
-// DMA'd during the barrier. Wave w takes the chunk's 32-row block w (src/mk_expert.py:225-251). The query
-// rows arrive split and un-normalised from the query projection.
+// Cross-attention stage: task (sample b, head hd, 16-query tile qt).
+//  1. Query projection of the tile's rows for the head (src/mk_expert.py:373-378): q = rstd(h2) (y2 Wq^T) +
+//     shift Wq^T over the head's 64 columns (y2 = h2 (1 + scale) split, rows of the tile; the shift row
+//     tile as in the GEMM stages), then, with whole head rows in the workgroup, the q norm, its weight and
+//     RoPE (:175-193), split into the Q chunks.
+//  2. Attention over the valid source rows (:225-251): K and V^T streamed in chunks of 128 rows through a
+//     3-slot LDS ring (32 KB per slot: 16 K chunks, then 16 V^T chunks from the per-launch copy); the first
+//     three chunks are DMA'd during the barrier. Wave w takes each chunk's 32-row block w; the waves'
+//     softmax states are merged at the end.
 template <class S>
 __device__ __forceinline__ char* ca_slot(Ctx<S>& c, int cc) {
-  const int sl = cc & 3;
-  return c.smem + (sl < 2 ? S::WBUF + sl * 32768 : S::ABUF + (sl - 2) * 32768);
+  const int sl = cc % 3;
+  return c.smem + (sl < 2 ? S::WBUF + sl * 32768 : S::ABUF);
 }
 
 template <class S>
@@ -1070,32 +1069,28 @@ __device__ __forceinline__ void ca_dma_chunk(Ctx<S>& c, int l, int b, int hd, in
 template <class S>
 __device__ __forceinline__ void ca_prefetch(Ctx<S>& c, int l, int b, int hd, int S_len) {
   const int nch = (S_len + 127) / 128;
-  for (int cc = 0; cc < min(nch, 4); ++cc) ca_dma_chunk(c, l, b, hd, cc, S_len);
-}
-
-// waits until at most n ring chunks (8 DMA instructions per wave each) are outstanding
-__device__ __forceinline__ void wait_vm_chunks(int n) {
-  switch (n) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-  }
+  for (int cc = 0; cc < min(nch, 3); ++cc) ca_dma_chunk(c, l, b, hd, cc, S_len);
 }
 
 template <class S>
 __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
+  constexpr int KPW = S::KPW;
   const int Mqp = p.Mqp, NQT = Mqp / 16, NRP = p.NRP, RT = c.RT;
   const int l = d.l;
   char* fr = c.frame(d.s, l);
-  const char* qcas = fr + S::qcas_off(NRP);
-  const float* ssca = (const float*)(fr + S::ssca_off(NRP));
+  const float* y2 = (const float*)(fr + S::y2_off(NRP));
+  const float* ss2 = (const float*)(fr + S::ss2_off(NRP));
   float* yca = (float*)(fr + S::yca_off(NRP));
+  const bf16_t* wq = p.wqca + l * p.s_o;
+  const char* shs = p.shs + ((long long)(d.s * p.L + l) * 3 + 1) * p.B * S::H * 4;
+  char* red = c.smem + S::ABUF + 32768;  // [wave][4 column tiles][q, shift][64 lanes] x 16 bytes
   char* Qh = c.smem + S::ABUF + 65536;
   char* Ql = Qh + 2048;
   float* mrg = (float*)(Ql + 2048);
+  float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
   const int NHB = p.B * S::NH;
+  const uint32_t vlane = (uint32_t)c.lane * 16;
   for (int v = c.wg; v < attn_vcount(NQT, NHB); v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
@@ -1107,34 +1102,128 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       __syncthreads();
       ca_prefetch(c, l, b, hd, S_len);
     }
-    const int rt0 = b * Mqp / 16;
-    if (c.wave == 0) {
+    const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
+    // 1a. operands: y2 fragments of the query rows, Wq fragments of the head's 4 column tiles, the shift
+    //     fragments (rows = samples), sums of squares; and for step 1b this lane's RoPE / norm constants
+    bf16x8 yh[KPW], ylo[KPW], sh_h[KPW], sh_l[KPW], wf[4][KPW];
+    u32x4 ssv[S::HT / 16];
+    {
+      const __amdgpu_buffer_rsrc_t ry = rsrc(y2);
+      const __amdgpu_buffer_rsrc_t rsh =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(shs), (short)0, p.B * S::H * 4, 0x00020000);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int db = k >> 1, part = k & 1;
-        dma16(qcas + ((long long)((2 * hd + db) * RT + rt0 + qt) * 2 + part) * 1024 + c.lane * 16, (part ? Ql : Qh) + db * 1024);
+      for (int i = 0; i < KPW; ++i) {
+        const int kb = c.wave + NWAVES * i;
+        const uint32_t blk = (uint32_t)((kb * RT + rq) * 2048);
+        yh[i] = __builtin_bit_cast(bf16x8, bload(ry, vlane, blk));
+        ylo[i] = __builtin_bit_cast(bf16x8, bload(ry, vlane, blk + 1024));
+        const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + kb) * 4 + (c.lane >> 4)) * 32);
+        sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
+        sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          wf[nt][i] = __builtin_bit_cast(bf16x8, ld16(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * 512 + c.lane * 8));
+      }
+      const __amdgpu_buffer_rsrc_t rs_ = rsrc(ss2);
+      const uint32_t so = (uint32_t)(((rq * 16 + (c.lane & 15)) * S::HT + c.wave * (S::HT / 4)) * 4);
+#pragma unroll
+      for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
+    }
+    // step 1b item of this lane: row r = 4 wave + lane / 16 of the tile, columns 4 cg .. 4 cg + 3 of the head
+    const int r = 4 * c.wave + (c.lane >> 4), cg = c.lane & 15;
+    const int pos = min(qt * 16 + r, p.Mq - 1);
+    const f32x4 cs = ldf4(p.ca_cos + pos * HD + 4 * cg), sn = ldf4(p.ca_sin + pos * HD + 4 * cg);
+    const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
+    wait_vm0();  // the prefetched chunks and the query operands have landed
+    {
+      float ssp = 0.f;
+#pragma unroll
+      for (int i = 0; i < S::HT / 16; ++i) {
+        const f32x4 x = as_f4(ssv[i]);
+        ssp += (x[0] + x[1]) + (x[2] + x[3]);
+      }
+      if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
+      f32x4 acc[4], accb[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = accb[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KPW; ++i)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          acc[nt] = mfma16(wf[nt][i], yh[i], acc[nt]);
+          acc[nt] = mfma16(wf[nt][i], ylo[i], acc[nt]);
+          accb[nt] = mfma16(wf[nt][i], sh_h[i], accb[nt]);
+          accb[nt] = mfma16(wf[nt][i], sh_l[i], accb[nt]);
+        }
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        sts16(red + (((c.wave * 4 + nt) * 2 + 0) * 64 + c.lane) * 16, as_u4(acc[nt]));
+        sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 64 + c.lane) * 16, as_u4(accb[nt]));
       }
     }
-    const int q = qt * 16 + (c.lane & 15);
-    const float ssq = ssca[(long long)(hd * 2) * NRP + b * Mqp + q] + ssca[(long long)(hd * 2 + 1) * NRP + b * Mqp + q];
-    wait_vm0();  // the prefetched chunks and the query tile have landed
+    __syncthreads();
+    {
+      // 1b. q of row r, columns 4 cg .. 4 cg + 3 (accumulator lane r + 16 (cg % 4) of column tile cg / 4)
+      const int nt = cg >> 2, lr = r + 16 * (cg & 3), lb = b + 16 * (cg & 3);
+      f32x4 qv = {0.f, 0.f, 0.f, 0.f};
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < NWAVES; ++w) {
+        qv += ldf4((const float*)(red + (((w * 4 + nt) * 2 + 0) * 64 + lr) * 16));
+        const f32x4 bb = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 64 + lb) * 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] += bb[e];
+      }
+      const float rs = rsqrtf((ssw[r] + ssw[16 + r] + ssw[32 + r] + ssw[48 + r]) / (float)S::H + p.eps);
+      f32x4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = qv[e] * rs + bv[e];
+      // q norm over the head's 64 columns (the 16 lanes of the row), weight 1 + w, rotate-half RoPE with the
+      // partner column d +- 32 on lane ^ 8
+      float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+      ss += __shfl_xor(ss, 1);
+      ss += __shfl_xor(ss, 2);
+      ss += __shfl_xor(ss, 4);
+      ss += __shfl_xor(ss, 8);
+      const float rn = rsqrtf(ss / 64.f + p.qk_eps);
+      const f32x4 gw = {1.0f + __uint_as_float(wn.x << 16), 1.0f + __uint_as_float(wn.x & 0xffff0000u),
+                        1.0f + __uint_as_float(wn.y << 16), 1.0f + __uint_as_float(wn.y & 0xffff0000u)};
+      const f32x4 xn = x * rn * gw;
+      const float sgn = cg < 8 ? -1.0f : 1.0f;
+      f32x4 u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) u[e] = xn[e] * cs[e] + sgn * __shfl_xor(xn[e], 8) * sn[e];
+      // Q chunk layout (row r, d = 4 cg): lane r + 16 ((d % 32) / 8), half (d % 8) / 4
+      const int dd = 4 * cg;
+      const int off = (dd >> 5) * 1024 + (r + 16 * ((dd & 31) >> 3)) * 16 + (dd & 4) * 2;
+      u32x2 hi, lo;
+      hi[0] = cvt_pk(u[0], u[1]);
+      hi[1] = cvt_pk(u[2], u[3]);
+      lo[0] = cvt_pk(u[0] - __uint_as_float(hi[0] << 16), u[1] - __uint_as_float(hi[0] & 0xffff0000u));
+      lo[1] = cvt_pk(u[2] - __uint_as_float(hi[1] << 16), u[3] - __uint_as_float(hi[1] & 0xffff0000u));
+      *reinterpret_cast<u32x2*>(Qh + off) = hi;
+      *reinterpret_cast<u32x2*>(Ql + off) = lo;
+    }
     __syncthreads();
     MKX_TR(c, 1);
     AttnState A;
     attn_begin(A, Qh, Ql, c.lane);
-    const float qsc = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
     for (int cc = 0; cc < nch; ++cc) {
-      if (cc >= 4) {
-        wait_vm_chunks(min(nch - 1 - cc, 3));
+      if (cc >= 3) {
+        // chunk cc was issued three iterations ago; the younger chunks cc + 1, cc + 2 (8 DMAs per wave
+        // each) may still be in flight
+        if (cc + 2 < nch) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (cc + 1 < nch) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else wait_vm0();
         __syncthreads();
       }
       char* slot = ca_slot(c, cc);
       const int k0 = cc * 128 + c.wave * 32;
       if (k0 < S_len)
-        attn_block(A, c.lane, slot + c.wave * 4096, nullptr, slot + 16384 + c.wave * 4096, nullptr, 0, S_len - k0, qsc, nullptr);
-      if (cc + 4 < nch) {
+        attn_block(A, c.lane, slot + c.wave * 4096, nullptr, slot + 16384 + c.wave * 4096, nullptr, 0, S_len - k0, p.sm_scale, nullptr);
+      if (cc + 3 < nch) {
         __syncthreads();
-        ca_dma_chunk(c, l, b, hd, cc + 4, S_len);
+        ca_dma_chunk(c, l, b, hd, cc + 3, S_len);
       }
     }
     MKX_TR(c, 2);
@@ -1328,7 +1417,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   __syncthreads();
   if (p.profile && c.wg == 0 && c.tid == 0) p.prof[0] = clock100() * 10;
 
-  const int total = 1 + p.n_steps * (8 * p.L + 1);
+  const int total = 1 + p.n_steps * (STAGES_PER_LAYER * p.L + 1);
   Desc cur = describe(c, 0);
   for (int g = 0; g < total; ++g) {
     {
