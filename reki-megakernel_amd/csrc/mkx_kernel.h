@@ -290,12 +290,13 @@ struct Desc {
   int st, s, l;
   bool first, last;
   // GEMM stages
-  const bf16_t* w; long long wstride;  // packed weight chunks; task t's tile at w + t * wstride (not split)
+  const bf16_t* w; long long wstride;  // packed weight chunks; tile t at w + t * wstride (not split)
   const float* a;                      // split operand frame
   float* out; const float* res; float* part;
   float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
   const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][NRP]
   int ntask, tiles, kind, nt;
+  int rgs;                             // row groups: task t = tile t % tiles over row-tile group t / tiles
   const char* shs;                     // AdaRMS stages: the split shift fragments of this step and layer
   // staged modulation slices (H floats each, per sample): AdaRMS stages: shift; residual stages: gate, then
   // the scale of the next AdaRMS
@@ -310,7 +311,7 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
   d.last = false;
   d.w = nullptr; d.wstride = 0; d.a = nullptr; d.out = nullptr; d.res = nullptr; d.part = nullptr;
   d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr; d.shs = nullptr;
-  d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.mod_off = 0; d.mod_off2 = 0;
+  d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.mod_off = 0; d.mod_off2 = 0; d.rgs = 1;
   if (g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
   const int per_step = STAGES_PER_LAYER * p.L + 1;
   const int h = g - 1;
@@ -360,13 +361,19 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
     default:
       break;
   }
+  if (d.st == ST_QKV || d.st == ST_O || d.st == ST_CAO) {
+    // as many row groups as idle workgroups allow: a task then loads only its rows of the operand (the
+    // operand rows are the stage's critical-path load; the weight tile is prefetched)
+    d.rgs = max(1, min(c.RT, c.G / d.tiles));
+    d.ntask = d.tiles * d.rgs;
+  }
   return d;
 }
 
 template <class S>
 __device__ __forceinline__ const bf16_t* wtile(const Desc& d, int t) {
   if (d.kind == K_SPLIT) return d.w + ((long long)(t % d.tiles) * S::SK + t / d.tiles) * S::NKB * 512;
-  return d.w + (long long)t * d.wstride;
+  return d.w + (long long)(t % d.tiles) * d.wstride;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -458,6 +465,114 @@ __device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int
   st_split4(buf, spiece(row, hd * HD + d0 + 32, c.RT), ub);
 }
 
+// MFMAs of one pass: acc[rt][nt][hi/lo] over this wave's k-blocks; the hi and lo products accumulate
+// separately and consecutive MFMAs target different accumulators, so none waits on its predecessor.
+// SWAP (V tasks): D = A W^T; otherwise D^T = W A^T. ADA adds the shift row tile acc[NRT] (always D^T).
+template <class S, int NRT, int NT, bool SWAP, bool ADA>
+__device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][2][2], const bf16x8 (&ah)[NRT][S::KPW],
+                                         const bf16x8 (&al)[NRT][S::KPW], const bf16x8 (&sh_h)[S::KPW],
+                                         const bf16x8 (&sh_l)[S::KPW], const char* wl, int wave) {
+#pragma unroll
+  for (int i = 0; i < S::KPW; ++i) {
+    const int kb = wave + NWAVES * i;
+    bf16x8 wf[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) wf[nt] = ldsfrag(wl + (nt * S::NKB + kb) * 1024);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+          const bf16x8 a = h ? al[rt][i] : ah[rt][i];
+          acc[rt][nt][h] = SWAP ? mfma16(a, wf[nt], acc[rt][nt][h]) : mfma16(wf[nt], a, acc[rt][nt][h]);
+        }
+    if (ADA) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        acc[NRT][nt][0] = mfma16(wf[nt], sh_h[i], acc[NRT][nt][0]);
+        acc[NRT][nt][1] = mfma16(wf[nt], sh_l[i], acc[NRT][nt][1]);
+      }
+    }
+  }
+}
+
+// One pass of a GEMM task over row tiles rt0 .. rt0 + NRT - 1: operand loads (and, for AdaRMS stages, the
+// shift fragments and sums of squares), the epilogue's preloaded constants, the MFMAs, and the per-wave
+// partial tiles written to the cross-wave reduction buffer.
+template <class S, int NRT>
+__device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int kb0, bool vtask, int qkind, int qj,
+                                          int tile, EpiPre& epre) {
+  constexpr int KPW = S::KPW, RB = S::RBMAX;
+  CP& p = c.p;
+  const int RT = c.RT, NRP = p.NRP;
+  const bool ada = d.kind == K_QKV || d.kind == K_GU;
+  const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
+  const uint32_t vlane = (uint32_t)c.lane * 16;
+  float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
+  char* red = c.smem + S::RED;                // [wave][RB + 1][2][64 lanes] x 16 bytes
+  bf16x8 ah[NRT][KPW], al[NRT][KPW];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const uint32_t blk = (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048);
+      ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
+      al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
+    }
+  bf16x8 sh_h[KPW], sh_l[KPW];  // the split shift fragments of this wave's k-blocks (rows = samples)
+  u32x4 ssv[S::HT / 16];  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
+  if (ada) {
+    // lane l reads sample l % 16; the samples >= B fall outside the buffer and read zeros
+    const __amdgpu_buffer_rsrc_t rsh =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(d.shs), (short)0, p.B * S::H * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + c.wave + NWAVES * i) * 4 + (c.lane >> 4)) * 32);
+      sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
+      sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
+    }
+    const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
+    const uint32_t so = (uint32_t)((min(rt0 * 16 + c.lane, NRP - 1) * S::HT + c.wave * (S::HT / 4)) * 4);
+#pragma unroll
+    for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
+  } else {
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) sh_h[i] = sh_l[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  const int ert = c.tid >> 6, eL = c.tid & 63;
+  epre = epi_preload(c, d, qkind, qj, tile, (rt0 + min(ert, NRT - 1)) * 16 + (eL & 15), eL);
+  wait_vm0();  // activations, and the staged weights and modulation slices, have landed
+  __syncthreads();
+  MKX_TR(c, 1);
+  if (ada) {
+    float ssp = 0.f;
+#pragma unroll
+    for (int i = 0; i < S::HT / 16; ++i) {
+      const f32x4 x = as_f4(ssv[i]);
+      ssp += (x[0] + x[1]) + (x[2] + x[3]);
+    }
+    ssw[c.wave * 64 + c.lane] = ssp;
+  }
+  f32x4 acc[NRT + 1][2][2];
+#pragma unroll
+  for (int rt = 0; rt <= NRT; ++rt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[rt][nt][0] = acc[rt][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const char* wl = c.smem + S::WBUF + c.lane * 16;
+  if (vtask) gemm_mma<S, NRT, 2, true, true>(acc, ah, al, sh_h, sh_l, wl, c.wave);
+  else if (d.nt == 2) gemm_mma<S, NRT, 2, false, true>(acc, ah, al, sh_h, sh_l, wl, c.wave);
+  else gemm_mma<S, NRT, 1, false, false>(acc, ah, al, sh_h, sh_l, wl, c.wave);
+  // cross-wave reduction through LDS (the shift tile at slot RB)
+#pragma unroll
+  for (int rt = 0; rt <= NRT; ++rt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+      if (nt < d.nt && (rt < NRT || ada))
+        sts16(red + (((c.wave * (RB + 1) + (rt < NRT ? rt : RB)) * 2 + nt) * 64 + c.lane) * 16,
+              as_u4(acc[rt][nt][0] + acc[rt][nt][1]));
+}
+
 template <class S>
 __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
   constexpr int KPW = S::KPW, RB = S::RBMAX;
@@ -469,116 +584,25 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
   char* red = c.smem + S::RED;                // [wave][RB + 1][2][64 lanes] x 16 bytes
   for (int t = c.wg; t < d.ntask; t += c.G) {
-    const int tile = t % d.tiles, split = t / d.tiles;
-    // QKV tasks: kind (q, k, v), head, quarter pair j; v is computed untransposed (D = A W^T) so that each
+    const int tile = t % d.tiles, split = t / d.tiles;  // split: K quarter (K_SPLIT) or row group
+    // QKV tiles: kind (q, k, v), head, quarter pair j; v is computed untransposed (D = A W^T) so that each
     // lane holds 4 consecutive keys of one d: 8 bytes of the V^T layout
-    const int qkind = d.kind == K_QKV ? t / (2 * S::NH) : 0, qhd = (t >> 1) % S::NH, qj = t & 1;
+    const int qkind = d.kind == K_QKV ? tile / (2 * S::NH) : 0, qhd = (tile >> 1) % S::NH, qj = tile & 1;
     const bool vtask = qkind == 2;
     if (t != c.wg) {  // later tasks of this workgroup: load their weights now (the first was prefetched)
       wait_vm0();
       __syncthreads();
       dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
     }
-    const int kb0 = split * S::NKB;
-    for (int rt0 = 0; rt0 < RT; rt0 += RB) {
-      const int nrt = min(RB, RT - rt0);
-      bf16x8 ah[RB][KPW], al[RB][KPW];
-      // row tiles beyond the pass repeat its last tile: every load is unconditional (one batch)
-#pragma unroll
-      for (int rt = 0; rt < RB; ++rt)
-#pragma unroll
-        for (int i = 0; i < KPW; ++i) {
-          const uint32_t blk = (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + min(rt, nrt - 1)) * 2048);
-          ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
-          al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
-        }
-      bf16x8 sh_h[KPW], sh_l[KPW];  // the split shift fragments of this wave's k-blocks (rows = samples)
-      u32x4 ssv[S::HT / 16];  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
-      if (ada) {
-        // lane l reads sample l % 16; the samples >= B fall outside the buffer and read zeros
-        const __amdgpu_buffer_rsrc_t rsh =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(d.shs), (short)0, p.B * S::H * 4, 0x00020000);
-#pragma unroll
-        for (int i = 0; i < KPW; ++i) {
-          const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + c.wave + NWAVES * i) * 4 + (c.lane >> 4)) * 32);
-          sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
-          sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
-        }
-        const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
-        const uint32_t so = (uint32_t)((min(rt0 * 16 + c.lane, NRP - 1) * S::HT + c.wave * (S::HT / 4)) * 4);
-#pragma unroll
-        for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
-      }
-      const int ert = c.tid >> 6, eL = c.tid & 63;
-      const EpiPre epre = epi_preload(c, d, qkind, qj, tile, (rt0 + min(ert, nrt - 1)) * 16 + (eL & 15), eL);
-      wait_vm0();  // activations, and the staged weights and modulation slices, have landed
-      __syncthreads();
-      MKX_TR(c, 1);
-      if (ada) {
-        float ssp = 0.f;
-#pragma unroll
-        for (int i = 0; i < S::HT / 16; ++i) {
-          const f32x4 x = as_f4(ssv[i]);
-          ssp += (x[0] + x[1]) + (x[2] + x[3]);
-        }
-        ssw[c.wave * 64 + c.lane] = ssp;
-      }
-      f32x4 acc[RB + 1][2];
-#pragma unroll
-      for (int rt = 0; rt <= RB; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (vtask) {
-#pragma unroll
-        for (int i = 0; i < KPW; ++i) {
-          const int kb = c.wave + NWAVES * i;
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            const bf16x8 wf = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
-#pragma unroll
-            for (int rt = 0; rt < RB; ++rt) {
-              acc[rt][nt] = mfma16(ah[rt][i], wf, acc[rt][nt]);
-              acc[rt][nt] = mfma16(al[rt][i], wf, acc[rt][nt]);
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < KPW; ++i) {
-          const int kb = c.wave + NWAVES * i;
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            if (nt < d.nt) {
-              const bf16x8 wf = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
-#pragma unroll
-              for (int rt = 0; rt < RB; ++rt) {
-                acc[rt][nt] = mfma16(wf, ah[rt][i], acc[rt][nt]);
-                acc[rt][nt] = mfma16(wf, al[rt][i], acc[rt][nt]);
-              }
-            }
-          }
-        }
-      }
-      if (ada) {
-        // shift W^T: row tile whose row b is sample b's shift slice (rows >= B are zero)
-#pragma unroll
-        for (int i = 0; i < KPW; ++i) {
-          const int kb = c.wave + NWAVES * i;
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            if (nt < d.nt) {
-              const bf16x8 wf = ldsfrag(c.smem + S::WBUF + (nt * S::NKB + kb) * 1024 + c.lane * 16);
-              acc[RB][nt] = mfma16(wf, sh_h[i], acc[RB][nt]);
-              acc[RB][nt] = mfma16(wf, sh_l[i], acc[RB][nt]);
-            }
-          }
-        }
-      }
-      // cross-wave reduction through LDS
-#pragma unroll
-      for (int rt = 0; rt <= RB; ++rt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          if (nt < d.nt && (rt < nrt || (rt == RB && ada)))
-            sts16(red + (((c.wave * (RB + 1) + rt) * 2 + nt) * 64 + c.lane) * 16, as_u4(acc[rt][nt]));
+    const int kb0 = d.kind == K_SPLIT ? split * S::NKB : 0;
+    const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
+    const int rt_hi = d.kind == K_SPLIT ? RT : (split + 1) * RT / d.rgs;
+    for (int rt0 = rt_lo; rt0 < rt_hi; rt0 += RB) {
+      const int nrt = min(RB, rt_hi - rt0);
+      EpiPre epre;
+      if (nrt == 1) gemm_pass<S, 1>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+      else if (nrt == 2 || RB == 2) gemm_pass<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+      else gemm_pass<S, RB>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
       __syncthreads();
       MKX_TR(c, 2);
       // epilogue: one (row tile, lane) item per thread: row (rt0 + rt) * 16 + L % 16, columns tile*16 + 4 (L / 16) + 0..3
@@ -1237,25 +1261,54 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 // h0' = x'_real Win + bin (action rows), register tokens (register rows), all fp32; with h0' its layer-0
 // AdaRMS operand y0' = h0' (1 + scale) (split) and sums of squares. Tasks [0, H/16):
 // in-projection tiles (each recomputes the velocity of the real action dims); tasks [H/16, H/16 + A):
-// one output dim each. One wave per action row; lane owns the 4-column pieces 4 (lane + 64 q).
-// The final modulation rows and Wout's real-dim rows were staged in LDS by the prefetch.
+// one output dim each. Wave w takes the action rows w + 4 k, TAIL_RPW of them per batch with their loads
+// issued together; lane owns the 4-column pieces 4 (lane + 64 q). The final modulation rows and Wout's
+// real-dim rows were staged in LDS by the prefetch; the in-projection's constant operands (Win tile, bias,
+// register tokens, layer-0 scale) are loaded with the first batch.
+constexpr int TAIL_RPW = 3;  // action rows per wave and batch
+constexpr int TAIL_AC = 8;   // action dims reduced together
+
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float* v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], o);
+}
+
 template <class S>
 __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
   CP& p = c.p;
   constexpr int NP = S::H / 256;  // pieces per lane
+  constexpr int R = TAIL_RPW;
   const int nin = d.last ? 0 : S::HT;
   const int nout = d.first ? 0 : p.A;
   const int nrows = p.B * p.T;
   const int adim = p.action_dim;
   const float* xcur = (d.first || d.s == 0) ? p.x_in : c.xstep(d.s);
   const float* hL = d.first ? p.x_in : (const float*)(c.frame(d.s, p.L - 1) + S::hl_off(p.NRP));
-  float* xp = (float*)(c.smem + S::ABUF);           // [nrows][adim] x' of the real dims
+  float* xp = (float*)(c.smem + S::ABUF);                // [nrows][adim] x' of the real dims
   const float* wo_l = (const float*)(c.smem + S::WBUF);  // Wout rows [adim][H]
-  float* win_t = (float*)(c.smem + S::SMALL);        // Win tile [adim][16]
+  float* win_t = (float*)(c.smem + S::SMALL);            // Win tile [adim][16]
+  const int sn = d.first ? 0 : d.s + 1;
   for (int t = c.wg; t < nin + nout; t += c.G) {
     __syncthreads();
     const bool inproj = t < nin;
     const int a_out = t - nin;
+    // in-projection item of this thread (first pass): row, 4-column piece q of tile t; its constant operands
+    const int row0 = c.tid >> 2, q0 = c.tid & 3;
+    f32x4 sc0 = {0.f, 0.f, 0.f, 0.f}, bv0 = {0.f, 0.f, 0.f, 0.f};
+    uint2 rg0 = {0u, 0u};
+    f32x4 wt = {0.f, 0.f, 0.f, 0.f};
+    if (inproj) {
+      const int b = row0 / p.Mqp, i = row0 - b * p.Mqp, col = t * 16 + 4 * q0;
+      if (row0 < p.NRP) {
+        sc0 = ldf4(c.modrow(min(b, p.B - 1), sn) + col);  // layer 0 self-attention AdaRMS scale
+        if (b < p.B && i < p.T) bv0 = ldf4(p.bin + col);
+        else if (b < p.B && i < p.Mq) rg0 = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
+      }
+      if (c.tid < adim * 4) wt = ldf4(p.win + (long long)(c.tid >> 2) * S::H + t * 16 + 4 * (c.tid & 3));
+    }
     if (!d.first) {
       f32x4 wa[NP];
       if (!inproj) {
@@ -1263,42 +1316,93 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
         for (int q = 0; q < NP; ++q) wa[q] = ldf4(p.wout + (long long)a_out * S::H + 4 * (c.lane + 64 * q));
       }
       const __amdgpu_buffer_rsrc_t rh = rsrc(hL);
-      for (int ri = c.wave; ri < nrows; ri += NWAVES) {
-        const int b = ri / p.T, i = ri - b * p.T;
-        const int grow = b * p.Mqp + i;
-        f32x4 x[NP];
+      // lane a < A holds bout[a]; with xc[k] below (x of row k, dim lane) the in-projection's x' is formed by
+      // the lanes of its dims
+      const float bo = p.bout[min(c.lane, p.A - 1)];
+      for (int r0 = c.wave; r0 < nrows; r0 += NWAVES * R) {
+        f32x4 x[R][NP];
+        float xc[R];
 #pragma unroll
-        for (int q = 0; q < NP; ++q) x[q] = as_f4(bload(rh, fpiece(grow, 4 * (c.lane + 64 * q), c.RT), 0));
-        float ss = 0.f;
+        for (int k = 0; k < R; ++k) {
+          const int ri = min(r0 + NWAVES * k, nrows - 1);
+          const int b = ri / p.T, grow = b * p.Mqp + (ri - b * p.T);
 #pragma unroll
-        for (int q = 0; q < NP; ++q) ss += x[q][0] * x[q][0] + x[q][1] * x[q][1] + x[q][2] * x[q][2] + x[q][3] * x[q][3];
-        const float rs = rsqrtf(wave_sum(ss) / (float)S::H + p.eps);
-        const float* ml = mods_lds(c, b, 2 * S::H);
+          for (int q = 0; q < NP; ++q) x[k][q] = as_f4(bload(rh, fpiece(grow, 4 * (c.lane + 64 * q), c.RT), 0));
+          xc[k] = xcur[(long long)ri * p.A + (inproj ? min(c.lane, p.A - 1) : a_out)];
+        }
+        float ss[R];
 #pragma unroll
-        for (int q = 0; q < NP; ++q) {
-          const int col = 4 * (c.lane + 64 * q);
-          x[q] = x[q] * rs * (1.0f + ldf4(ml + col)) + ldf4(ml + S::H + col);
+        for (int k = 0; k < R; ++k) {
+          ss[k] = 0.f;
+#pragma unroll
+          for (int q = 0; q < NP; ++q) ss[k] += x[k][q][0] * x[k][q][0] + x[k][q][1] * x[k][q][1] + x[k][q][2] * x[k][q][2] + x[k][q][3] * x[k][q][3];
+        }
+        wave_sum_n<R>(ss);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+          const int ri = min(r0 + NWAVES * k, nrows - 1);
+          const float rs = rsqrtf(ss[k] / (float)S::H + p.eps);
+          const float* ml = mods_lds(c, ri / p.T, 2 * S::H);
+#pragma unroll
+          for (int q = 0; q < NP; ++q) {
+            const int col = 4 * (c.lane + 64 * q);
+            x[k][q] = x[k][q] * rs * (1.0f + ldf4(ml + col)) + ldf4(ml + S::H + col);
+          }
         }
         if (inproj) {
-          for (int a = 0; a < adim; ++a) {
-            float dd = 0.f;
+          for (int a0 = 0; a0 < adim; a0 += TAIL_AC) {
+            float dd[TAIL_AC * R];
 #pragma unroll
-            for (int q = 0; q < NP; ++q) {
-              const f32x4 w = ldf4(wo_l + a * S::H + 4 * (c.lane + 64 * q));
-              dd += x[q][0] * w[0] + x[q][1] * w[1] + x[q][2] * w[2] + x[q][3] * w[3];
+            for (int j = 0; j < TAIL_AC; ++j) {
+              const int a = min(a0 + j, adim - 1);
+#pragma unroll
+              for (int k = 0; k < R; ++k) dd[j * R + k] = 0.f;
+#pragma unroll
+              for (int q = 0; q < NP; ++q) {
+                const f32x4 w = ldf4(wo_l + a * S::H + 4 * (c.lane + 64 * q));
+#pragma unroll
+                for (int k = 0; k < R; ++k)
+                  dd[j * R + k] += x[k][q][0] * w[0] + x[k][q][1] * w[1] + x[k][q][2] * w[2] + x[k][q][3] * w[3];
+              }
             }
-            dd = wave_sum(dd);
-            if (c.lane == 0) xp[ri * adim + a] = xcur[(long long)ri * p.A + a] + c.dt * (dd + p.bout[a]);
+            wave_sum_n<TAIL_AC * R>(dd);
+            float sel[R];
+#pragma unroll
+            for (int k = 0; k < R; ++k) sel[k] = 0.f;
+#pragma unroll
+            for (int j = 0; j < TAIL_AC; ++j)
+              if (c.lane == a0 + j) {
+#pragma unroll
+                for (int k = 0; k < R; ++k) sel[k] = dd[j * R + k];
+              }
+            if (c.lane >= a0 && c.lane < min(a0 + TAIL_AC, adim)) {
+#pragma unroll
+              for (int k = 0; k < R; ++k) {
+                const int ri = r0 + NWAVES * k;
+                if (ri < nrows) xp[ri * adim + c.lane] = xc[k] + c.dt * (sel[k] + bo);
+              }
+            }
           }
         } else {
-          float dd = 0.f;
+          float dd[R];
 #pragma unroll
-          for (int q = 0; q < NP; ++q) dd += x[q][0] * wa[q][0] + x[q][1] * wa[q][1] + x[q][2] * wa[q][2] + x[q][3] * wa[q][3];
-          dd = wave_sum(dd);
+          for (int k = 0; k < R; ++k) {
+            dd[k] = 0.f;
+#pragma unroll
+            for (int q = 0; q < NP; ++q)
+              dd[k] += x[k][q][0] * wa[q][0] + x[k][q][1] * wa[q][1] + x[k][q][2] * wa[q][2] + x[k][q][3] * wa[q][3];
+          }
+          wave_sum_n<R>(dd);
           if (c.lane == 0) {
             float* xn = d.last ? p.x_out : c.xstep(d.s + 1);
-            const float xa = a_out < adim ? xcur[(long long)ri * p.A + a_out] : 0.f;
-            st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + a_out) * 4), __float_as_uint(xa + c.dt * (dd + p.bout[a_out])));
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+              const int ri = r0 + NWAVES * k;
+              if (ri < nrows) {
+                const float xa = a_out < adim ? xc[k] : 0.f;
+                st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + a_out) * 4), __float_as_uint(xa + c.dt * (dd[k] + p.bout[a_out])));
+              }
+            }
           }
         }
       }
@@ -1309,28 +1413,33 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
       }
     }
     if (inproj) {
-      if (c.tid < adim * 4) {
-        const int a = c.tid >> 2, q = c.tid & 3;
-        *reinterpret_cast<f32x4*>(win_t + a * 16 + 4 * q) = ldf4(p.win + (long long)a * S::H + t * 16 + 4 * q);
-      }
+      if (c.tid < adim * 4) *reinterpret_cast<f32x4*>(win_t + (c.tid >> 2) * 16 + 4 * (c.tid & 3)) = wt;
       __syncthreads();
       MKX_TR(c, 1);
-      const int sn = d.first ? 0 : d.s + 1;
       float* h0n = c.h0(sn);
       for (int it = c.tid; it < p.NRP * 4; it += NTHREADS) {
         const int row = it >> 2, q = it & 3;
         const int b = row / p.Mqp, i = row - b * p.Mqp;
         const int col = t * 16 + 4 * q;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 sc = ldf4(c.modrow(min(b, p.B - 1), sn) + col);  // layer 0 self-attention AdaRMS scale
+        f32x4 v, sc;
+        uint2 rg;
+        if (it == c.tid) {
+          v = bv0;
+          sc = sc0;
+          rg = rg0;
+        } else {
+          v = f32x4{0.f, 0.f, 0.f, 0.f};
+          rg = uint2{0u, 0u};
+          sc = ldf4(c.modrow(min(b, p.B - 1), sn) + col);
+          if (b < p.B && i < p.T) v = ldf4(p.bin + col);
+          else if (b < p.B && i < p.Mq) rg = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
+        }
         if (b < p.B && i < p.T) {
-          v = ldf4(p.bin + col);
           const float* xr = xp + (b * p.T + i) * adim;
           for (int a = 0; a < adim; ++a) v += xr[a] * ldf4(win_t + a * 16 + 4 * q);
         } else if (b < p.B && i < p.Mq) {
-          const uint2 r = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
-          v = f32x4{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
-                    __uint_as_float(r.y & 0xffff0000u)};
+          v = f32x4{__uint_as_float(rg.x << 16), __uint_as_float(rg.x & 0xffff0000u), __uint_as_float(rg.y << 16),
+                    __uint_as_float(rg.y & 0xffff0000u)};
         }
         st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
         st_split4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc));
