@@ -90,6 +90,41 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Cross-lane sums and maxima in registers (no LDS round trip): DPP within a 16-lane row, the gfx950
+// permlane swaps across rows. Each step adds a lane's value and its partner's, so both partners (and, at the
+// end, all lanes of the group) hold bitwise the same result.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_xor8(float v) { return dpp<0x128>(v); }  // row_ror:8 = lane ^ 8 within a row
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp<0xB1>(v);  // quad_perm [1, 0, 3, 2]: lane ^ 1
+  return v + dpp<0x4E>(v);  // quad_perm [2, 3, 0, 1]: lane ^ 2
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v = quad_sum(v);
+  v += dpp<0x141>(v);  // row_half_mirror: a lane of the other quad of the half-row (quads are uniform)
+  return v + dpp<0x140>(v);  // row_mirror: a lane of the other half-row
+}
+__device__ __forceinline__ float xor16_sum(float v) {  // v[l] + v[l ^ 16]
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {  // v[l] + v[l ^ 32]
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float wave_sum(float v) { return xor32_sum(xor16_sum(row_sum16(v))); }
+
 // ---------------------------------------------------------------------------------------------
 // grid barrier state (device memory, zeroed at handle creation)
 struct BarState {

@@ -271,11 +271,6 @@ __device__ __forceinline__ float act_fn(float x, int gelu) {
   }
   return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
 
 // staged per-sample modulation slice: AdaRMS stages hold [scale | shift] (2H), gated-residual stages hold gate (H)
 template <class S>
@@ -405,8 +400,7 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
   st_sc1(d.out, off, as_u4(h));
   st_split4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)));
   float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
-  ss += __shfl_xor(ss, 16);
-  ss += __shfl_xor(ss, 32);
+  ss = xor32_sum(xor16_sum(ss));
   if (L < 16) st_sc1_b32(d.ssout, ss_slot(row, tile, S::HT), __float_as_uint(ss));
 }
 
@@ -448,8 +442,7 @@ __device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int
                                          const EpiPre& e) {
   CP& p = c.p;
   float ss = xa[0] * xa[0] + xa[1] * xa[1] + xa[2] * xa[2] + xa[3] * xa[3] + xb[0] * xb[0] + xb[1] * xb[1] + xb[2] * xb[2] + xb[3] * xb[3];
-  ss += __shfl_xor(ss, 16);
-  ss += __shfl_xor(ss, 32);
+  ss = xor32_sum(xor16_sum(ss));
   if (L < 16) st_sc1_b32(d.ssout, (uint32_t)((((long long)(kind * S::NH + hd) * 2 + j) * p.NRP + row) * 4), __float_as_uint(ss));
   const int d0 = 16 * j + 4 * (L >> 4);
   const uint2 wa = e.w0, wb = e.w1;
@@ -627,7 +620,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int r = rt * 16 + 4 * (L >> 4) + e;
-              rs[e] = rsqrtf((ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r]) / (float)S::H + p.eps);
+              rs[e] = rsqrtf((ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r]) * (1.0f / (float)S::H) + p.eps);
             }
             const uint32_t vo = (uint32_t)(((b * S::NH + qhd) * KBO + (ib >> 5)) * 8192 + L * 16 + ((ib >> 4) & 1) * 8);
 #pragma unroll
@@ -649,7 +642,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
           } else {
             const int r = rt * 16 + (L & 15);
             const float tot = ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r];
-            const float rs = rsqrtf(tot / (float)S::H + p.eps);
+            const float rs = rsqrtf(tot * (1.0f / (float)S::H) + p.eps);
             const int bl = c.sample_of(row) + 16 * (L >> 4);
             v = v * rs + wsum(RB, 0, bl);
             const f32x4 u = wsum(rt, 1, L) * rs + wsum(RB, 1, bl);
@@ -749,8 +742,7 @@ __device__ __forceinline__ void attn_block(AttnState& A, int lane, const char* K
     pv[j] = s[j >> 2][j & 3] * sc + ((key >= klo && key < khi) ? 0.f : -INFINITY);
     mb = fmaxf(mb, pv[j]);
   }
-  mb = fmaxf(mb, __shfl_xor(mb, 16));
-  mb = fmaxf(mb, __shfl_xor(mb, 32));
+  mb = xor32_max(xor16_max(mb));
   const float mn = fmaxf(A.m, mb);
   const float mu = mn == -INFINITY ? 0.f : mn;
   const float alpha = __expf(A.m - mu);
@@ -788,32 +780,34 @@ __device__ __forceinline__ void attn_begin(AttnState& A, const char* Qh, const c
 }
 
 // merges the 4 waves' states (mrg: 18 KB of LDS) and stores the tile's output rows of head hd of sample b
-// (split, written through; query rows >= M get zeros). Wave w finishes the 16-d slice dt = w.
+// (split, written through; query rows >= M get zeros). Wave w finishes the 16-d slice dt = w. The states are
+// exchanged lane-contiguously ([wave][dt][lane] accumulators, [wave][lane] maxima and denominators), so no
+// LDS access has bank conflicts.
 template <class S>
 __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float* mrg, float* y, int b, int hd, int qt) {
-  float* me = mrg + (c.wave * 64 + c.lane) * 18;
-  me[0] = A.m;
-  me[1] = A.den;
+  f32x4* macc = reinterpret_cast<f32x4*>(mrg);  // [4 waves][4 dt][64 lanes]
+  float* mm = mrg + NWAVES * 4 * 64 * 4;         // [4 waves][64 lanes]
+  float* md = mm + NWAVES * 64;                  // [4 waves][64 lanes]
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4*>(me + 2 + 4 * dt) = A.acc[dt];
+  for (int dt = 0; dt < 4; ++dt) macc[(c.wave * 4 + dt) * 64 + c.lane] = A.acc[dt];
+  mm[c.wave * 64 + c.lane] = A.m;
+  md[c.wave * 64 + c.lane] = A.den;
   __syncthreads();
   float mw[NWAVES], M = -INFINITY;
 #pragma unroll
   for (int w = 0; w < NWAVES; ++w) {
-    mw[w] = mrg[(w * 64 + c.lane) * 18];
+    mw[w] = mm[w * 64 + c.lane];
     M = fmaxf(M, mw[w]);
   }
   float den = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 0; w < NWAVES; ++w) {
-    const float* o = mrg + (w * 64 + c.lane) * 18;
     const float f = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - M);
-    den += o[1] * f;
-    acc += ldf4(o + 2 + 4 * c.wave) * f;
+    den += md[w * 64 + c.lane] * f;
+    acc += macc[(w * 4 + c.wave) * 64 + c.lane] * f;
   }
-  den += __shfl_xor(den, 16);
-  den += __shfl_xor(den, 32);
+  den = xor32_sum(xor16_sum(den));
   const int q = qt * 16 + (c.lane & 15);
   const f32x4 out = (den > 0.f && q < c.p.Mq) ? acc * (1.0f / den) : f32x4{0.f, 0.f, 0.f, 0.f};
   st_split4(y, spiece(b * c.p.Mqp + q, hd * HD + c.wave * 16 + 4 * (c.lane >> 4), c.RT), out);
@@ -1077,14 +1071,17 @@ __device__ __forceinline__ void ca_dma_chunk(Ctx<S>& c, int l, int b, int hd, in
   const bf16_t* kb_ = c.p.kca[l] + (long long)b * c.p.src_sb;
   const int ncb = c.p.SPP / 32;
   const bf16_t* vt = c.p.cavt + ((long long)(l * c.p.B + b) * S::NH + hd) * ncb * 2048;
+  // 32-key blocks that start beyond the valid length are not loaded (no wave reads them); within a partly
+  // valid block, rows beyond the length are replaced by the last valid row (they are masked)
   for (int k = c.dw; k < 32; k += c.dn) {
     if (k < 16) {
-      // rows beyond the valid length are replaced by the last valid row (they are masked)
       const int kt = k >> 1, db = k & 1;
+      if (cc * 128 + (kt >> 1) * 32 >= S_len) continue;
       const int key = min(cc * 128 + kt * 16 + (c.lane & 15), S_len - 1);
       dma16(kb_ + ((long long)key * S::NH + hd) * HD + db * 32 + 8 * (c.lane >> 4), slot + k * 1024);
     } else {
-      const int i = k - 16, kb = min(cc * 4 + (i >> 2), ncb - 1);
+      const int i = k - 16, kb = cc * 4 + (i >> 2);
+      if (kb * 32 >= S_len) continue;
       dma16(vt + ((long long)kb * 4 + (i & 3)) * 512 + c.lane * 8, slot + 16384 + i * 1024);
     }
   }
@@ -1108,10 +1105,13 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* yca = (float*)(fr + S::yca_off(NRP));
   const bf16_t* wq = p.wqca + l * p.s_o;
   const char* shs = p.shs + ((long long)(d.s * p.L + l) * 3 + 1) * p.B * S::H * 4;
-  char* red = c.smem + S::ABUF + 32768;  // [wave][4 column tiles][q, shift][64 lanes] x 16 bytes
-  char* Qh = c.smem + S::ABUF + 65536;
+  // [wave][4 column tiles][q, shift][68 slots] x 16 bytes: lane L at slot L + L / 16, so that the
+  // transposed reads of the finishing step fall in distinct banks
+  char* red = c.smem + S::ABUF + 32768;
+  char* Qh = c.smem + S::ABUF + 32768 + NWAVES * 4 * 2 * 68 * 16;
   char* Ql = Qh + 2048;
   float* mrg = (float*)(Ql + 2048);
+  static_assert(32768 + NWAVES * 4 * 2 * 68 * 16 + 4096 + NWAVES * 64 * 18 * 4 <= S::ABUF_BYTES, "cross-attention LDS map");
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
   const int NHB = p.B * S::NH;
   const uint32_t vlane = (uint32_t)c.lane * 16;
@@ -1159,6 +1159,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     const f32x4 cs = ldf4(p.ca_cos + pos * HD + 4 * cg), sn = ldf4(p.ca_sin + pos * HD + 4 * cg);
     const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
     wait_vm0();  // the prefetched chunks and the query operands have landed
+    MKX_TR(c, 3);
     {
       float ssp = 0.f;
 #pragma unroll
@@ -1167,25 +1168,28 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
         ssp += (x[0] + x[1]) + (x[2] + x[3]);
       }
       if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
-      f32x4 acc[4], accb[4];
+      // [column tile][q hi, q lo, shift hi, shift lo]: 16 independent accumulation chains
+      f32x4 acc[4][4];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) acc[nt] = accb[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) acc[nt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < KPW; ++i)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          acc[nt] = mfma16(wf[nt][i], yh[i], acc[nt]);
-          acc[nt] = mfma16(wf[nt][i], ylo[i], acc[nt]);
-          accb[nt] = mfma16(wf[nt][i], sh_h[i], accb[nt]);
-          accb[nt] = mfma16(wf[nt][i], sh_l[i], accb[nt]);
-        }
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt)
+            acc[nt][h] = mfma16(wf[nt][i], h == 0 ? yh[i] : h == 1 ? ylo[i] : h == 2 ? sh_h[i] : sh_l[i], acc[nt][h]);
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
-        sts16(red + (((c.wave * 4 + nt) * 2 + 0) * 64 + c.lane) * 16, as_u4(acc[nt]));
-        sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 64 + c.lane) * 16, as_u4(accb[nt]));
+        const int sl = c.lane + (c.lane >> 4);
+        sts16(red + (((c.wave * 4 + nt) * 2 + 0) * 68 + sl) * 16, as_u4(acc[nt][0] + acc[nt][1]));
+        sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 68 + sl) * 16, as_u4(acc[nt][2] + acc[nt][3]));
       }
     }
     __syncthreads();
+    MKX_TR(c, 7);
     {
       // 1b. q of row r, columns 4 cg .. 4 cg + 3 (accumulator lane r + 16 (cg % 4) of column tile cg / 4)
       const int nt = cg >> 2, lr = r + 16 * (cg & 3), lb = b + 16 * (cg & 3);
@@ -1193,22 +1197,19 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       float bv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < NWAVES; ++w) {
-        qv += ldf4((const float*)(red + (((w * 4 + nt) * 2 + 0) * 64 + lr) * 16));
-        const f32x4 bb = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 64 + lb) * 16));
+        qv += ldf4((const float*)(red + (((w * 4 + nt) * 2 + 0) * 68 + lr + (lr >> 4)) * 16));
+        const f32x4 bb = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 68 + lb + (lb >> 4)) * 16));
 #pragma unroll
         for (int e = 0; e < 4; ++e) bv[e] += bb[e];
       }
-      const float rs = rsqrtf((ssw[r] + ssw[16 + r] + ssw[32 + r] + ssw[48 + r]) / (float)S::H + p.eps);
+      const float rs = rsqrtf((ssw[r] + ssw[16 + r] + ssw[32 + r] + ssw[48 + r]) * (1.0f / (float)S::H) + p.eps);
       f32x4 x;
 #pragma unroll
       for (int e = 0; e < 4; ++e) x[e] = qv[e] * rs + bv[e];
       // q norm over the head's 64 columns (the 16 lanes of the row), weight 1 + w, rotate-half RoPE with the
       // partner column d +- 32 on lane ^ 8
       float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-      ss += __shfl_xor(ss, 1);
-      ss += __shfl_xor(ss, 2);
-      ss += __shfl_xor(ss, 4);
-      ss += __shfl_xor(ss, 8);
+      ss = row_sum16(ss);
       const float rn = rsqrtf(ss / 64.f + p.qk_eps);
       const f32x4 gw = {1.0f + __uint_as_float(wn.x << 16), 1.0f + __uint_as_float(wn.x & 0xffff0000u),
                         1.0f + __uint_as_float(wn.y << 16), 1.0f + __uint_as_float(wn.y & 0xffff0000u)};
@@ -1216,7 +1217,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       const float sgn = cg < 8 ? -1.0f : 1.0f;
       f32x4 u;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) u[e] = xn[e] * cs[e] + sgn * __shfl_xor(xn[e], 8) * sn[e];
+      for (int e = 0; e < 4; ++e) u[e] = xn[e] * cs[e] + sgn * lane_xor8(xn[e]) * sn[e];
       // Q chunk layout (row r, d = 4 cg): lane r + 16 ((d % 32) / 8), half (d % 8) / 4
       const int dd = 4 * cg;
       const int off = (dd >> 5) * 1024 + (r + 16 * ((dd & 31) >> 3)) * 16 + (dd & 4) * 2;
@@ -1234,10 +1235,10 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     attn_begin(A, Qh, Ql, c.lane);
     for (int cc = 0; cc < nch; ++cc) {
       if (cc >= 3) {
-        // chunk cc was issued three iterations ago; the younger chunks cc + 1, cc + 2 (8 DMAs per wave
-        // each) may still be in flight
-        if (cc + 2 < nch) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-        else if (cc + 1 < nch) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        // chunk cc was issued three iterations ago; the younger chunks cc + 1, cc + 2 may still be in
+        // flight: 8 DMAs per wave each, except the last chunk, which may issue fewer
+        if (cc + 2 < nch - 1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (cc + 1 < nch - 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         else wait_vm0();
         __syncthreads();
       }
@@ -1252,6 +1253,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     }
     MKX_TR(c, 2);
     attn_merge_store(c, A, mrg, yca, b, hd, qt);
+    MKX_TR(c, 13);
     __syncthreads();
   }
 }
@@ -1271,9 +1273,7 @@ constexpr int TAIL_AC = 8;   // action dims reduced together
 template <int N>
 __device__ __forceinline__ void wave_sum_n(float* v) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], o);
+  for (int i = 0; i < N; ++i) v[i] = wave_sum(v[i]);
 }
 
 template <class S>
@@ -1341,7 +1341,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
 #pragma unroll
         for (int k = 0; k < R; ++k) {
           const int ri = min(r0 + NWAVES * k, nrows - 1);
-          const float rs = rsqrtf(ss[k] / (float)S::H + p.eps);
+          const float rs = rsqrtf(ss[k] * (1.0f / (float)S::H) + p.eps);
           const float* ml = mods_lds(c, ri / p.T, 2 * S::H);
 #pragma unroll
           for (int q = 0; q < NP; ++q) {
@@ -1444,8 +1444,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
         st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
         st_split4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc));
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
+        ss = quad_sum(ss);
         if (q == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, t, S::HT), __float_as_uint(ss));
       }
     }
