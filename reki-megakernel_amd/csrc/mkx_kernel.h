@@ -813,21 +813,31 @@ __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float*
   st_split4(y, spiece(b * c.p.Mqp + q, hd * HD + c.wave * 16 + 4 * (c.lane >> 4), c.RT), out);
 }
 
-// Attention tasks: virtual workgroup v -> (sample-head hh, query tile qt), arranged so that the query
-// tiles of one head run on workgroups of one XCD (v % 8 is the XCD class) and share its L2.
+// Attention tasks: task u -> (sample-head hh, query tile qt), u in [0, nqt * nhb), run by workgroup G - 1 - u
+// (and G - 1 - u + k G): the top of the grid, which the GEMM stage before each attention stage leaves idle,
+// so the idle workgroups' prefetch of the attention operands overlaps that GEMM stage. Heads in complete
+// groups of 8 are arranged so that the query tiles of one head run on one XCD (u % 8 is the XCD class) and
+// share its L2; the remaining heads follow compactly.
 struct AttnTask {
   int hh, qt;
   bool ok;
 };
-__device__ __forceinline__ AttnTask attn_task(int v, int nqt, int nhb) {
+__device__ __forceinline__ AttnTask attn_task(int u, int nqt, int nhb) {
   AttnTask a;
-  const int k = v >> 3;
-  a.qt = k % nqt;
-  a.hh = (v & 7) + 8 * (k / nqt);
-  a.ok = a.hh < nhb;
+  const int g8 = nhb & ~7, rem = nhb - g8;
+  if (u < nqt * g8) {
+    const int k = u >> 3;
+    a.qt = k % nqt;
+    a.hh = (u & 7) + 8 * (k / nqt);
+  } else {
+    const int r = u - nqt * g8;
+    a.qt = rem ? r / rem : 0;
+    a.hh = g8 + (rem ? r % rem : 0);
+  }
+  a.ok = u >= 0 && a.qt < nqt && a.hh < nhb;
   return a;
 }
-__device__ __forceinline__ int attn_vcount(int nqt, int nhb) { return 8 * nqt * ((nhb + 7) / 8); }
+__device__ __forceinline__ int attn_count(int nqt, int nhb) { return nqt * nhb; }
 
 template <class S>
 __device__ __forceinline__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd, int kvs) {
@@ -961,12 +971,13 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* mrg = rk + 128;
   const int NHB = p.B * S::NH;
   const bool want_kv = (d.s == 0 && p.cur_k != nullptr && p.R > 0);
-  for (int v = c.wg; v < attn_vcount(NQT, NHB); v += c.G) {
+  const int u0 = c.G - 1 - c.wg;
+  for (int v = u0; v < attn_count(NQT, NHB); v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
     const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
     const int kvs = s_ks[b];
-    if (v != c.wg) {
+    if (v != u0) {
       wait_vm0();
       __syncthreads();
       sa_prefetch(c, l, b, hd, kvs);
@@ -1115,13 +1126,14 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
   const int NHB = p.B * S::NH;
   const uint32_t vlane = (uint32_t)c.lane * 16;
-  for (int v = c.wg; v < attn_vcount(NQT, NHB); v += c.G) {
+  const int u0 = c.G - 1 - c.wg;
+  for (int v = u0; v < attn_count(NQT, NHB); v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
     const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
     const int S_len = s_ks[MAX_BATCH + b];
     const int nch = (S_len + 127) / 128;
-    if (v != c.wg) {
+    if (v != u0) {
       wait_vm0();
       __syncthreads();
       ca_prefetch(c, l, b, hd, S_len);
@@ -1291,7 +1303,8 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
   const float* wo_l = (const float*)(c.smem + S::WBUF);  // Wout rows [adim][H]
   float* win_t = (float*)(c.smem + S::SMALL);            // Win tile [adim][16]
   const int sn = d.first ? 0 : d.s + 1;
-  for (int t = c.wg; t < nin + nout; t += c.G) {
+  // task t runs on workgroup G - 1 - t: the top of the grid, mostly idle in the down projection before it
+  for (int t = c.G - 1 - c.wg; t < nin + nout; t += c.G) {
     __syncthreads();
     const bool inproj = t < nin;
     const int a_out = t - nin;
@@ -1461,14 +1474,14 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   char* mb = c.smem + S::MODS;
   MKX_TRW(c, 8);
   if (d.st == ST_SA || d.st == ST_CA) {
-    const AttnTask at = attn_task(t, p.Mqp / 16, p.B * S::NH);
+    const AttnTask at = attn_task(c.G - 1 - t, p.Mqp / 16, p.B * S::NH);
     if (at.ok) {
       const int b = at.hh / S::NH, hd = at.hh % S::NH;
       if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
       else ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);
     }
   } else if (d.st == ST_TAIL) {
-    if (!d.first && t < (d.last ? 0 : S::HT) + p.A) {
+    if (!d.first && c.G - 1 - t < (d.last ? 0 : S::HT) + p.A) {
       for (int b = 0; b < p.B; ++b) dma_f32(c, mb + b * 2 * S::H * 4, c.modrow(b, d.s) + 9 * p.L * S::H, 2 * S::H);
       dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
     }
