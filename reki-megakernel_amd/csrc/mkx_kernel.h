@@ -656,7 +656,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
           }
         }
       }
-      __syncthreads();  // red and ssw are reused by the next pass
+      if (rt0 + RB < rt_hi) __syncthreads();  // red and ssw are reused by the next pass
       MKX_TR(c, 3);
     }
     if (d.kind == K_SPLIT) {
@@ -1105,7 +1105,7 @@ __device__ __forceinline__ void ca_prefetch(Ctx<S>& c, int l, int b, int hd, int
 }
 
 template <class S>
-__device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_ks) {
+__device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_ks, BarCtx& bc, int g) {
   CP& p = c.p;
   constexpr int KPW = S::KPW;
   const int Mqp = p.Mqp, NQT = Mqp / 16, NRP = p.NRP, RT = c.RT;
@@ -1126,8 +1126,32 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
   const int NHB = p.B * S::NH;
   const uint32_t vlane = (uint32_t)c.lane * 16;
-  const int u0 = c.G - 1 - c.wg;
-  for (int v = u0; v < attn_count(NQT, NHB); v += c.G) {
+  const int u0 = c.G - 1 - c.wg, cnt = attn_count(NQT, NHB);
+  // The operands that do not depend on the stage before, the Wq fragments of the task's head and the shift
+  // fragments (an MFMA row tile whose rows are the samples), are loaded before the barrier completes: the
+  // workgroups running this stage are idle in the stage before. (Loads only: the waves that do not poll the
+  // barrier reach it without waiting for them.)
+  bf16x8 wf[4][KPW], sh_h[KPW], sh_l[KPW];
+  auto pre = [&](int hd) {
+    const __amdgpu_buffer_rsrc_t rsh =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(shs), (short)0, p.B * S::H * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int kb = c.wave + NWAVES * i;
+      // lane l reads sample l % 16; samples >= B fall outside the buffer and read zeros
+      const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + kb) * 4 + (c.lane >> 4)) * 32);
+      sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
+      sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        wf[nt][i] = __builtin_bit_cast(bf16x8, ld16(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * 512 + c.lane * 8));
+    }
+  };
+  if (u0 < cnt) pre(attn_task(u0, NQT, NHB).hh % S::NH);
+  bar_wait(bc, (unsigned long long)g);
+  MKX_TR(c, 0);
+  if (p.profile && c.wg == 0 && c.tid == 0) p.prof[g] = clock100() * 10;
+  for (int v = u0; v < cnt; v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
     const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
@@ -1137,28 +1161,21 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       wait_vm0();
       __syncthreads();
       ca_prefetch(c, l, b, hd, S_len);
+      pre(hd);
     }
     const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
-    // 1a. operands: y2 fragments of the query rows, Wq fragments of the head's 4 column tiles, the shift
-    //     fragments (rows = samples), sums of squares; and for step 1b this lane's RoPE / norm constants
-    bf16x8 yh[KPW], ylo[KPW], sh_h[KPW], sh_l[KPW], wf[4][KPW];
+    // 1a. operands: y2 fragments of the query rows, sums of squares; and for step 1b this lane's RoPE / norm
+    //     constants
+    bf16x8 yh[KPW], ylo[KPW];
     u32x4 ssv[S::HT / 16];
     {
       const __amdgpu_buffer_rsrc_t ry = rsrc(y2);
-      const __amdgpu_buffer_rsrc_t rsh =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(shs), (short)0, p.B * S::H * 4, 0x00020000);
 #pragma unroll
       for (int i = 0; i < KPW; ++i) {
         const int kb = c.wave + NWAVES * i;
         const uint32_t blk = (uint32_t)((kb * RT + rq) * 2048);
         yh[i] = __builtin_bit_cast(bf16x8, bload(ry, vlane, blk));
         ylo[i] = __builtin_bit_cast(bf16x8, bload(ry, vlane, blk + 1024));
-        const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + kb) * 4 + (c.lane >> 4)) * 32);
-        sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
-        sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          wf[nt][i] = __builtin_bit_cast(bf16x8, ld16(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * 512 + c.lane * 8));
       }
       const __amdgpu_buffer_rsrc_t rs_ = rsrc(ss2);
       const uint32_t so = (uint32_t)(((rq * 16 + (c.lane & 15)) * S::HT + c.wave * (S::HT / 4)) * 4);
@@ -1170,6 +1187,16 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     const int pos = min(qt * 16 + r, p.Mq - 1);
     const f32x4 cs = ldf4(p.ca_cos + pos * HD + 4 * cg), sn = ldf4(p.ca_sin + pos * HD + 4 * cg);
     const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
+    // shift Wq^T while the query rows are in flight
+    f32x4 accb[4][2];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) accb[nt][0] = accb[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KPW; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) accb[nt][h] = mfma16(wf[nt][i], h ? sh_l[i] : sh_h[i], accb[nt][h]);
     wait_vm0();  // the prefetched chunks and the query operands have landed
     MKX_TR(c, 3);
     {
@@ -1180,24 +1207,21 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
         ssp += (x[0] + x[1]) + (x[2] + x[3]);
       }
       if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
-      // [column tile][q hi, q lo, shift hi, shift lo]: 16 independent accumulation chains
-      f32x4 acc[4][4];
+      // [column tile][hi, lo]: 8 independent accumulation chains
+      f32x4 acc[4][2];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int h = 0; h < 4; ++h) acc[nt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < 4; ++nt) acc[nt][0] = acc[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < KPW; ++i)
 #pragma unroll
-        for (int h = 0; h < 4; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int nt = 0; nt < 4; ++nt)
-            acc[nt][h] = mfma16(wf[nt][i], h == 0 ? yh[i] : h == 1 ? ylo[i] : h == 2 ? sh_h[i] : sh_l[i], acc[nt][h]);
+          for (int nt = 0; nt < 4; ++nt) acc[nt][h] = mfma16(wf[nt][i], h ? ylo[i] : yh[i], acc[nt][h]);
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const int sl = c.lane + (c.lane >> 4);
         sts16(red + (((c.wave * 4 + nt) * 2 + 0) * 68 + sl) * 16, as_u4(acc[nt][0] + acc[nt][1]));
-        sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 68 + sl) * 16, as_u4(acc[nt][2] + acc[nt][3]));
+        sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 68 + sl) * 16, as_u4(accb[nt][0] + accb[nt][1]));
       }
     }
     __syncthreads();
@@ -1550,7 +1574,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       c.dt = dt;
       c.ep = (unsigned)g;
       if (cur.st == ST_SA) sa_stage(c, cur, s_ks);
-      else if (cur.st == ST_CA) ca_stage(c, cur, s_ks);
+      else if (cur.st == ST_CA) ca_stage(c, cur, s_ks, bc, g);  // completes barrier g itself
       else if (cur.st == ST_TAIL) tail_stage(c, cur);
       else gemm_stage(c, cur);
       if (g == 0) {
@@ -1572,6 +1596,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       if (c.wave != 0) prefetch(c, cur, s_ks);
     }
     MKX_TR(c, 6);
+    if (g + 1 < total && cur.st == ST_CA) continue;
     bar_wait(bc, (unsigned long long)g + 1);
     c.ep = (unsigned)(g + 1);
     MKX_TR(c, 0);
