@@ -3,6 +3,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -108,6 +109,7 @@ struct mkx_handle {
   size_t vts_cap = 0;
   unsigned* dcnt = nullptr;
   BarState* bar = nullptr;
+  unsigned long long* flags = nullptr;  // [FLAG_KINDS][FLAG_MAX][FLAG_STRIDE] ready epochs
   long long* prof = nullptr;
   int prof_len = 0;
   int profile = 0;
@@ -120,7 +122,7 @@ struct mkx_handle {
 static void free_handle(mkx_handle* h) {
   if (!h) return;
   void* ptrs[] = {h->wqkv, h->wo, h->wqca, h->woca, h->wgu, h->wd, h->qn, h->kn, h->qcan, h->win, h->bin,
-                  h->wout, h->bout, h->frames, h->steps, h->vts, h->dcnt, h->bar};
+                  h->wout, h->bout, h->frames, h->steps, h->vts, h->dcnt, h->bar, h->flags};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete h;
@@ -249,6 +251,8 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   HCHK(hipMemsetAsync(h->dcnt, 0, (size_t)(H / 16) * 4, stream));
   HCHK(alloc((void**)&h->bar, sizeof(BarState)));
   HCHK(hipMemsetAsync(h->bar, 0, sizeof(BarState), stream));
+  HCHK(alloc((void**)&h->flags, sizeof(unsigned long long) * FLAG_KINDS * FLAG_MAX * FLAG_STRIDE));
+  HCHK(hipMemsetAsync(h->flags, 0, sizeof(unsigned long long) * FLAG_KINDS * FLAG_MAX * FLAG_STRIDE, stream));
   HCHK(hipStreamSynchronize(stream));
 #undef HCHK
   *out = h;
@@ -297,6 +301,15 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   const int NR = a->B * Mqp;
   const int NRP = ceil16(NR);
   if (NRP > MAX_ROWS_PADDED) return fail(MKX_EUNSUPPORTED, "B * (T_act + R_reg) too large for this build");
+  if ((long long)a->B * (H / 64) * (Mqp / 16) > FLAG_MAX) return fail(MKX_EUNSUPPORTED, "too many attention tasks for the ready-epoch table");
+  {
+    // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes)
+    const int RTn = NRP / 16, HT = H / 16, NH = H / 64;
+    auto rgs = [&](int tiles) { return std::max(1, std::min(RTn, h->G / tiles)); };
+    const int rg_o = rgs(HT);
+    if (HT * rg_o > 256 || ((RTn + rg_o - 1) / rg_o) * NH > 256 || 6 * rgs(6 * NH) > 256)
+      return fail(MKX_EUNSUPPORTED, "row grouping needs more than 256 ready epochs per wait");
+  }
   // LDS working sets (layout in mkx_kernel.h): self-attention keeps one query tile, the own rows' K and
   // V^T (hi + lo, 32-key blocks, at most 128 rows) and the wave-merge area in the 88 KB activation region;
   // the GEMM stages stage every sample's modulation slices (2 H floats) in 56 KB.
@@ -364,7 +377,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.act = d.activation == MKX_ACT_GELU_TANH ? 1 : 0;
   p.eps = d.eps; p.qk_eps = d.qk_eps; p.sm_scale = 1.0f / 8.0f;
   p.frames = h->frames; p.frame_bytes = fb; p.steps = h->steps; p.step_bytes = sb;
-  p.dcnt = h->dcnt; p.bar = h->bar;
+  p.dcnt = h->dcnt; p.bar = h->bar; p.flags = h->flags;
   for (int x = 0; x < MAX_XCD; ++x) p.nx[x] = h->nx[x];
   p.xmask = h->xmask;
   p.prof = h->prof; p.profile = h->profile;
@@ -389,9 +402,10 @@ int mkx_check(mkx_handle* h, void* stream_) {
   HIPCHK(hipMemcpy(&err, &h->bar->err, sizeof(int), hipMemcpyDeviceToHost));
   if (err) {
     HIPCHK(hipMemset(h->bar, 0, sizeof(BarState)));
+    HIPCHK(hipMemset(h->flags, 0, sizeof(unsigned long long) * FLAG_KINDS * FLAG_MAX * FLAG_STRIDE));
     HIPCHK(hipMemset(h->dcnt, 0, (size_t)(h->d.H / 16) * 4));
     h->gen_before = 0;
-    return fail(MKX_ETIMEOUT, "a grid-barrier wait exceeded its spin bound; barrier state was reset");
+    return fail(MKX_ETIMEOUT, "a stage wait exceeded its spin bound; the synchronisation state was reset");
   }
   return MKX_OK;
 }

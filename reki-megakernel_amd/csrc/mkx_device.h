@@ -4,10 +4,14 @@
 // each other):
 //  * Activations cross workgroups through write-once "frames": a producer writes with sc1 (device-scope,
 //    write-through past its XCD's L2), and every frame address is written at most once per launch and
-//    only read after the barrier that follows the write. Consumers therefore read with ordinary loads:
-//    no L2 can hold a stale copy of an address that was never read before it was written, and the L2 of
-//    each XCD de-duplicates the 32 CUs' reads of the same activation rows. No cache writeback or
-//    invalidate (buffer_wbl2 / buffer_inv) is executed on the hot path.
+//    only read after every task that writes its cache line has published its ready epoch (below).
+//    Consumers therefore read with ordinary loads: no L2 can hold a stale copy of a line that was never
+//    read before all of its writers were done, and the L2 of each XCD de-duplicates the 32 CUs' reads of
+//    the same activation rows. No cache writeback or invalidate (buffer_wbl2 / buffer_inv) is executed on
+//    the hot path.
+//  * Stages are ordered by per-task ready epochs (flag_publish / flag_wait): a consumer waits only for the
+//    producer tasks whose output it reads. One grid barrier per launch remains, after the launch's first
+//    stage (whose per-launch copies every later stage reads).
 //  * The grid barrier is hierarchical and fence-free: each workgroup waits for its own stores to be
 //    acknowledged, bumps its XCD's arrival counter with an L2 atomic, the last arrival of an XCD publishes
 //    the epoch with a device-scope store, and every workgroup polls the eight per-XCD flags with
@@ -130,16 +134,25 @@ __device__ __forceinline__ float wave_sum(float v) { return xor32_sum(xor16_sum(
 struct BarState {
   unsigned long long arrive[MAX_XCD][32];   // per-XCD arrival counters (L2 atomics), 256 B apart
   unsigned long long done[MAX_XCD][512];    // per-XCD published epochs (device scope), 4 KB apart
-  unsigned long long gen;                   // epoch base: barriers completed by earlier launches
+  unsigned long long gen;                   // epoch base: stage boundaries passed by earlier launches
   unsigned long long pad0[15];
   int err;                                  // 1 = a wait exceeded its spin bound
   int pad1[31];
   unsigned long long arrivals_last;         // barriers x workgroups recorded by the last launch
 };
 
+// Ready epochs: flags[kind][task] holds the epoch (gen at launch start + stage + 1) of the last stage in
+// which that producer task completed; a consumer task waits until the flags of exactly the producer tasks
+// whose output lines it reads have reached its stage. 64-bit and monotonic across launches (a launch of
+// `total` stages advances gen by total, so no flag of an earlier launch satisfies a later wait).
+constexpr int FLAG_MAX = 2048;
+constexpr int FLAG_STRIDE = 16;  // one 128-byte line per flag: no two writers share a line
+enum FlagKind { F_TAIL_IN = 0, F_TAIL_OUT, F_QKV, F_SA, F_O, F_CA, F_CAO, F_GU, F_DOWN, FLAG_KINDS };
+
 struct BarCtx {
   BarState* bs;
-  unsigned long long base;  // gen at launch start
+  unsigned long long* flags;  // [FLAG_KINDS][FLAG_MAX][FLAG_STRIDE]
+  unsigned long long base;    // gen at launch start
   unsigned x;               // this workgroup's XCD
   unsigned nx;              // workgroups on this XCD
   unsigned xmask;           // XCDs that have workgroups
@@ -182,6 +195,51 @@ __device__ __forceinline__ void bar_wait(BarCtx& c, unsigned long long e) {
   if (threadIdx.x == 0) s_failed = c.failed ? 1 : 0;
   __syncthreads();
   c.failed = s_failed != 0;
+}
+
+// publish: every wave's stores of the task have been acknowledged (write-through, so they are at the
+// device coherence point), then one device-scope store of the task's ready epoch
+__device__ __forceinline__ void flag_publish(BarCtx& c, int kind, int idx, unsigned long long e) {
+  wait_vm0();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&c.flags[((long long)kind * FLAG_MAX + idx) * FLAG_STRIDE], c.base + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// wait until flags[kind][idx(i)] >= base + e for every i < n (n <= 256): wave 0 polls them all, 64 per
+// device-scope load, each poll one round trip; the workgroup proceeds together. Bounded like bar_wait.
+template <class F>
+__device__ __forceinline__ void flag_wait(BarCtx& c, int kind, int n, F idx, unsigned long long e) {
+  constexpr int NCH = 4;  // up to 256 flags: every poll reads them all with one load per 64
+  if (threadIdx.x < 64 && !c.failed) {
+    const unsigned long long t = c.base + e;
+    const int lane = (int)threadIdx.x;
+    const unsigned long long* fp[NCH];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) fp[k] = c.flags + ((long long)kind * FLAG_MAX + idx(min(k * 64 + lane, n - 1))) * FLAG_STRIDE;
+    const int nch = (n + 63) / 64;
+    unsigned spins = 0;
+    while (true) {
+      unsigned long long v[NCH];
+#pragma unroll
+      for (int k = 0; k < NCH; ++k)
+        v[k] = k < nch ? __hip_atomic_load(fp[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : t;
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) ok = ok && v[k] >= t;
+      if (__all(ok)) break;
+      if (++spins > c.spin_limit) {
+        if (lane == 0) __hip_atomic_store(&c.bs->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        c.failed = true;
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  __shared__ int s_ffailed;
+  if (threadIdx.x == 0) s_ffailed = c.failed ? 1 : 0;
+  __syncthreads();
+  c.failed = s_ffailed != 0;
 }
 
 }  // namespace mkx

@@ -73,6 +73,7 @@ struct Params {
   char* steps; long long step_bytes;     // [n_steps] step areas: h0 (fp32, fragment-major) + x (fp32)
   unsigned* dcnt;                        // [H/16] split-K arrival counters
   BarState* bar; unsigned nx[MAX_XCD]; unsigned xmask;
+  unsigned long long* flags;             // [FLAG_KINDS][FLAG_MAX][FLAG_STRIDE] ready epochs
   long long* prof; int profile;
   unsigned spin_limit;
 };
@@ -278,6 +279,12 @@ __device__ __forceinline__ const float* mods_lds(Ctx<S>& c, int b, int width) {
   return (const float*)(c.smem + S::MODS) + (long long)b * width;
 }
 
+// row groups of a single-pass GEMM stage with `tiles` column tiles: as many as idle workgroups allow (the
+// operand rows are the stage's critical-path load; the weight tile is prefetched)
+__device__ __forceinline__ int rgs_of(int RT, int G, int tiles) { return max(1, min(RT, G / tiles)); }
+// row group (of rgs over RT row tiles, group g covering [g RT / rgs, (g + 1) RT / rgs)) holding row tile rt
+__device__ __forceinline__ int row_group_of(int rt, int RT, int rgs) { return ((rt + 1) * rgs - 1) / RT; }
+
 // ------------------------------------------------------------------------------------------------
 // Stage descriptor: what one stage computes, where its operands live, and what to prefetch for it.
 
@@ -357,9 +364,7 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
       break;
   }
   if (d.st == ST_QKV || d.st == ST_O || d.st == ST_CAO) {
-    // as many row groups as idle workgroups allow: a task then loads only its rows of the operand (the
-    // operand rows are the stage's critical-path load; the weight tile is prefetched)
-    d.rgs = max(1, min(c.RT, c.G / d.tiles));
+    d.rgs = rgs_of(c.RT, c.G, d.tiles);
     d.ntask = d.tiles * d.rgs;
   }
   return d;
@@ -566,8 +571,29 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
               as_u4(acc[rt][nt][0] + acc[rt][nt][1]));
 }
 
+// Waits until the producer tasks of stage g - 1 whose output lines this task reads have published: QKV reads
+// every column of its rows (all tiles of the down projection or the step tail's in-projection), the
+// out-projections read every head of their row tiles (attention tasks), gate/up every row of every column
+// (all out-projection tasks), a down split its quarter of the gate/up tiles.
 template <class S>
-__device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
+__device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, int g, int split, int rt_lo, int rt_hi) {
+  const int NQT = c.p.Mqp / 16;
+  if (d.st == ST_QKV) {
+    flag_wait(bc, d.l == 0 ? F_TAIL_IN : F_DOWN, S::HT, [](int i) { return i; }, (unsigned long long)g);
+  } else if (d.st == ST_O || d.st == ST_CAO) {
+    flag_wait(bc, d.st == ST_O ? F_SA : F_CA, (rt_hi - rt_lo) * S::NH, [&](int i) {
+      const int rt = rt_lo + i / S::NH, hd = i % S::NH;
+      return ((rt / NQT) * S::NH + hd) * NQT + rt % NQT;
+    }, (unsigned long long)g);
+  } else if (d.st == ST_GU) {
+    flag_wait(bc, F_CAO, S::HT * rgs_of(c.RT, c.G, S::HT), [](int i) { return i; }, (unsigned long long)g);
+  } else {
+    flag_wait(bc, F_GU, S::HT, [&](int i) { return split * S::HT + i; }, (unsigned long long)g);
+  }
+}
+
+template <class S>
+__device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc, int g) {
   constexpr int KPW = S::KPW, RB = S::RBMAX;
   CP& p = c.p;
   const int RT = c.RT, NRP = p.NRP;
@@ -590,6 +616,8 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
     const int kb0 = d.kind == K_SPLIT ? split * S::NKB : 0;
     const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
     const int rt_hi = d.kind == K_SPLIT ? RT : (split + 1) * RT / d.rgs;
+    gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
+    MKX_TR(c, 0);
     for (int rt0 = rt_lo; rt0 < rt_hi; rt0 += RB) {
       const int nrt = min(RB, rt_hi - rt0);
       EpiPre epre;
@@ -659,6 +687,8 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
       if (rt0 + RB < rt_hi) __syncthreads();  // red and ssw are reused by the next pass
       MKX_TR(c, 3);
     }
+    if (d.kind != K_SPLIT)
+      flag_publish(bc, d.st == ST_QKV ? F_QKV : d.st == ST_O ? F_O : d.st == ST_CAO ? F_CAO : F_GU, t, (unsigned long long)g + 1);
     if (d.kind == K_SPLIT) {
       // the last-arriving split task of this tile sums the partials in split order and applies the residual
       int* flag = (int*)(c.smem + S::SMALL + 3 * 1024 + 512);
@@ -684,6 +714,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d) {
           res_piece(c, d, tile, row, tile * 16 + 4 * (L >> 4), L, v, as_f4(ld16((const char*)d.res + fpiece(row, tile * 16 + 4 * (L >> 4), RT))));
         }
         MKX_TR(c, 7);
+        flag_publish(bc, F_DOWN, tile, (unsigned long long)g + 1);
       }
     }
   }
@@ -813,9 +844,9 @@ __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float*
   st_split4(y, spiece(b * c.p.Mqp + q, hd * HD + c.wave * 16 + 4 * (c.lane >> 4), c.RT), out);
 }
 
-// Attention tasks: task u -> (sample-head hh, query tile qt), u in [0, nqt * nhb), run by workgroup G - 1 - u
-// (and G - 1 - u + k G): the top of the grid, which the GEMM stage before each attention stage leaves idle,
-// so the idle workgroups' prefetch of the attention operands overlaps that GEMM stage. Heads in complete
+// Attention tasks: task u -> (sample-head hh, query tile qt), u in [0, nqt * nhb), placed by attn_first on
+// workgroups that the stages before leave idle, so their prefetch of the attention operands overlaps those
+// stages. Heads in complete
 // groups of 8 are arranged so that the query tiles of one head run on one XCD (u % 8 is the XCD class) and
 // share its L2; the remaining heads follow compactly.
 struct AttnTask {
@@ -838,6 +869,12 @@ __device__ __forceinline__ AttnTask attn_task(int u, int nqt, int nhb) {
   return a;
 }
 __device__ __forceinline__ int attn_count(int nqt, int nhb) { return nqt * nhb; }
+// first task of workgroup wg (then every G-th): self-attention tasks occupy the top of the grid (idle in
+// QKV), cross-attention tasks the workgroups just below them (idle in self-attention and the
+// out-projection, so their constant operands load during both)
+__device__ __forceinline__ int attn_first(bool cross, int G, int wg, int cnt) {
+  return ((G - 1 - (cross ? cnt : 0) - wg) % G + G) % G;
+}
 
 template <class S>
 __device__ __forceinline__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd, int kvs) {
@@ -948,7 +985,7 @@ __device__ __forceinline__ void transpose_caches(Ctx<S>& c, const int* s_ks) {
 // memory rows [kv_start, PM) (bf16 cache, pre-normed and rotated, DMA'd during the barrier) || the
 // sample's own rows (split q/k/v written by the QKV stage).
 template <class S>
-__device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_ks) {
+__device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_ks, BarCtx& bc, int g) {
   CP& p = c.p;
   const int M = p.Mq, Mqp = p.Mqp, PM = p.PM, PMP = ceil_to(PM, 32), NOWN32 = ceil_to(M, 32);
   const int NQT = Mqp / 16, NKT = NOWN32 / 16, KBO = NOWN32 / 32, NRP = p.NRP, RT = c.RT;
@@ -971,7 +1008,7 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* mrg = rk + 128;
   const int NHB = p.B * S::NH;
   const bool want_kv = (d.s == 0 && p.cur_k != nullptr && p.R > 0);
-  const int u0 = c.G - 1 - c.wg;
+  const int u0 = attn_first(false, c.G, c.wg, attn_count(NQT, NHB));
   for (int v = u0; v < attn_count(NQT, NHB); v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
@@ -982,6 +1019,16 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
       __syncthreads();
       sa_prefetch(c, l, b, hd, kvs);
     }
+    // the QKV tasks of this head (q, k, v x two column pairs, every row group): the rows' sums of squares
+    // and V^T blocks of one head interleave row groups within cache lines
+    {
+      const int rgq = rgs_of(RT, c.G, 6 * S::NH);
+      flag_wait(bc, F_QKV, 6 * rgq, [&](int i) {
+        const int k = i % 6, rg = i / 6;
+        return rg * 6 * S::NH + (k >> 1) * 2 * S::NH + 2 * hd + (k & 1);
+      }, (unsigned long long)g);
+    }
+    MKX_TR(c, 0);
     // own-row operands: Q tile (hi, lo), K tiles of all own keys, V^T blocks (all DMA, one batch)
     const int rt0 = b * Mqp / 16;
     for (int k = c.wave; k < 4 + 4 * NKT + 8 * KBO; k += NWAVES) {
@@ -1057,7 +1104,7 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
         *reinterpret_cast<u32x4*>(p.cur_v + o) = wv;
       }
     }
-    __syncthreads();
+    flag_publish(bc, F_SA, at.hh * NQT + qt, (unsigned long long)g + 1);
   }
 }
 
@@ -1126,7 +1173,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
   const int NHB = p.B * S::NH;
   const uint32_t vlane = (uint32_t)c.lane * 16;
-  const int u0 = c.G - 1 - c.wg, cnt = attn_count(NQT, NHB);
+  const int cnt = attn_count(NQT, NHB), u0 = attn_first(true, c.G, c.wg, cnt);
   // The operands that do not depend on the stage before, the Wq fragments of the task's head and the shift
   // fragments (an MFMA row tile whose rows are the samples), are loaded before the barrier completes: the
   // workgroups running this stage are idle in the stage before. (Loads only: the waves that do not poll the
@@ -1147,10 +1194,9 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
         wf[nt][i] = __builtin_bit_cast(bf16x8, ld16(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * 512 + c.lane * 8));
     }
   };
-  if (u0 < cnt) pre(attn_task(u0, NQT, NHB).hh % S::NH);
-  bar_wait(bc, (unsigned long long)g);
-  MKX_TR(c, 0);
-  if (p.profile && c.wg == 0 && c.tid == 0) p.prof[g] = clock100() * 10;
+  // (wave 0 polls the ready epochs first: its loads would delay the poll, so it issues its share after)
+  if (u0 < cnt && c.wave != 0) pre(attn_task(u0, NQT, NHB).hh % S::NH);
+  const int rgo = rgs_of(RT, c.G, S::HT);
   for (int v = u0; v < cnt; v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
@@ -1164,6 +1210,13 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       pre(hd);
     }
     const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
+    // every out-projection tile of the row group holding the query rows (their sums of squares share lines)
+    {
+      const int rg = row_group_of(rq, RT, rgo);
+      flag_wait(bc, F_O, S::HT, [&](int i) { return rg * S::HT + i; }, (unsigned long long)g);
+    }
+    if (v == u0 && c.wave == 0) pre(hd);
+    MKX_TR(c, 0);
     // 1a. operands: y2 fragments of the query rows, sums of squares; and for step 1b this lane's RoPE / norm
     //     constants
     bf16x8 yh[KPW], ylo[KPW];
@@ -1290,7 +1343,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     MKX_TR(c, 2);
     attn_merge_store(c, A, mrg, yca, b, hd, qt);
     MKX_TR(c, 13);
-    __syncthreads();
+    flag_publish(bc, F_CA, at.hh * NQT + qt, (unsigned long long)g + 1);
   }
 }
 
@@ -1313,7 +1366,7 @@ __device__ __forceinline__ void wave_sum_n(float* v) {
 }
 
 template <class S>
-__device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
+__device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc, int g) {
   CP& p = c.p;
   constexpr int NP = S::H / 256;  // pieces per lane
   constexpr int R = TAIL_RPW;
@@ -1346,6 +1399,12 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
       }
       if (c.tid < adim * 4) wt = ldf4(p.win + (long long)(c.tid >> 2) * S::H + t * 16 + 4 * (c.tid & 3));
     }
+    if (!d.first) {
+      // every tile of the last layer's output, and x of this step (the previous step tail's output dims)
+      flag_wait(bc, F_DOWN, S::HT, [](int i) { return i; }, (unsigned long long)g);
+      if (d.s > 0) flag_wait(bc, F_TAIL_OUT, p.A, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
+    }
+    MKX_TR(c, 0);
     if (!d.first) {
       f32x4 wa[NP];
       if (!inproj) {
@@ -1485,6 +1544,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d) {
         if (q == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, t, S::HT), __float_as_uint(ss));
       }
     }
+    flag_publish(bc, inproj ? F_TAIL_IN : F_TAIL_OUT, inproj ? t : a_out, (unsigned long long)g + 1);
   }
 }
 
@@ -1498,7 +1558,8 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   char* mb = c.smem + S::MODS;
   MKX_TRW(c, 8);
   if (d.st == ST_SA || d.st == ST_CA) {
-    const AttnTask at = attn_task(c.G - 1 - t, p.Mqp / 16, p.B * S::NH);
+    const int nqt = p.Mqp / 16, cnt = attn_count(nqt, p.B * S::NH);
+    const AttnTask at = attn_task(attn_first(d.st == ST_CA, c.G, t, cnt), nqt, p.B * S::NH);
     if (at.ok) {
       const int b = at.hh / S::NH, hd = at.hh % S::NH;
       if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
@@ -1556,6 +1617,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   bc.spin_limit = p.spin_limit;
   bc.failed = false;
   bc.base = __hip_atomic_load(&p.bar->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  bc.flags = p.flags;
   // one agent-scope acquire per launch: no cache of this XCD holds lines from before the launch
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (c.wg == 0 && c.tid < S::HT) __hip_atomic_store(&p.dcnt[c.tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1573,35 +1635,42 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       Ctx<S> c(*pl, smem);
       c.dt = dt;
       c.ep = (unsigned)g;
-      if (cur.st == ST_SA) sa_stage(c, cur, s_ks);
-      else if (cur.st == ST_CA) ca_stage(c, cur, s_ks, bc, g);  // completes barrier g itself
-      else if (cur.st == ST_TAIL) tail_stage(c, cur);
-      else gemm_stage(c, cur);
+      if (cur.st == ST_SA) sa_stage(c, cur, s_ks, bc, g);
+      else if (cur.st == ST_CA) ca_stage(c, cur, s_ks, bc, g);
+      else if (cur.st == ST_TAIL) tail_stage(c, cur, bc, g);
+      else gemm_stage(c, cur, bc, g);
       if (g == 0) {
         transpose_caches(c, s_ks);
         split_shifts(c);
       }
     }
-    // barrier; the next stage's constant operands are DMA'd while it completes
     c.ep = (unsigned)g;
     MKX_TR(c, 4);
-    wait_vm0();  // (bar_arrive waits for the stores too; separated here so a trace can time it)
-    MKX_TR(c, 11);
-    bar_arrive(bc, (unsigned long long)g + 1);
-    MKX_TR(c, 5);
-    MKX_TRW(c, 12);
-    // the next stage's descriptor, computed while the barrier completes
-    if (g + 1 < total) {
-      cur = describe(c, g + 1);
+    if (g == 0) {
+      // the per-launch copies (V^T of the caches, split shifts) are read by every later stage: the launch's
+      // one grid barrier; the next stage's constant operands are DMA'd while it completes
+      wait_vm0();
+      bar_arrive(bc, 1);
+      cur = describe(c, 1);
       if (c.wave != 0) prefetch(c, cur, s_ks);
+      bar_wait(bc, 1);
+    } else {
+      __syncthreads();  // this stage's LDS is no longer read: the next stage's prefetch may overwrite it
+      if (g + 1 < total) {
+        cur = describe(c, g + 1);
+        // waves 1-3 issue the prefetch; wave 0, which polls the ready epochs, keeps no loads in flight
+        if (c.wave != 0) prefetch(c, cur, s_ks);
+      }
     }
-    MKX_TR(c, 6);
-    if (g + 1 < total && cur.st == ST_CA) continue;
-    bar_wait(bc, (unsigned long long)g + 1);
     c.ep = (unsigned)(g + 1);
-    MKX_TR(c, 0);
+    MKX_TR(c, 6);
     if (p.profile && c.wg == 0 && c.tid == 0) p.prof[g + 1] = clock100() * 10;
   }
+  // every workgroup has passed every stage boundary: count them like barrier arrivals (the arrival counters
+  // then read (gen + total) x workgroups, the state the next launch's barrier expects)
+  wait_vm0();
+  __syncthreads();
+  if (c.tid == 0) __hip_atomic_fetch_add(&p.bar->arrive[bc.x][0], (unsigned long long)(total - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   if (c.wg == 0 && c.tid == 0) __hip_atomic_store(&p.bar->gen, bc.base + (unsigned long long)total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
