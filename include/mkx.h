@@ -6,7 +6,7 @@
  * src/mk_expert.py (muninn-huginn/reki-megakernel):
  *   mkx_create   <- ExpertMegakernel.__init__   (src/mk_expert.py:436-481: pack weights once, own scratch)
  *   mkx_run      <- ExpertMegakernel.run        (src/mk_expert.py:483-515: marshal caches, one launch)
- *   mkx_barriers <- ExpertMegakernel.barriers   (src/mk_expert.py:517-518: grid barriers per launch)
+ *   mkx_barriers <- ExpertMegakernel.barriers   (src/mk_expert.py:517-518: stage boundaries per launch)
  *   mkx_query    <- attributes the reference reads off the object (nprog, bar, prof; test_mk.py:44-45,
  *                   tune_mk.py:131-153)
  *   mkx_destroy, mkx_last_error, mkx_status_string: lifetime and error reporting the Python object
@@ -36,7 +36,7 @@ typedef enum {
   MKX_EINVAL = 1,        /* shape / dtype / pointer / stride invalid (reference: assert) */
   MKX_ENORESIDENT = 2,   /* the persistent grid cannot be co-resident (reference: hangs, README.md:262-263) */
   MKX_EHIP = 3,          /* a HIP runtime call failed; mkx_last_error() names it */
-  MKX_ETIMEOUT = 4,      /* a grid-barrier wait exceeded its spin bound; results are invalid */
+  MKX_ETIMEOUT = 4,      /* a barrier or ready-epoch wait exceeded its spin bound; results are invalid */
   MKX_ENOMEM = 5,
   MKX_EUNSUPPORTED = 6   /* a shape this build has no kernel instantiation for */
 } mkx_status;
@@ -117,7 +117,7 @@ typedef struct {
 typedef enum {
   MKX_Q_GRID = 0,          /* workgroups in the persistent launch (reference: nprog = SM count, :473) */
   MKX_Q_BLOCK = 1,         /* threads per workgroup */
-  MKX_Q_BARRIER_COUNT = 2, /* barriers completed by the last launch (reference: mk.bar after the run, test_mk.py:44) */
+  MKX_Q_BARRIER_COUNT = 2, /* workgroup passages of stage boundaries since the last query (reference: mk.bar after the run, test_mk.py:44) */
   MKX_Q_ERROR_FLAG = 3,    /* device error flag of the last launch (spin bound exceeded = 1) */
   MKX_Q_PROFILE_LEN = 5,   /* entries of the caller's timestamp buffer, 0 when profiling is off */
   MKX_Q_WEIGHT_BYTES = 6,  /* bytes of packed linear weights streamed per Euler step */
@@ -134,17 +134,18 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* weights, void* stream, m
 /* ExpertMegakernel.run (src/mk_expert.py:483-515): one persistent launch on `stream` (a hipStream_t;
  * NULL = default stream). Inputs are borrowed for the duration of the call. A handle's scratch is shared
  * by its calls: use one handle per stream (the reference is not re-entrant either). Asynchronous; call
- * mkx_check after synchronising to learn whether a barrier wait timed out. */
+ * mkx_check after synchronising to learn whether a barrier or ready-epoch wait timed out. */
 int mkx_run(mkx_handle* h, const mkx_step_args* args, void* stream);
 
 /* Reads the device error flag of the last launch (synchronises `stream`): MKX_OK or MKX_ETIMEOUT. */
 int mkx_check(mkx_handle* h, void* stream);
 
-/* ExpertMegakernel.barriers (src/mk_expert.py:517-518): grid barriers one launch of n_steps executes. */
+/* ExpertMegakernel.barriers (src/mk_expert.py:517-518): stage boundaries one launch of n_steps passes
+ * (1 + n_steps (7 L + 1); the first is a grid barrier, the others per-task ready epochs). */
 int64_t mkx_barriers(const mkx_handle* h, int32_t n_steps);
 
-/* Per-barrier timestamps (tune_mk.py PROFILE mode, src/mk_expert.py:66-69): later launches store, from
- * workgroup 0, the ns clock after barrier nb into buf[nb] (buf[0] = launch start). buf is a caller-owned
+/* Per-boundary timestamps (tune_mk.py PROFILE mode, src/mk_expert.py:66-69): later launches store, from
+ * workgroup 0, the ns clock when it passes stage boundary nb into buf[nb] (buf[0] = launch start). buf is a caller-owned
  * device int64 array of len entries (>= mkx_barriers(n_steps) + 1); NULL turns profiling off. */
 int mkx_set_profile(mkx_handle* h, int64_t* buf, int32_t len);
 

@@ -2,9 +2,11 @@
 //
 // Schedule (the stage math of expert_megakernel, src/mk_expert.py:302-426): an in-projection tail, then for
 // each step and layer seven stages (QKV, self-attention, out-proj + gated residual, cross-attention with its
-// own query projection, out-proj + gated residual, gate/up, down + gated residual) and a step tail. Every
-// stage is followed by one grid barrier: 1 + n_steps * (7 L + 1) barriers (the reference runs the
-// cross-attention query projection as a stage of its own: 8 L + 1).
+// own query projection, out-proj + gated residual, gate/up, down + gated residual) and a step tail:
+// 1 + n_steps * (7 L + 1) stage boundaries (the reference runs the cross-attention query projection as a
+// stage of its own and a grid barrier after every stage: 8 L + 1). Only the first boundary is a grid
+// barrier; afterwards every task publishes a ready epoch and every task waits for exactly the producer
+// tasks whose output it reads.
 //
 // Code layout: the kernel is one flat loop over stages, and each kind of stage (GEMM, self-attention,
 // cross-attention, tail) is a single inlined body driven by a runtime descriptor. The whole loop stays
@@ -12,10 +14,10 @@
 //
 // Work decomposition for 256 CUs: every linear layer is cut into 16-column output tiles (one task per
 // workgroup, K = H per task; the down projection is split over K into I/H tasks per tile whose fp32
-// partials are summed in a fixed order by the last-arriving task). Between arriving at a barrier and
-// waiting on it, a workgroup DMAs into LDS everything constant its next task needs: the packed weight tile
-// and the per-sample modulation slices (or, for attention, the cached K/V). After the barrier only the
-// activations are loaded, straight into VGPRs.
+// partials are summed in a fixed order by the last-arriving task). Between finishing its work in one stage
+// and waiting for the producers of its next task, a workgroup DMAs into LDS everything constant that task
+// needs: the packed weight tile (or, for attention, the cached K/V). After the wait only the activations
+// are loaded, straight into VGPRs.
 //
 // Activation frames are fragment-major: a buffer of C columns and NRP rows is cut into 2 KB blocks
 // (32-column block kb, 16-row tile rt) at ((kb * RT + rt) * 2) KB, lane-major inside (lane = row % 16 +
