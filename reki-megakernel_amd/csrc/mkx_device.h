@@ -197,6 +197,16 @@ __device__ __forceinline__ void bar_wait(BarCtx& c, unsigned long long e) {
   c.failed = s_failed != 0;
 }
 
+// Execution barrier of the workgroup that orders no memory operation: waves whose LDS DMAs (the prefetch of
+// a later phase) are still in flight pass it without waiting for them (__syncthreads' workgroup fences make
+// every wave wait for its outstanding DMAs first). The empty asm statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void exec_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // publish: every wave's stores of the task have been acknowledged (write-through, so they are at the
 // device coherence point), then one device-scope store of the task's ready epoch
 __device__ __forceinline__ void flag_publish(BarCtx& c, int kind, int idx, unsigned long long e) {
@@ -207,7 +217,8 @@ __device__ __forceinline__ void flag_publish(BarCtx& c, int kind, int idx, unsig
 }
 
 // wait until flags[kind][idx(i)] >= base + e for every i < n (n <= 256): wave 0 polls them all, 64 per
-// device-scope load, each poll one round trip; the workgroup proceeds together. Bounded like bar_wait.
+// device-scope load, each poll one round trip; the workgroup proceeds together. Bounded like bar_wait (only
+// wave 0 polls, so only wave 0 tracks whether a wait gave up).
 template <class F>
 __device__ __forceinline__ void flag_wait(BarCtx& c, int kind, int n, F idx, unsigned long long e) {
   constexpr int NCH = 4;  // up to 256 flags: every poll reads them all with one load per 64
@@ -235,11 +246,7 @@ __device__ __forceinline__ void flag_wait(BarCtx& c, int kind, int n, F idx, uns
       }
     }
   }
-  __syncthreads();
-  __shared__ int s_ffailed;
-  if (threadIdx.x == 0) s_ffailed = c.failed ? 1 : 0;
-  __syncthreads();
-  c.failed = s_ffailed != 0;
+  exec_barrier();
 }
 
 }  // namespace mkx

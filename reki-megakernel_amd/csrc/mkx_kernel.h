@@ -1384,7 +1384,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   const int sn = d.first ? 0 : d.s + 1;
   // task t runs on workgroup G - 1 - t: the top of the grid, mostly idle in the down projection before it
   for (int t = c.G - 1 - c.wg; t < nin + nout; t += c.G) {
-    __syncthreads();
+    if (t != c.G - 1 - c.wg) __syncthreads();  // the previous task's LDS (the first task's is free already)
     const bool inproj = t < nin;
     const int a_out = t - nin;
     // in-projection item of this thread (first pass): row, 4-column piece q of tile t; its constant operands
@@ -1406,6 +1406,9 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       flag_wait(bc, F_DOWN, S::HT, [](int i) { return i; }, (unsigned long long)g);
       if (d.s > 0) flag_wait(bc, F_TAIL_OUT, p.A, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
     }
+    // the staged final modulation rows and Wout rows (DMA'd by the prefetch) have landed
+    wait_vm0();
+    __syncthreads();
     MKX_TR(c, 0);
     if (!d.first) {
       f32x4 wa[NP];
