@@ -107,7 +107,6 @@ struct mkx_handle {
   size_t steps_cap = 0;
   bf16_t* vts = nullptr;  // per-launch V^T copies of the memory and cross-attention V caches
   size_t vts_cap = 0;
-  unsigned* dcnt = nullptr;
   BarState* bar = nullptr;
   unsigned long long* flags = nullptr;  // [FLAG_KINDS][FLAG_MAX][FLAG_STRIDE] ready epochs
   long long* prof = nullptr;
@@ -122,7 +121,7 @@ struct mkx_handle {
 static void free_handle(mkx_handle* h) {
   if (!h) return;
   void* ptrs[] = {h->wqkv, h->wo, h->wqca, h->woca, h->wgu, h->wd, h->qn, h->kn, h->qcan, h->win, h->bin,
-                  h->wout, h->bout, h->frames, h->steps, h->vts, h->dcnt, h->bar, h->flags};
+                  h->wout, h->bout, h->frames, h->steps, h->vts, h->bar, h->flags};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete h;
@@ -201,6 +200,8 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   // many workgroups as it has CUs. The probe finds which XCDs exist; the dispatcher's rotation between
   // launches changes which workgroup lands where, not how many land on each XCD.
   if (h->G > 256) return bail(fail(MKX_EUNSUPPORTED, "more than 256 CUs"));
+  // the top of the grid holds the step tail's H/32 in-projection tasks and the 16 down-projection reducers
+  if (h->G < d.H / 32 + 16) return bail(fail(MKX_ENORESIDENT, "too few CUs for the step tail and the down-projection reducers"));
   int nxcd = 0;
   for (int i = 0; i < h->G; ++i) {
     if (hx[i] >= MAX_XCD) return bail(fail(MKX_EUNSUPPORTED, "unexpected XCC id"));
@@ -247,8 +248,6 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   HCHK(hipMemcpyAsync(h->bin, w->bin, (size_t)H * 4, hipMemcpyDeviceToDevice, stream));
   HCHK(hipMemcpyAsync(h->wout, w->wout, (size_t)d.A * H * 4, hipMemcpyDeviceToDevice, stream));
   HCHK(hipMemcpyAsync(h->bout, w->bout, (size_t)d.A * 4, hipMemcpyDeviceToDevice, stream));
-  HCHK(alloc((void**)&h->dcnt, (size_t)(H / 16) * 4));
-  HCHK(hipMemsetAsync(h->dcnt, 0, (size_t)(H / 16) * 4, stream));
   HCHK(alloc((void**)&h->bar, sizeof(BarState)));
   HCHK(hipMemsetAsync(h->bar, 0, sizeof(BarState), stream));
   HCHK(alloc((void**)&h->flags, sizeof(unsigned long long) * FLAG_KINDS * FLAG_MAX * FLAG_STRIDE));
@@ -282,6 +281,8 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   // step tail: x' of the real action dims (32 KB) and Wout's real-dim rows (64 KB) are staged in LDS
   if ((long long)a->B * a->T_act * a->action_dim * 4 > 32 * 1024) return fail(MKX_EUNSUPPORTED, "B * T_act * action_dim too large for the step tail");
   if ((long long)a->action_dim * H * 4 > 64 * 1024) return fail(MKX_EUNSUPPORTED, "action_dim * H too large for the step tail");
+  // the in-projection task's Win columns [action_dim][32] are staged in 3 KB of LDS
+  if (a->action_dim > 24) return fail(MKX_EUNSUPPORTED, "action_dim above 24 is not supported by the step tail");
   if (a->B < 1 || a->B > d.max_batch) return fail(MKX_EINVAL, "B out of range");
   if (a->T_act < 1 || a->R_reg < 0) return fail(MKX_EINVAL, "T_act must be >= 1 and R_reg >= 0");
   const int Mq = a->T_act + a->R_reg;
@@ -377,7 +378,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.act = d.activation == MKX_ACT_GELU_TANH ? 1 : 0;
   p.eps = d.eps; p.qk_eps = d.qk_eps; p.sm_scale = 1.0f / 8.0f;
   p.frames = h->frames; p.frame_bytes = fb; p.steps = h->steps; p.step_bytes = sb;
-  p.dcnt = h->dcnt; p.bar = h->bar; p.flags = h->flags;
+  p.bar = h->bar; p.flags = h->flags;
   for (int x = 0; x < MAX_XCD; ++x) p.nx[x] = h->nx[x];
   p.xmask = h->xmask;
   p.prof = h->prof; p.profile = h->profile;
@@ -403,7 +404,6 @@ int mkx_check(mkx_handle* h, void* stream_) {
   if (err) {
     HIPCHK(hipMemset(h->bar, 0, sizeof(BarState)));
     HIPCHK(hipMemset(h->flags, 0, sizeof(unsigned long long) * FLAG_KINDS * FLAG_MAX * FLAG_STRIDE));
-    HIPCHK(hipMemset(h->dcnt, 0, (size_t)(h->d.H / 16) * 4));
     h->gen_before = 0;
     return fail(MKX_ETIMEOUT, "a stage wait exceeded its spin bound; the synchronisation state was reset");
   }

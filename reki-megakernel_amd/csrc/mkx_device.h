@@ -147,7 +147,7 @@ struct BarState {
 // `total` stages advances gen by total, so no flag of an earlier launch satisfies a later wait).
 constexpr int FLAG_MAX = 2048;
 constexpr int FLAG_STRIDE = 16;  // one 128-byte line per flag: no two writers share a line
-enum FlagKind { F_TAIL_IN = 0, F_TAIL_OUT, F_QKV, F_SA, F_O, F_CA, F_CAO, F_GU, F_DOWN, FLAG_KINDS };
+enum FlagKind { F_TAIL_IN = 0, F_TAIL_OUT, F_QKV, F_SA, F_O, F_CA, F_CAO, F_GU, F_DPART, F_DOWN, FLAG_KINDS };
 
 struct BarCtx {
   BarState* bs;

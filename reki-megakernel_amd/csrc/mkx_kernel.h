@@ -14,10 +14,10 @@
 //
 // Work decomposition for 256 CUs: every linear layer is cut into 16-column output tiles (one task per
 // workgroup, K = H per task; the down projection is split over K into I/H tasks per tile whose fp32
-// partials are summed in a fixed order by the last-arriving task). Between finishing its work in one stage
-// and waiting for the producers of its next task, a workgroup DMAs into LDS everything constant that task
-// needs: the packed weight tile (or, for attention, the cached K/V). After the wait only the activations
-// are loaded, straight into VGPRs.
+// partials are summed in a fixed order by reducer workgroups that have no QKV task). Between finishing its
+// work in one stage and waiting for the producers of its next task, a workgroup DMAs into LDS everything
+// constant that task needs: the packed weight tile (or, for attention, the cached K/V). After the wait only
+// the activations are loaded, straight into VGPRs.
 //
 // Activation frames are fragment-major: a buffer of C columns and NRP rows is cut into 2 KB blocks
 // (32-column block kb, 16-row tile rt) at ((kb * RT + rt) * 2) KB, lane-major inside (lane = row % 16 +
@@ -73,7 +73,6 @@ struct Params {
   // scratch
   char* frames; long long frame_bytes;   // [n_steps * L] layer frames
   char* steps; long long step_bytes;     // [n_steps] step areas: h0 (fp32, fragment-major) + x (fp32)
-  unsigned* dcnt;                        // [H/16] split-K arrival counters
   BarState* bar; unsigned nx[MAX_XCD]; unsigned xmask;
   unsigned long long* flags;             // [FLAG_KINDS][FLAG_MAX][FLAG_STRIDE] ready epochs
   long long* prof; int profile;
@@ -97,8 +96,15 @@ struct Shape {
   static constexpr int SMALL = ABUF + ABUF_BYTES, SMALL_BYTES = 4 * 1024;
   static constexpr int LDS = SMALL + SMALL_BYTES;
   static constexpr int RB_FIT = 144 / (KPW * 8);  // row tiles per GEMM pass held in VGPRs (hi + lo)
+  // Workgroups of the top of the grid with fixed roles at the end of a layer and of a step: the step tail's
+  // in-projection tasks (two 16-column tiles each) on the NIN highest workgroups, below them NRED reducers,
+  // each of which sums the down projection's split-K partials of TPR output tiles (and, at the end of a step,
+  // runs the tail's output-dim tasks). None of them has a QKV task, so the next layer's QKV tasks never wait
+  // behind a reduction or a step tail on their own workgroup.
+  static constexpr int NIN = HT / 2, NRED = 16, TPR = HT / NRED;
   static constexpr int RBMAX = RB_FIT > 3 ? 3 : RB_FIT;
   static_assert(H % 256 == 0 && I % H == 0, "H must be a multiple of 256 and I a multiple of H");
+  static_assert(HT % NRED == 0 && TPR * SK <= 256, "each reducer waits on at most 256 partial tasks");
   static_assert(KPW >= 1 && RBMAX >= 1, "tile does not fit registers");
   static_assert(NKB * 1024 * 2 <= WBUF_BYTES, "gate/up weight tile pair must fit the weight buffer");
   static_assert(NWAVES * (RBMAX + 1) * 2 * 1024 <= RED_BYTES, "cross-wave reduction must fit LDS");
@@ -286,6 +292,12 @@ __device__ __forceinline__ const float* mods_lds(Ctx<S>& c, int b, int width) {
 __device__ __forceinline__ int rgs_of(int RT, int G, int tiles) { return max(1, min(RT, G / tiles)); }
 // row group (of rgs over RT row tiles, group g covering [g RT / rgs, (g + 1) RT / rgs)) holding row tile rt
 __device__ __forceinline__ int row_group_of(int rt, int RT, int rgs) { return ((rt + 1) * rgs - 1) / RT; }
+// the step tail's in-projection task of workgroup wg (or >= NIN: none) and its reducer index (or outside
+// [0, NRED): none)
+template <class S>
+__device__ __forceinline__ int tail_in_task(int G, int wg) { return G - 1 - wg; }
+template <class S>
+__device__ __forceinline__ int reducer_of(int G, int wg) { return G - 1 - S::NIN - wg; }
 
 // ------------------------------------------------------------------------------------------------
 // Stage descriptor: what one stage computes, where its operands live, and what to prefetch for it.
@@ -388,8 +400,8 @@ __device__ __forceinline__ const bf16_t* wtile(const Desc& d, int t) {
 //     samples' shift slices. K_QKV: see qk_piece / the V^T epilogue; K_GU stores act(gate) * up split
 //     (:404-413).
 //   K_RES: h_out = res + acc * gate (:162-172), stored fp32, plus y = h_out * (1 + next scale) split and
-//     the tile's sums of squares of h_out; K_SPLIT: K-split partial, the last split of a tile sums the
-//     partials in split order and applies K_RES.
+//     the tile's sums of squares of h_out; K_SPLIT: K-split partial; the tile's reducer sums the partials
+//     in split order and applies K_RES (down_reduce).
 // K (= H per task) is split over the 4 waves; the wave partials are summed through LDS.
 
 // byte offset of the sum of squares of (row, 16-column tile t) in an [NRP][HT] array
@@ -574,14 +586,15 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
 }
 
 // Waits until the producer tasks of stage g - 1 whose output lines this task reads have published: QKV reads
-// every column of its rows (all tiles of the down projection or the step tail's in-projection), the
+// every column of its rows (the down projection's reducers or the step tail's in-projection tasks), the
 // out-projections read every head of their row tiles (attention tasks), gate/up every row of every column
 // (all out-projection tasks), a down split its quarter of the gate/up tiles.
 template <class S>
 __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, int g, int split, int rt_lo, int rt_hi) {
   const int NQT = c.p.Mqp / 16;
   if (d.st == ST_QKV) {
-    flag_wait(bc, d.l == 0 ? F_TAIL_IN : F_DOWN, S::HT, [](int i) { return i; }, (unsigned long long)g);
+    // every column of its rows: the step tail's in-projection tasks, or the down projection's reducers
+    flag_wait(bc, d.l == 0 ? F_TAIL_IN : F_DOWN, d.l == 0 ? S::NIN : S::NRED, [](int i) { return i; }, (unsigned long long)g);
   } else if (d.st == ST_O || d.st == ST_CAO) {
     flag_wait(bc, d.st == ST_O ? F_SA : F_CA, (rt_hi - rt_lo) * S::NH, [&](int i) {
       const int rt = rt_lo + i / S::NH, hd = i % S::NH;
@@ -592,6 +605,32 @@ __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, 
   } else {
     flag_wait(bc, F_GU, S::HT, [&](int i) { return split * S::HT + i; }, (unsigned long long)g);
   }
+}
+
+// Down-projection reducer r: once the SK split tasks of its output tiles t0 .. t0 + TPR - 1 have published
+// their partial sums, it adds them in split order and applies the gated residual (hl = h3 + gate * sum, with
+// yl and the sums of squares for the next AdaRMS), then publishes one ready epoch for the TPR tiles.
+template <class S>
+__device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc, int g, int r) {
+  const int RT = c.RT, t0 = r * S::TPR;
+  flag_wait(bc, F_DPART, S::TPR * S::SK, [&](int i) { return (i % S::SK) * S::HT + t0 + i / S::SK; }, (unsigned long long)g);
+  wait_vm0();  // the staged gate and next AdaRMS scale (the prefetch's DMA) have landed
+  __syncthreads();
+  // one (tile, row tile) block of 64 items per wave and round: lanes L, L^16, L^32, L^48 hold one row
+  for (int it = c.tid; it < S::TPR * RT * 64; it += NTHREADS) {
+    const int tile = t0 + it / (RT * 64), rem = it % (RT * 64), rtg = rem >> 6, L = rem & 63;
+    u32x4 xp[S::SK];
+#pragma unroll
+    for (int j = 0; j < S::SK; ++j) xp[j] = ld16((const char*)d.part + ((((j * S::HT + tile) * RT + rtg) * 64 + L) * 16));
+    const int row = rtg * 16 + (L & 15), col = tile * 16 + 4 * (L >> 4);
+    const f32x4 res = as_f4(ld16((const char*)d.res + fpiece(row, col, RT)));
+    f32x4 v = as_f4(xp[0]);
+#pragma unroll
+    for (int j = 1; j < S::SK; ++j) v += as_f4(xp[j]);
+    res_piece(c, d, tile, row, col, L, v, res);
+  }
+  MKX_TR(c, 7);
+  flag_publish(bc, F_DOWN, r, (unsigned long long)g + 1);
 }
 
 template <class S>
@@ -689,36 +728,12 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       if (rt0 + RB < rt_hi) __syncthreads();  // red and ssw are reused by the next pass
       MKX_TR(c, 3);
     }
-    if (d.kind != K_SPLIT)
-      flag_publish(bc, d.st == ST_QKV ? F_QKV : d.st == ST_O ? F_O : d.st == ST_CAO ? F_CAO : F_GU, t, (unsigned long long)g + 1);
-    if (d.kind == K_SPLIT) {
-      // the last-arriving split task of this tile sums the partials in split order and applies the residual
-      int* flag = (int*)(c.smem + S::SMALL + 3 * 1024 + 512);
-      wait_vm0();
-      __syncthreads();
-      if (c.tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(&p.dcnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = (old == (unsigned)(S::SK - 1));
-        if (last) __hip_atomic_store(&p.dcnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = last;
-      }
-      __syncthreads();
-      if (*flag) {
-        for (int it = c.tid; it < RT * 64; it += NTHREADS) {
-          const int rtg = it >> 6, L = it & 63;
-          u32x4 xp[S::SK];
-#pragma unroll
-          for (int j = 0; j < S::SK; ++j) xp[j] = ld_sc1(d.part, (uint32_t)((((j * d.tiles + tile) * RT + rtg) * 64 + L) * 16));
-          f32x4 v = as_f4(xp[0]);
-#pragma unroll
-          for (int j = 1; j < S::SK; ++j) v += as_f4(xp[j]);
-          const int row = rtg * 16 + (L & 15);
-          res_piece(c, d, tile, row, tile * 16 + 4 * (L >> 4), L, v, as_f4(ld16((const char*)d.res + fpiece(row, tile * 16 + 4 * (L >> 4), RT))));
-        }
-        MKX_TR(c, 7);
-        flag_publish(bc, F_DOWN, tile, (unsigned long long)g + 1);
-      }
-    }
+    flag_publish(bc, d.st == ST_QKV ? F_QKV : d.st == ST_O ? F_O : d.st == ST_CAO ? F_CAO : d.st == ST_GU ? F_GU : F_DPART, t,
+                 (unsigned long long)g + 1);
+  }
+  if (d.kind == K_SPLIT) {
+    const int r = reducer_of<S>(c.G, c.wg);
+    if (r >= 0 && r < S::NRED) down_reduce(c, d, bc, g, r);
   }
 }
 
@@ -1352,9 +1367,10 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 // ------------------------------------------------------------------------------------------------
 // Step tail (src/mk_expert.py:254-299): o = AdaRMS_final(h_L); v = o Wout^T + bout; x' = x + dt v;
 // h0' = x'_real Win + bin (action rows), register tokens (register rows), all fp32; with h0' its layer-0
-// AdaRMS operand y0' = h0' (1 + scale) (split) and sums of squares. Tasks [0, H/16):
-// in-projection tiles (each recomputes the velocity of the real action dims); tasks [H/16, H/16 + A):
-// one output dim each. Wave w takes the action rows w + 4 k, TAIL_RPW of them per batch with their loads
+// AdaRMS operand y0' = h0' (1 + scale) (split) and sums of squares. Tasks [0, NIN): in-projection tasks of
+// two 16-column tiles (each recomputes the velocity of the real action dims), on the NIN highest workgroups;
+// tasks [NIN, NIN + A): one output dim each, on the down projection's reducers (nothing waits for them
+// before the next step tail). Wave w takes the action rows w + 4 k, TAIL_RPW of them per batch with their loads
 // issued together; lane owns the 4-column pieces 4 (lane + 64 q). The final modulation rows and Wout's
 // real-dim rows were staged in LDS by the prefetch; the in-projection's constant operands (Win tile, bias,
 // register tokens, layer-0 scale) are loaded with the first batch.
@@ -1372,7 +1388,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   CP& p = c.p;
   constexpr int NP = S::H / 256;  // pieces per lane
   constexpr int R = TAIL_RPW;
-  const int nin = d.last ? 0 : S::HT;
+  const int nin = d.last ? 0 : S::NIN;
   const int nout = d.first ? 0 : p.A;
   const int nrows = p.B * p.T;
   const int adim = p.action_dim;
@@ -1380,30 +1396,39 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   const float* hL = d.first ? p.x_in : (const float*)(c.frame(d.s, p.L - 1) + S::hl_off(p.NRP));
   float* xp = (float*)(c.smem + S::ABUF);                // [nrows][adim] x' of the real dims
   const float* wo_l = (const float*)(c.smem + S::WBUF);  // Wout rows [adim][H]
-  float* win_t = (float*)(c.smem + S::SMALL);            // Win tile [adim][16]
+  float* win_t = (float*)(c.smem + S::SMALL);            // Win columns of the task [adim][32]
   const int sn = d.first ? 0 : d.s + 1;
-  // task t runs on workgroup G - 1 - t: the top of the grid, mostly idle in the down projection before it
-  for (int t = c.G - 1 - c.wg; t < nin + nout; t += c.G) {
-    if (t != c.G - 1 - c.wg) __syncthreads();  // the previous task's LDS (the first task's is free already)
+  // this workgroup's tasks: its in-projection task (k = 0), then its output-dim tasks (reducer r: r + NRED j)
+  const int tin = tail_in_task<S>(c.G, c.wg), red = reducer_of<S>(c.G, c.wg);
+  bool first_task = true;
+  for (int k = 0; k <= (p.A + S::NRED - 1) / S::NRED; ++k) {
+    int t = -1;
+    if (k == 0) t = tin < nin ? tin : -1;
+    else if (red >= 0 && red < S::NRED && red + (k - 1) * S::NRED < nout) t = nin + red + (k - 1) * S::NRED;
+    if (t < 0) continue;
+    if (!first_task) __syncthreads();  // the previous task's LDS (the first task's is free already)
+    first_task = false;
     const bool inproj = t < nin;
     const int a_out = t - nin;
-    // in-projection item of this thread (first pass): row, 4-column piece q of tile t; its constant operands
-    const int row0 = c.tid >> 2, q0 = c.tid & 3;
+    // in-projection item of this thread (first pass): row, 4-column piece q of the task's 32 columns; its
+    // constant operands
+    const int row0 = c.tid >> 3, q0 = c.tid & 7;
     f32x4 sc0 = {0.f, 0.f, 0.f, 0.f}, bv0 = {0.f, 0.f, 0.f, 0.f};
     uint2 rg0 = {0u, 0u};
     f32x4 wt = {0.f, 0.f, 0.f, 0.f};
     if (inproj) {
-      const int b = row0 / p.Mqp, i = row0 - b * p.Mqp, col = t * 16 + 4 * q0;
+      const int b = row0 / p.Mqp, i = row0 - b * p.Mqp, col = t * 32 + 4 * q0;
       if (row0 < p.NRP) {
         sc0 = ldf4(c.modrow(min(b, p.B - 1), sn) + col);  // layer 0 self-attention AdaRMS scale
         if (b < p.B && i < p.T) bv0 = ldf4(p.bin + col);
         else if (b < p.B && i < p.Mq) rg0 = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
       }
-      if (c.tid < adim * 4) wt = ldf4(p.win + (long long)(c.tid >> 2) * S::H + t * 16 + 4 * (c.tid & 3));
+      if (c.tid < adim * 8) wt = ldf4(p.win + (long long)(c.tid >> 3) * S::H + t * 32 + 4 * (c.tid & 7));
     }
     if (!d.first) {
-      // every tile of the last layer's output, and x of this step (the previous step tail's output dims)
-      flag_wait(bc, F_DOWN, S::HT, [](int i) { return i; }, (unsigned long long)g);
+      // every tile of the last layer's output (its reducers), and x of this step (the previous step tail's
+      // output dims)
+      flag_wait(bc, F_DOWN, S::NRED, [](int i) { return i; }, (unsigned long long)g);
       if (d.s > 0) flag_wait(bc, F_TAIL_OUT, p.A, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
     }
     // the staged final modulation rows and Wout rows (DMA'd by the prefetch) have landed
@@ -1514,14 +1539,15 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       }
     }
     if (inproj) {
-      if (c.tid < adim * 4) *reinterpret_cast<f32x4*>(win_t + (c.tid >> 2) * 16 + 4 * (c.tid & 3)) = wt;
+      if (c.tid < adim * 8) *reinterpret_cast<f32x4*>(win_t + (c.tid >> 3) * 32 + 4 * (c.tid & 7)) = wt;
       __syncthreads();
       MKX_TR(c, 1);
       float* h0n = c.h0(sn);
-      for (int it = c.tid; it < p.NRP * 4; it += NTHREADS) {
-        const int row = it >> 2, q = it & 3;
+      // item: row, 4-column piece q of the task's tiles 2 t (q < 4) and 2 t + 1
+      for (int it = c.tid; it < p.NRP * 8; it += NTHREADS) {
+        const int row = it >> 3, q = it & 7;
         const int b = row / p.Mqp, i = row - b * p.Mqp;
-        const int col = t * 16 + 4 * q;
+        const int col = t * 32 + 4 * q;
         f32x4 v, sc;
         uint2 rg;
         if (it == c.tid) {
@@ -1537,7 +1563,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
         }
         if (b < p.B && i < p.T) {
           const float* xr = xp + (b * p.T + i) * adim;
-          for (int a = 0; a < adim; ++a) v += xr[a] * ldf4(win_t + a * 16 + 4 * q);
+          for (int a = 0; a < adim; ++a) v += xr[a] * ldf4(win_t + a * 32 + 4 * q);
         } else if (b < p.B && i < p.Mq) {
           v = f32x4{__uint_as_float(rg.x << 16), __uint_as_float(rg.x & 0xffff0000u), __uint_as_float(rg.y << 16),
                     __uint_as_float(rg.y & 0xffff0000u)};
@@ -1545,8 +1571,8 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
         st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
         st_split4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc));
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-        ss = quad_sum(ss);
-        if (q == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, t, S::HT), __float_as_uint(ss));
+        ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
+        if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, 2 * t + (q >> 2), S::HT), __float_as_uint(ss));
       }
     }
     flag_publish(bc, inproj ? F_TAIL_IN : F_TAIL_OUT, inproj ? t : a_out, (unsigned long long)g + 1);
@@ -1571,14 +1597,21 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
       else ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);
     }
   } else if (d.st == ST_TAIL) {
-    if (!d.first && c.G - 1 - t < (d.last ? 0 : S::HT) + p.A) {
+    // workgroups with a tail task: the in-projection tasks and the reducers (output dims)
+    const int red = reducer_of<S>(c.G, t);
+    if (!d.first && (tail_in_task<S>(c.G, t) < (d.last ? 0 : S::NIN) || (red >= 0 && red < S::NRED && red < p.A))) {
       for (int b = 0; b < p.B; ++b) dma_f32(c, mb + b * 2 * S::H * 4, c.modrow(b, d.s) + 9 * p.L * S::H, 2 * S::H);
       dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
     }
-  } else if (t < d.ntask) {
-    dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
-    MKX_TRW(c, 9);
-    if (d.kind == K_RES || d.kind == K_SPLIT) {  // gate and the next AdaRMS scale
+  } else {
+    if (t < d.ntask) {
+      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
+      MKX_TRW(c, 9);
+    }
+    // gate and the next AdaRMS scale: the residual stages' tasks, and the down projection's reducers (its
+    // split tasks only store partial sums)
+    const int red = reducer_of<S>(c.G, t);
+    if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && red >= 0 && red < S::NRED)) {
       for (int b = 0; b < p.B; ++b) {
         const float* mr = c.modrow(b, d.s);
         dma_f32(c, mb + b * 2 * S::H * 4, mr + d.mod_off, S::H);
@@ -1625,7 +1658,6 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   bc.flags = p.flags;
   // one agent-scope acquire per launch: no cache of this XCD holds lines from before the launch
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  if (c.wg == 0 && c.tid < S::HT) __hip_atomic_store(&p.dcnt[c.tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (p.profile && c.wg == 0 && c.tid == 0) p.prof[0] = clock100() * 10;
 
