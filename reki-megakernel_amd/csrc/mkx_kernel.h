@@ -298,6 +298,13 @@ template <class S>
 __device__ __forceinline__ int tail_in_task(int G, int wg) { return G - 1 - wg; }
 template <class S>
 __device__ __forceinline__ int reducer_of(int G, int wg) { return G - 1 - S::NIN - wg; }
+// the step tail's output task of workgroup wg (valid when below the task count): on the lowest reducers,
+// which host no self-attention task of the next step
+template <class S>
+__device__ __forceinline__ int tail_out_task(int G, int wg) {
+  const int r = reducer_of<S>(G, wg);
+  return r >= 0 && r < S::NRED ? S::NRED - 1 - r : 1 << 30;
+}
 
 // ------------------------------------------------------------------------------------------------
 // Stage descriptor: what one stage computes, where its operands live, and what to prefetch for it.
@@ -1369,11 +1376,11 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 // h0' = x'_real Win + bin (action rows), register tokens (register rows), all fp32; with h0' its layer-0
 // AdaRMS operand y0' = h0' (1 + scale) (split) and sums of squares. Tasks [0, NIN): in-projection tasks of
 // two 16-column tiles (each recomputes the velocity of the real action dims), on the NIN highest workgroups;
-// tasks [NIN, NIN + A): one output dim each, on the down projection's reducers (nothing waits for them
-// before the next step tail). Wave w takes the action rows w + 4 k, TAIL_RPW of them per batch with their loads
-// issued together; lane owns the 4-column pieces 4 (lane + 64 q). The final modulation rows and Wout's
-// real-dim rows were staged in LDS by the prefetch; the in-projection's constant operands (Win tile, bias,
-// register tokens, layer-0 scale) are loaded with the first batch.
+// then A / TAIL_AC output tasks of TAIL_AC dims each (x after the step, which only the next step tail
+// reads), on reducers of the down projection. Wave w takes the action rows w + 4 k, TAIL_RPW of them per
+// batch with their loads issued together; lane owns the 4-column pieces 4 (lane + 64 q). The final
+// modulation rows and the task's Wout rows were staged in LDS by the prefetch; the in-projection's constant
+// operands (Win columns, bias, register tokens, layer-0 scale) are loaded with the first batch.
 constexpr int TAIL_RPW = 3;  // action rows per wave and batch
 constexpr int TAIL_AC = 8;   // action dims reduced together
 
@@ -1389,7 +1396,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   constexpr int NP = S::H / 256;  // pieces per lane
   constexpr int R = TAIL_RPW;
   const int nin = d.last ? 0 : S::NIN;
-  const int nout = d.first ? 0 : p.A;
+  const int nout = d.first ? 0 : (p.A + TAIL_AC - 1) / TAIL_AC;
   const int nrows = p.B * p.T;
   const int adim = p.action_dim;
   const float* xcur = (d.first || d.s == 0) ? p.x_in : c.xstep(d.s);
@@ -1398,13 +1405,13 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   const float* wo_l = (const float*)(c.smem + S::WBUF);  // Wout rows [adim][H]
   float* win_t = (float*)(c.smem + S::SMALL);            // Win columns of the task [adim][32]
   const int sn = d.first ? 0 : d.s + 1;
-  // this workgroup's tasks: its in-projection task (k = 0), then its output-dim tasks (reducer r: r + NRED j)
-  const int tin = tail_in_task<S>(c.G, c.wg), red = reducer_of<S>(c.G, c.wg);
+  // this workgroup's tasks: its in-projection task (k = 0), then its output task
+  const int tin = tail_in_task<S>(c.G, c.wg), tout = tail_out_task<S>(c.G, c.wg);
   bool first_task = true;
-  for (int k = 0; k <= (p.A + S::NRED - 1) / S::NRED; ++k) {
+  for (int k = 0; k < 2; ++k) {
     int t = -1;
     if (k == 0) t = tin < nin ? tin : -1;
-    else if (red >= 0 && red < S::NRED && red + (k - 1) * S::NRED < nout) t = nin + red + (k - 1) * S::NRED;
+    else t = tout < nout ? nin + tout : -1;
     if (t < 0) continue;
     if (!first_task) __syncthreads();  // the previous task's LDS (the first task's is free already)
     first_task = false;
@@ -1429,22 +1436,19 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       // every tile of the last layer's output (its reducers), and x of this step (the previous step tail's
       // output dims)
       flag_wait(bc, F_DOWN, S::NRED, [](int i) { return i; }, (unsigned long long)g);
-      if (d.s > 0) flag_wait(bc, F_TAIL_OUT, p.A, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
+      if (d.s > 0) flag_wait(bc, F_TAIL_OUT, nout, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
     }
     // the staged final modulation rows and Wout rows (DMA'd by the prefetch) have landed
     wait_vm0();
     __syncthreads();
     MKX_TR(c, 0);
     if (!d.first) {
-      f32x4 wa[NP];
-      if (!inproj) {
-#pragma unroll
-        for (int q = 0; q < NP; ++q) wa[q] = ldf4(p.wout + (long long)a_out * S::H + 4 * (c.lane + 64 * q));
-      }
       const __amdgpu_buffer_rsrc_t rh = rsrc(hL);
-      // lane a < A holds bout[a]; with xc[k] below (x of row k, dim lane) the in-projection's x' is formed by
-      // the lanes of its dims
+      // dims [a_lo, a_hi) of this task (Wout rows staged in LDS from row a_lo): the in-projection's real dims,
+      // or an output task's TAIL_AC dims. Lane a holds bout[a] and, in xc[k], x of row k's dim a.
+      const int a_lo = inproj ? 0 : a_out * TAIL_AC, a_hi = inproj ? adim : min(a_lo + TAIL_AC, p.A);
       const float bo = p.bout[min(c.lane, p.A - 1)];
+      float* xn = d.last ? p.x_out : c.xstep(d.s + 1);
       for (int r0 = c.wave; r0 < nrows; r0 += NWAVES * R) {
         f32x4 x[R][NP];
         float xc[R];
@@ -1454,7 +1458,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
           const int b = ri / p.T, grow = b * p.Mqp + (ri - b * p.T);
 #pragma unroll
           for (int q = 0; q < NP; ++q) x[k][q] = as_f4(bload(rh, fpiece(grow, 4 * (c.lane + 64 * q), c.RT), 0));
-          xc[k] = xcur[(long long)ri * p.A + (inproj ? min(c.lane, p.A - 1) : a_out)];
+          xc[k] = xcur[(long long)ri * p.A + min(c.lane, p.A - 1)];
         }
         float ss[R];
 #pragma unroll
@@ -1475,58 +1479,42 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
             x[k][q] = x[k][q] * rs * (1.0f + ldf4(ml + col)) + ldf4(ml + S::H + col);
           }
         }
-        if (inproj) {
-          for (int a0 = 0; a0 < adim; a0 += TAIL_AC) {
-            float dd[TAIL_AC * R];
+        for (int a0 = a_lo; a0 < a_hi; a0 += TAIL_AC) {
+          float dd[TAIL_AC * R];
 #pragma unroll
-            for (int j = 0; j < TAIL_AC; ++j) {
-              const int a = min(a0 + j, adim - 1);
+          for (int j = 0; j < TAIL_AC; ++j) {
+            const int a = min(a0 + j, a_hi - 1);
 #pragma unroll
-              for (int k = 0; k < R; ++k) dd[j * R + k] = 0.f;
+            for (int k = 0; k < R; ++k) dd[j * R + k] = 0.f;
 #pragma unroll
-              for (int q = 0; q < NP; ++q) {
-                const f32x4 w = ldf4(wo_l + a * S::H + 4 * (c.lane + 64 * q));
+            for (int q = 0; q < NP; ++q) {
+              const f32x4 w = ldf4(wo_l + (a - a_lo) * S::H + 4 * (c.lane + 64 * q));
 #pragma unroll
-                for (int k = 0; k < R; ++k)
-                  dd[j * R + k] += x[k][q][0] * w[0] + x[k][q][1] * w[1] + x[k][q][2] * w[2] + x[k][q][3] * w[3];
-              }
-            }
-            wave_sum_n<TAIL_AC * R>(dd);
-            float sel[R];
-#pragma unroll
-            for (int k = 0; k < R; ++k) sel[k] = 0.f;
-#pragma unroll
-            for (int j = 0; j < TAIL_AC; ++j)
-              if (c.lane == a0 + j) {
-#pragma unroll
-                for (int k = 0; k < R; ++k) sel[k] = dd[j * R + k];
-              }
-            if (c.lane >= a0 && c.lane < min(a0 + TAIL_AC, adim)) {
-#pragma unroll
-              for (int k = 0; k < R; ++k) {
-                const int ri = r0 + NWAVES * k;
-                if (ri < nrows) xp[ri * adim + c.lane] = xc[k] + c.dt * (sel[k] + bo);
-              }
+              for (int k = 0; k < R; ++k)
+                dd[j * R + k] += x[k][q][0] * w[0] + x[k][q][1] * w[1] + x[k][q][2] * w[2] + x[k][q][3] * w[3];
             }
           }
-        } else {
-          float dd[R];
+          wave_sum_n<TAIL_AC * R>(dd);
+          float sel[R];
 #pragma unroll
-          for (int k = 0; k < R; ++k) {
-            dd[k] = 0.f;
+          for (int k = 0; k < R; ++k) sel[k] = 0.f;
 #pragma unroll
-            for (int q = 0; q < NP; ++q)
-              dd[k] += x[k][q][0] * wa[q][0] + x[k][q][1] * wa[q][1] + x[k][q][2] * wa[q][2] + x[k][q][3] * wa[q][3];
-          }
-          wave_sum_n<R>(dd);
-          if (c.lane == 0) {
-            float* xn = d.last ? p.x_out : c.xstep(d.s + 1);
+          for (int j = 0; j < TAIL_AC; ++j)
+            if (c.lane == a0 + j) {
+#pragma unroll
+              for (int k = 0; k < R; ++k) sel[k] = dd[j * R + k];
+            }
+          if (c.lane >= a0 && c.lane < min(a0 + TAIL_AC, a_hi)) {
 #pragma unroll
             for (int k = 0; k < R; ++k) {
               const int ri = r0 + NWAVES * k;
-              if (ri < nrows) {
-                const float xa = a_out < adim ? xc[k] : 0.f;
-                st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + a_out) * 4), __float_as_uint(xa + c.dt * (dd[k] + p.bout[a_out])));
+              if (ri >= nrows) continue;
+              if (inproj) {
+                xp[ri * adim + c.lane] = xc[k] + c.dt * (sel[k] + bo);
+              } else {
+                // x after the step: x + dt v on the real dims, dt v on the padded ones
+                const float xa = c.lane < adim ? xc[k] : 0.f;
+                st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + c.lane) * 4), __float_as_uint(xa + c.dt * (sel[k] + bo)));
               }
             }
           }
@@ -1597,11 +1585,14 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
       else ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);
     }
   } else if (d.st == ST_TAIL) {
-    // workgroups with a tail task: the in-projection tasks and the reducers (output dims)
-    const int red = reducer_of<S>(c.G, t);
-    if (!d.first && (tail_in_task<S>(c.G, t) < (d.last ? 0 : S::NIN) || (red >= 0 && red < S::NRED && red < p.A))) {
+    // workgroups with a tail task: the final modulation rows, and the Wout rows of the task's dims (the real
+    // dims for an in-projection task)
+    const int tout = tail_out_task<S>(c.G, t);
+    const bool tin = tail_in_task<S>(c.G, t) < (d.last ? 0 : S::NIN);
+    if (!d.first && (tin || tout < (p.A + TAIL_AC - 1) / TAIL_AC)) {
       for (int b = 0; b < p.B; ++b) dma_f32(c, mb + b * 2 * S::H * 4, c.modrow(b, d.s) + 9 * p.L * S::H, 2 * S::H);
-      dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
+      if (tin) dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
+      else dma_f32(c, c.smem + S::WBUF, p.wout + (long long)tout * TAIL_AC * S::H, min(TAIL_AC, p.A - tout * TAIL_AC) * S::H);
     }
   } else {
     if (t < d.ntask) {
