@@ -96,6 +96,17 @@ def test_batch_of_two_independent_chunks():
     _check_loop("A batch 2", case)
 
 
+def test_config_B_batch_of_eight():
+    # eight independent chunks (M = 8 x 48 rows): several row groups per tile in every GEMM stage
+    _check_loop("B (b8)", make_case(SY.WORKLOADS["B"]))
+
+
+def test_wide_expert_D_shape_bf16():
+    # the wide expert's shape (L16 H1024 NH16 I4096, 50 action + 32 register rows) with bf16 weights
+    from dataclasses import replace
+    _check_loop("D shape, bf16 weights", make_case(replace(SY.WORKLOADS["D"], weight_dtype="bf16")))
+
+
 def test_long_context_C():
     _check_loop("C (S 1024, PM 256)", make_case(SY.WORKLOADS["C"]))
 
