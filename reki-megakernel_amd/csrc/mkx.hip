@@ -51,17 +51,37 @@ __global__ void pack_tiles(const bf16_t* __restrict__ src, bf16_t* __restrict__ 
   *reinterpret_cast<u32x4*>(d) = *reinterpret_cast<const u32x4*>(s);
 }
 
+// The same chunk layout for e4m3 bytes: 8 bytes per lane, 512-byte chunks (dls, tstride in chunks).
+__global__ void pack_tiles8(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int L, int N, int K,
+                            long long dls, int tstride, int toff, int pairs) {
+  const long long total = (long long)L * (N / 16) * (K / 32) * 64;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int lane = (int)(i % 64);
+  long long r = i / 64;
+  const int kb = (int)(r % (K / 32));
+  r /= (K / 32);
+  const int t = (int)(r % (N / 16));
+  const int l = (int)(r / (N / 16));
+  const uint8_t* s = src + ((long long)l * N + t * 16 + lane % 16) * K + kb * 32 + 8 * (lane / 16);
+  const int tp = pairs ? ((t & ~3) | ((t & 1) << 1) | ((t >> 1) & 1)) : t;
+  uint8_t* d = dst + (l * dls + (long long)tp * tstride + toff + kb) * 512 + lane * 8;
+  *reinterpret_cast<uint2*>(d) = *reinterpret_cast<const uint2*>(s);
+}
+
 __global__ void xcc_probe(unsigned* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
 template <int H, int I>
-const void* kernel_of() { return reinterpret_cast<const void*>(&mkx_megakernel<H, I>); }
+const void* kernel_of(bool w8) {
+  return w8 ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true>) : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false>);
+}
 
-const void* pick_kernel(int H, int I) {
-  if (H == 768 && I == 3072) return kernel_of<768, 3072>();
-  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>();
-  if (H == 256 && I == 512) return kernel_of<256, 512>();
+const void* pick_kernel(int H, int I, bool w8) {
+  if (H == 768 && I == 3072) return kernel_of<768, 3072>(w8);
+  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>(w8);
+  if (H == 256 && I == 512) return kernel_of<256, 512>(w8);
   return nullptr;
 }
 
@@ -98,7 +118,9 @@ struct mkx_handle {
   unsigned nx[MAX_XCD] = {};
   unsigned xmask = 0;
   const void* kernel = nullptr;
-  bf16_t *wqkv = nullptr, *wo = nullptr, *wqca = nullptr, *woca = nullptr, *wgu = nullptr, *wd = nullptr;
+  char *wqkv = nullptr, *wo = nullptr, *wqca = nullptr, *woca = nullptr, *wgu = nullptr, *wd = nullptr;  // packed chunks
+  float* scales = nullptr;  // fp8: [L][3H] qkv | [L][H] o | [L][H] ca q | [L][H] ca o | [L][I] gate | [L][I] up | [L][H] down
+  int w8 = 0;
   bf16_t *qn = nullptr, *kn = nullptr, *qcan = nullptr;
   float *win = nullptr, *bin = nullptr, *wout = nullptr, *bout = nullptr;
   char* frames = nullptr;
@@ -121,7 +143,7 @@ struct mkx_handle {
 static void free_handle(mkx_handle* h) {
   if (!h) return;
   void* ptrs[] = {h->wqkv, h->wo, h->wqca, h->woca, h->wgu, h->wd, h->qn, h->kn, h->qcan, h->win, h->bin,
-                  h->wout, h->bout, h->frames, h->steps, h->vts, h->bar, h->flags};
+                  h->wout, h->bout, h->frames, h->steps, h->vts, h->bar, h->flags, h->scales};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete h;
@@ -154,19 +176,23 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   if (d.HD != HD) return fail(MKX_EUNSUPPORTED, "head dim must be 64");
   if (d.NH * d.HD != d.H) return fail(MKX_EINVAL, "H must equal NH * HD");
   if (d.A != 32) return fail(MKX_EUNSUPPORTED, "padded action width A must be 32");
-  if (d.weight_dtype != MKX_WEIGHTS_BF16) return fail(MKX_EUNSUPPORTED, "only bf16 weights are supported by this build");
+  if (d.weight_dtype != MKX_WEIGHTS_BF16 && d.weight_dtype != MKX_WEIGHTS_FP8_E4M3) return fail(MKX_EUNSUPPORTED, "unknown weight dtype");
+  const bool w8 = d.weight_dtype == MKX_WEIGHTS_FP8_E4M3;
   if (d.activation != MKX_ACT_SILU && d.activation != MKX_ACT_GELU_TANH) return fail(MKX_EINVAL, "unknown activation");
   if (d.max_batch < 1 || d.max_batch > MAX_BATCH) return fail(MKX_EINVAL, "max_batch must be in [1, 16]");
   if (d.max_rows < 1 || d.max_rows > 128) return fail(MKX_EINVAL, "max_rows (own rows per sample) must be in [1, 128]");
   if (d.max_mem_rows < 0 || d.max_mem_rows > 256) return fail(MKX_EINVAL, "max_mem_rows must be in [0, 256]");
-  const void* kern = pick_kernel(d.H, d.I);
+  const void* kern = pick_kernel(d.H, d.I, w8);
   if (!kern) return fail(MKX_EUNSUPPORTED, "no kernel instantiation for (H, I) = (" + std::to_string(d.H) + ", " + std::to_string(d.I) + ")");
   if (!w->wqkv || !w->wo || !w->wqca || !w->woca || !w->wg || !w->wu || !w->wd || !w->qn || !w->kn || !w->qcan ||
       !w->win || !w->bin || !w->wout || !w->bout)
     return fail(MKX_EINVAL, "null weight pointer");
+  if (w8 && (!w->wqkv_scale || !w->wo_scale || !w->wqca_scale || !w->woca_scale || !w->wg_scale || !w->wu_scale || !w->wd_scale))
+    return fail(MKX_EINVAL, "fp8 weights need every per-output-channel scale pointer");
   hipStream_t stream = (hipStream_t)stream_;
   mkx_handle* h = new mkx_handle();
   h->d = d;
+  h->w8 = w8 ? 1 : 0;
   h->kernel = kern;
   auto bail = [&](int code) { free_handle(h); return code; };
 #define HCHK(x)                                                                                       \
@@ -214,26 +240,43 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   const int L = d.L, H = d.H, I = d.I;
   auto alloc = [&](void** p, size_t bytes) { return hipMalloc(p, bytes); };
   const size_t sq = (size_t)L * 3 * H * H, so = (size_t)L * H * H, sgu = (size_t)L * 2 * I * H, sd = (size_t)L * H * I;
-  HCHK(alloc((void**)&h->wqkv, sq * 2));
-  HCHK(alloc((void**)&h->wo, so * 2));
-  HCHK(alloc((void**)&h->wqca, so * 2));
-  HCHK(alloc((void**)&h->woca, so * 2));
-  HCHK(alloc((void**)&h->wgu, sgu * 2));
-  HCHK(alloc((void**)&h->wd, sd * 2));
-  auto pack = [&](const void* src, bf16_t* dst, int N, int K, long long dls, int tstride, int toff, int pairs) {
+  const size_t wb = w8 ? 1 : 2;  // bytes per weight
+  HCHK(alloc((void**)&h->wqkv, sq * wb));
+  HCHK(alloc((void**)&h->wo, so * wb));
+  HCHK(alloc((void**)&h->wqca, so * wb));
+  HCHK(alloc((void**)&h->woca, so * wb));
+  HCHK(alloc((void**)&h->wgu, sgu * wb));
+  HCHK(alloc((void**)&h->wd, sd * wb));
+  // dls, tstride, toff in chunks (16 x 32 weights)
+  auto pack = [&](const void* src, char* dst, int N, int K, long long dls, int tstride, int toff, int pairs) {
     const long long total = (long long)L * (N / 16) * (K / 32) * 64;
-    hipLaunchKernelGGL(pack_tiles, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)src, dst,
-                       L, N, K, dls, tstride, toff, pairs);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (w8)
+      hipLaunchKernelGGL(pack_tiles8, grid, dim3(256), 0, stream, (const uint8_t*)src, (uint8_t*)dst, L, N, K, dls, tstride, toff, pairs);
+    else
+      hipLaunchKernelGGL(pack_tiles, grid, dim3(256), 0, stream, (const bf16_t*)src, (bf16_t*)dst, L, N, K, dls * 512, tstride, toff, pairs);
   };
-  pack(w->wqkv, h->wqkv, 3 * H, H, 3LL * H * H, H / 32, 0, 1);
-  pack(w->wo, h->wo, H, H, (long long)H * H, H / 32, 0, 0);
-  pack(w->wqca, h->wqca, H, H, (long long)H * H, H / 32, 0, 0);
-  pack(w->woca, h->woca, H, H, (long long)H * H, H / 32, 0, 0);
-  pack(w->wg, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), 0, 0);
-  pack(w->wu, h->wgu, I, H, 2LL * I * H, 2 * (H / 32), H / 32, 0);
-  pack(w->wd, h->wd, H, I, (long long)H * I, I / 32, 0, 0);
+  const int kbh = H / 32, kbi = I / 32;
+  pack(w->wqkv, h->wqkv, 3 * H, H, 3LL * (H / 16) * kbh, kbh, 0, 1);
+  pack(w->wo, h->wo, H, H, (long long)(H / 16) * kbh, kbh, 0, 0);
+  pack(w->wqca, h->wqca, H, H, (long long)(H / 16) * kbh, kbh, 0, 0);
+  pack(w->woca, h->woca, H, H, (long long)(H / 16) * kbh, kbh, 0, 0);
+  pack(w->wg, h->wgu, I, H, 2LL * (I / 16) * kbh, 2 * kbh, 0, 0);
+  pack(w->wu, h->wgu, I, H, 2LL * (I / 16) * kbh, 2 * kbh, kbh, 0);
+  pack(w->wd, h->wd, H, I, (long long)(H / 16) * kbi, kbi, 0, 0);
   HCHK(hipGetLastError());
-  h->weight_bytes = (long long)(sq + 3 * so + sgu + sd) * 2;
+  if (w8) {
+    const size_t n = (size_t)L * (3 * H + 3 * H + 2 * I + H);
+    HCHK(alloc((void**)&h->scales, n * 4));
+    float* sc = h->scales;
+    const float* src[7] = {w->wqkv_scale, w->wo_scale, w->wqca_scale, w->woca_scale, w->wg_scale, w->wu_scale, w->wd_scale};
+    const size_t len[7] = {(size_t)3 * H, (size_t)H, (size_t)H, (size_t)H, (size_t)I, (size_t)I, (size_t)H};
+    for (int k = 0; k < 7; ++k) {
+      HCHK(hipMemcpyAsync(sc, src[k], (size_t)L * len[k] * 4, hipMemcpyDeviceToDevice, stream));
+      sc += (size_t)L * len[k];
+    }
+  }
+  h->weight_bytes = (long long)(sq + 3 * so + sgu + sd) * (long long)wb;
   HCHK(alloc((void**)&h->qn, (size_t)L * HD * 2));
   HCHK(alloc((void**)&h->kn, (size_t)L * HD * 2));
   HCHK(alloc((void**)&h->qcan, (size_t)L * HD * 2));
@@ -357,7 +400,14 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   Params p;
   std::memset(&p, 0, sizeof(p));
   p.wqkv = h->wqkv; p.wo = h->wo; p.wqca = h->wqca; p.woca = h->woca; p.wgu = h->wgu; p.wd = h->wd;
-  p.s_qkv = 3LL * H * H; p.s_o = (long long)H * H; p.s_gu = 2LL * I * H; p.s_d = (long long)H * I;
+  const long long wb = h->w8 ? 1 : 2;
+  p.s_qkv = 3LL * H * H * wb; p.s_o = (long long)H * H * wb; p.s_gu = 2LL * I * H * wb; p.s_d = (long long)H * I * wb;
+  {
+    const float* sc = h->scales;  // null for bf16
+    auto take = [&](size_t n) { const float* r = sc; if (sc) sc += (size_t)L * n; return r; };
+    p.sc_qkv = take(3 * H); p.sc_o = take(H); p.sc_qca = take(H); p.sc_oca = take(H);
+    p.sc_g = take(I); p.sc_u = take(I); p.sc_d = take(H);
+  }
   p.qn = h->qn; p.kn = h->kn; p.qcan = h->qcan;
   p.win = h->win; p.bin = h->bin; p.wout = h->wout; p.bout = h->bout;
   p.x_in = a->x_in; p.x_out = a->x_out;

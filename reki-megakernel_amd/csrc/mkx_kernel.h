@@ -48,8 +48,11 @@ namespace mkx {
 
 struct Params {
   // packed weights; per-layer strides in elements
-  const bf16_t* wqkv; const bf16_t* wo; const bf16_t* wqca; const bf16_t* woca; const bf16_t* wgu; const bf16_t* wd;
-  long long s_qkv, s_o, s_gu, s_d;
+  const char* wqkv; const char* wo; const char* wqca; const char* woca; const char* wgu; const char* wd;
+  long long s_qkv, s_o, s_gu, s_d;  // bytes per layer
+  // fp8 weights: per-output-channel scales, [L][3H] (q;k;v), [L][H], [L][H], [L][H], [L][I] (gate), [L][I]
+  // (up), [L][H] (down); null for bf16 weights
+  const float* sc_qkv; const float* sc_o; const float* sc_qca; const float* sc_oca; const float* sc_g; const float* sc_u; const float* sc_d;
   const bf16_t* qn; const bf16_t* kn; const bf16_t* qcan;  // [L][64]
   const float* win; const float* bin; const float* wout; const float* bout;  // [A][H], [H], [A][H], [A]
   // call inputs
@@ -85,9 +88,13 @@ typedef const __attribute__((address_space(4))) Params CP;
 
 __host__ __device__ constexpr int ceil_to(int a, int m) { return (a + m - 1) / m * m; }
 
-template <int H_, int I_>
+template <int H_, int I_, bool W8_ = false>
 struct Shape {
   static constexpr int H = H_, I = I_, NH = H / HD, NKB = H / 32, HT = H / 16, IT = I / 16, SK = I / H;
+  // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): bf16, or fp8
+  // e4m3 converted to bf16 fragments when read (weight-only quantisation; the activations stay split bf16)
+  static constexpr bool W8 = W8_;
+  static constexpr int CH = W8 ? 512 : 1024;  // bytes per chunk
   static constexpr int KPW = NKB / NWAVES;  // 32-wide k-blocks per wave
   static constexpr int WBUF = 0, WBUF_BYTES = 64 * 1024;
   static constexpr int ABUF = WBUF_BYTES, ABUF_BYTES = 88 * 1024;
@@ -106,7 +113,7 @@ struct Shape {
   static_assert(H % 256 == 0 && I % H == 0, "H must be a multiple of 256 and I a multiple of H");
   static_assert(HT % NRED == 0 && TPR * SK <= 256, "each reducer waits on at most 256 partial tasks");
   static_assert(KPW >= 1 && RBMAX >= 1, "tile does not fit registers");
-  static_assert(NKB * 1024 * 2 <= WBUF_BYTES, "gate/up weight tile pair must fit the weight buffer");
+  static_assert(NKB * CH * 2 <= WBUF_BYTES, "gate/up weight tile pair must fit the weight buffer");
   static_assert(NWAVES * (RBMAX + 1) * 2 * 1024 <= RED_BYTES, "cross-wave reduction must fit LDS");
   static_assert(LDS <= 160 * 1024 - 256, "LDS budget");
   // frame layout (bytes), buffers of NRP rows; HB = NRP * H * 4:
@@ -221,9 +228,10 @@ __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 __device__ __forceinline__ f32x4 as_f4(u32x4 v) { return __builtin_bit_cast(f32x4, v); }
 __device__ __forceinline__ u32x4 as_u4(f32x4 v) { return __builtin_bit_cast(u32x4, v); }
 
+// nbytes (a multiple of 1 KB) of packed weight chunks into LDS
 template <class S>
-__device__ __forceinline__ void dma_w(Ctx<S>& c, char* dst, const bf16_t* src, int nchunks) {
-  for (int k = c.dw; k < nchunks; k += c.dn) dma16(src + (long long)k * 512 + c.lane * 8, dst + k * 1024);
+__device__ __forceinline__ void dma_w(Ctx<S>& c, char* dst, const char* src, int nbytes) {
+  for (int k = c.dw; k < nbytes / 1024; k += c.dn) dma16(src + (long long)k * 1024 + c.lane * 16, dst + k * 1024);
 }
 // nfloats (a multiple of 256) contiguous fp32 values into LDS
 template <class S>
@@ -247,6 +255,30 @@ __device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
   }
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);
+}
+// 8 e4m3 values (OCP fp8, as the weights are quantised) -> 8 bf16, exactly (v_cvt_pk_f32_fp8 decodes OCP
+// e4m3 on gfx950; every e4m3 value is a bf16 value)
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint2 v) {
+  const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.x, true);
+  const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.y, true);
+  u32x4 r;
+  r[0] = cvt_pk(a[0], a[1]);
+  r[1] = cvt_pk(b[0], b[1]);
+  r[2] = cvt_pk(c[0], c[1]);
+  r[3] = cvt_pk(d[0], d[1]);
+  return __builtin_bit_cast(bf16x8, r);
+}
+// this lane's weight operand fragment of a packed chunk in LDS (chunk = its first byte)
+template <class S>
+__device__ __forceinline__ bf16x8 wfrag_lds(const char* chunk, int lane) {
+  if constexpr (S::W8) return fp8x8_to_bf16(*reinterpret_cast<const uint2*>(chunk + lane * 8));
+  else return *reinterpret_cast<const bf16x8*>(chunk + lane * 16);
+}
+// the same from global memory
+template <class S>
+__device__ __forceinline__ bf16x8 wfrag_glb(const char* chunk, int lane) {
+  if constexpr (S::W8) return fp8x8_to_bf16(*reinterpret_cast<const uint2*>(chunk + lane * 8));
+  else return __builtin_bit_cast(bf16x8, ld16(chunk + lane * 16));
 }
 __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
 #pragma unroll
@@ -313,7 +345,8 @@ struct Desc {
   int st, s, l;
   bool first, last;
   // GEMM stages
-  const bf16_t* w; long long wstride;  // packed weight chunks; tile t at w + t * wstride (not split)
+  const char* w; long long wstride;    // packed weight chunks; tile t at w + t * wstride bytes (not split)
+  const float* sc; const float* sc2;   // fp8 weights: the layer's output-channel scales (gate/up: sc2 = up)
   const float* a;                      // split operand frame
   float* out; const float* res; float* part;
   float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
@@ -333,6 +366,7 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
   d.first = g == 0;
   d.last = false;
   d.w = nullptr; d.wstride = 0; d.a = nullptr; d.out = nullptr; d.res = nullptr; d.part = nullptr;
+  d.sc = nullptr; d.sc2 = nullptr;
   d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr; d.shs = nullptr;
   d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.mod_off = 0; d.mod_off2 = 0; d.rgs = 1;
   if (g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
@@ -351,32 +385,37 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
   // AdaRMS slices of a layer's mods row (src/mk_expert.py:302-426): [scale | shift | gate] for self-attention,
   // cross-attention and the MLP; the next layer's (or the final) AdaRMS scale follows at 9 (l + 1) H
   const int m_sa = 9 * l * S::H, m_ca = m_sa + 3 * S::H, m_mlp = m_sa + 6 * S::H, m_next = m_sa + 9 * S::H;
-  d.wstride = (long long)S::NKB * 512;
+  d.wstride = (long long)S::NKB * S::CH;
   const char* shs = p.shs + (long long)(d.s * p.L + l) * 3 * p.B * S::H * 4;
   switch (d.st) {
     case ST_QKV:  // task ((kind * NH + head) * 2 + j): columns 16 j + [0, 16) and 16 j + 32 + [0, 16) of the head
-      d.w = p.wqkv + l * p.s_qkv; d.wstride = 2LL * S::NKB * 512; d.a = c.y_in(d.s, l); d.ssin = c.ss_in(d.s, l);
+      d.w = p.wqkv + l * p.s_qkv; d.wstride = 2LL * S::NKB * S::CH; d.a = c.y_in(d.s, l); d.ssin = c.ss_in(d.s, l);
+      if (S::W8) d.sc = p.sc_qkv + (long long)l * 3 * S::H;
       d.out = (float*)(fr + S::qs_off(NRP)); d.yout = (float*)(fr + S::ks_off(NRP)); d.part = (float*)(fr + S::vtb_off(NRP));
       d.ssout = (float*)(fr + S::ssqk_off(NRP)); d.ntask = d.tiles = 6 * S::NH; d.nt = 2; d.shs = shs;
       break;
     case ST_O:
       d.w = p.wo + l * p.s_o; d.a = (const float*)(fr + S::ysa_off(NRP)); d.out = (float*)(fr + S::h2_off(NRP));
+      if (S::W8) d.sc = p.sc_o + (long long)l * S::H;
       d.yout = (float*)(fr + S::y2_off(NRP)); d.ssout = (float*)(fr + S::ss2_off(NRP));
       d.res = c.h_in(d.s, l); d.ntask = d.tiles = S::HT; d.kind = K_RES; d.mod_off = m_sa + 2 * S::H; d.mod_off2 = m_ca;
       break;
     case ST_CAO:
       d.w = p.woca + l * p.s_o; d.a = (const float*)(fr + S::yca_off(NRP)); d.out = (float*)(fr + S::h3_off(NRP));
+      if (S::W8) d.sc = p.sc_oca + (long long)l * S::H;
       d.yout = (float*)(fr + S::y3_off(NRP)); d.ssout = (float*)(fr + S::ss3_off(NRP));
       d.res = (const float*)(fr + S::h2_off(NRP)); d.ntask = d.tiles = S::HT; d.kind = K_RES;
       d.mod_off = m_ca + 2 * S::H; d.mod_off2 = m_mlp;
       break;
     case ST_GU:
-      d.w = p.wgu + l * p.s_gu; d.wstride = 2LL * S::NKB * 512; d.a = (const float*)(fr + S::y3_off(NRP));
+      d.w = p.wgu + l * p.s_gu; d.wstride = 2LL * S::NKB * S::CH; d.a = (const float*)(fr + S::y3_off(NRP));
+      if (S::W8) { d.sc = p.sc_g + (long long)l * S::I; d.sc2 = p.sc_u + (long long)l * S::I; }
       d.ssin = (const float*)(fr + S::ss3_off(NRP)); d.out = (float*)(fr + S::g_off(NRP));
       d.ntask = d.tiles = S::IT; d.kind = K_GU; d.nt = 2; d.shs = shs + 2 * p.B * S::H * 4;
       break;
     case ST_DOWN:
       d.w = p.wd + l * p.s_d; d.a = (const float*)(fr + S::g_off(NRP)); d.out = (float*)(fr + S::hl_off(NRP));
+      if (S::W8) d.sc = p.sc_d + (long long)l * S::H;
       d.yout = (float*)(fr + S::yl_off(NRP)); d.ssout = (float*)(fr + S::ssl_off(NRP));
       d.res = (const float*)(fr + S::h3_off(NRP)); d.part = (float*)(fr + S::part_off(NRP));
       d.tiles = S::HT; d.ntask = S::HT * S::SK; d.kind = K_SPLIT; d.mod_off = m_mlp + 2 * S::H; d.mod_off2 = m_next;
@@ -392,8 +431,8 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
 }
 
 template <class S>
-__device__ __forceinline__ const bf16_t* wtile(const Desc& d, int t) {
-  if (d.kind == K_SPLIT) return d.w + ((long long)(t % d.tiles) * S::SK + t / d.tiles) * S::NKB * 512;
+__device__ __forceinline__ const char* wtile(const Desc& d, int t) {
+  if (d.kind == K_SPLIT) return d.w + ((long long)(t % d.tiles) * S::SK + t / d.tiles) * S::NKB * S::CH;
   return d.w + (long long)(t % d.tiles) * d.wstride;
 }
 
@@ -439,6 +478,7 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
 struct EpiPre {
   f32x4 c0, s0, c1, s1;
   uint2 w0, w1;
+  f32x4 sa, sb;  // fp8 weights: output-channel scales of the item's columns (V tasks: one per 16-column tile)
 };
 
 template <class S>
@@ -459,6 +499,25 @@ __device__ __forceinline__ EpiPre epi_preload(Ctx<S>& c, const Desc& d, int kind
     e.s0 = ldf4(sn);
     e.c1 = ldf4(cs + 32);
     e.s1 = ldf4(sn + 32);
+  }
+  if constexpr (S::W8) {
+    // K_RES / K_GU: columns tile * 16 + 4 (L / 16) + 0..3 (gate/up: sa gate, sb up); q, k: d0 and d0 + 32 of
+    // the head; v: column 16 j + L % 16 (+ 32 for the second tile) of the head
+    if (d.kind == K_RES) {
+      e.sa = ldf4(d.sc + tile * 16 + 4 * (L >> 4));
+    } else if (d.kind == K_GU) {
+      e.sa = ldf4(d.sc + tile * 16 + 4 * (L >> 4));
+      e.sb = ldf4(d.sc2 + tile * 16 + 4 * (L >> 4));
+    } else if (d.kind == K_QKV) {
+      const float* sq = d.sc + kind * S::H + ((tile >> 1) % S::NH) * HD;
+      if (kind < 2) {
+        e.sa = ldf4(sq + 16 * j + 4 * (L >> 4));
+        e.sb = ldf4(sq + 16 * j + 4 * (L >> 4) + 32);
+      } else {
+        e.sa[0] = sq[16 * j + (L & 15)];
+        e.sa[1] = sq[16 * j + (L & 15) + 32];
+      }
+    }
   }
   return e;
 }
@@ -490,13 +549,13 @@ __device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int
 template <class S, int NRT, int NT, bool SWAP, bool ADA>
 __device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][2][2], const bf16x8 (&ah)[NRT][S::KPW],
                                          const bf16x8 (&al)[NRT][S::KPW], const bf16x8 (&sh_h)[S::KPW],
-                                         const bf16x8 (&sh_l)[S::KPW], const char* wl, int wave) {
+                                         const bf16x8 (&sh_l)[S::KPW], const char* wl, int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < S::KPW; ++i) {
     const int kb = wave + NWAVES * i;
     bf16x8 wf[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) wf[nt] = ldsfrag(wl + (nt * S::NKB + kb) * 1024);
+    for (int nt = 0; nt < NT; ++nt) wf[nt] = wfrag_lds<S>(wl + (nt * S::NKB + kb) * S::CH, lane);
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -578,10 +637,10 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   for (int rt = 0; rt <= NRT; ++rt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[rt][nt][0] = acc[rt][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const char* wl = c.smem + S::WBUF + c.lane * 16;
-  if (vtask) gemm_mma<S, NRT, 2, true, true>(acc, ah, al, sh_h, sh_l, wl, c.wave);
-  else if (d.nt == 2) gemm_mma<S, NRT, 2, false, true>(acc, ah, al, sh_h, sh_l, wl, c.wave);
-  else gemm_mma<S, NRT, 1, false, false>(acc, ah, al, sh_h, sh_l, wl, c.wave);
+  const char* wl = c.smem + S::WBUF;
+  if (vtask) gemm_mma<S, NRT, 2, true, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
+  else if (d.nt == 2) gemm_mma<S, NRT, 2, false, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
+  else gemm_mma<S, NRT, 1, false, false>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
   // cross-wave reduction through LDS (the shift tile at slot RB)
 #pragma unroll
   for (int rt = 0; rt <= NRT; ++rt)
@@ -634,6 +693,7 @@ __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc
     f32x4 v = as_f4(xp[0]);
 #pragma unroll
     for (int j = 1; j < S::SK; ++j) v += as_f4(xp[j]);
+    if (S::W8) v *= ldf4(d.sc + col);  // the output channel's scale
     res_piece(c, d, tile, row, col, L, v, res);
   }
   MKX_TR(c, 7);
@@ -659,7 +719,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     if (t != c.wg) {  // later tasks of this workgroup: load their weights now (the first was prefetched)
       wait_vm0();
       __syncthreads();
-      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
+      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB * S::CH);
     }
     const int kb0 = d.kind == K_SPLIT ? split * S::NKB : 0;
     const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
@@ -706,22 +766,27 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
               float bias = 0.f;
 #pragma unroll
               for (int w = 0; w < NWAVES; ++w) bias += ((const float*)(red + (((w * (RB + 1) + RB) * 2 + nt) * 64 + bl) * 16))[cl & 3];
+              const float sv = S::W8 ? epre.sa[nt] : 1.0f;  // fp8: the output channel's scale
               f32x4 x;
 #pragma unroll
-              for (int e = 0; e < 4; ++e) x[e] = ib + e < p.Mq ? a[e] * rs[e] + bias : 0.f;
+              for (int e = 0; e < 4; ++e) x[e] = ib + e < p.Mq ? (a[e] * rs[e] + bias) * sv : 0.f;
               st_split4(d.part, vo + (uint32_t)((qj + 2 * nt) * 2048), x);
             }
           } else if (d.kind == K_SPLIT) {
             st_sc1(d.part, (uint32_t)((((split * d.tiles + tile) * RT + rt0 + rt) * 64 + L) * 16), as_u4(v));
           } else if (d.kind == K_RES) {
-            res_piece(c, d, tile, row, col, L, v, epre.c0);
+            res_piece(c, d, tile, row, col, L, S::W8 ? v * epre.sa : v, epre.c0);
           } else {
             const int r = rt * 16 + (L & 15);
             const float tot = ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r];
             const float rs = rsqrtf(tot * (1.0f / (float)S::H) + p.eps);
             const int bl = c.sample_of(row) + 16 * (L >> 4);
             v = v * rs + wsum(RB, 0, bl);
-            const f32x4 u = wsum(rt, 1, L) * rs + wsum(RB, 1, bl);
+            f32x4 u = wsum(rt, 1, L) * rs + wsum(RB, 1, bl);
+            if (S::W8) {  // output-channel scales (the shift row tile used the same weights)
+              v *= epre.sa;
+              u *= epre.sb;
+            }
             if (d.kind == K_GU) {
 #pragma unroll
               for (int j = 0; j < 4; ++j) v[j] = act_fn(v[j], p.act) * u[j];
@@ -1185,7 +1250,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   const float* y2 = (const float*)(fr + S::y2_off(NRP));
   const float* ss2 = (const float*)(fr + S::ss2_off(NRP));
   float* yca = (float*)(fr + S::yca_off(NRP));
-  const bf16_t* wq = p.wqca + l * p.s_o;
+  const char* wq = p.wqca + l * p.s_o;
   const char* shs = p.shs + ((long long)(d.s * p.L + l) * 3 + 1) * p.B * S::H * 4;
   // [wave][4 column tiles][q, shift][68 slots] x 16 bytes: lane L at slot L + L / 16, so that the
   // transposed reads of the finishing step fall in distinct banks
@@ -1215,7 +1280,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
-        wf[nt][i] = __builtin_bit_cast(bf16x8, ld16(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * 512 + c.lane * 8));
+        wf[nt][i] = wfrag_glb<S>(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * S::CH, c.lane);
     }
   };
   // (wave 0 polls the ready epochs first: its loads would delay the poll, so it issues its share after)
@@ -1264,6 +1329,8 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     const int pos = min(qt * 16 + r, p.Mq - 1);
     const f32x4 cs = ldf4(p.ca_cos + pos * HD + 4 * cg), sn = ldf4(p.ca_sin + pos * HD + 4 * cg);
     const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
+    // fp8 weights: the output-channel scales of the head's columns 4 cg .. 4 cg + 3
+    const f32x4 scq = S::W8 ? ldf4(p.sc_qca + (long long)l * S::H + hd * HD + 4 * cg) : f32x4{1.f, 1.f, 1.f, 1.f};
     // shift Wq^T while the query rows are in flight
     f32x4 accb[4][2];
 #pragma unroll
@@ -1318,7 +1385,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       const float rs = rsqrtf((ssw[r] + ssw[16 + r] + ssw[32 + r] + ssw[48 + r]) * (1.0f / (float)S::H) + p.eps);
       f32x4 x;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = qv[e] * rs + bv[e];
+      for (int e = 0; e < 4; ++e) x[e] = (qv[e] * rs + bv[e]) * scq[e];
       // q norm over the head's 64 columns (the 16 lanes of the row), weight 1 + w, rotate-half RoPE with the
       // partner column d +- 32 on lane ^ 8
       float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
@@ -1596,7 +1663,7 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
     }
   } else {
     if (t < d.ntask) {
-      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB);
+      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB * S::CH);
       MKX_TRW(c, 9);
     }
     // gate and the next AdaRMS scale: the residual stages' tasks, and the down projection's reducers (its
@@ -1625,9 +1692,9 @@ __device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_
 }
 
 // ------------------------------------------------------------------------------------------------
-template <int H, int I>
+template <int H, int I, bool W8>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
-  using S = Shape<H, I>;
+  using S = Shape<H, I, W8>;
   __shared__ __attribute__((aligned(1024))) char smem[S::LDS];
   CP& p = *(CP*)(__builtin_amdgcn_kernarg_segment_ptr());
   Ctx<S> c(p, smem);

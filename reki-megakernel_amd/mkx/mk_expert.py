@@ -42,13 +42,26 @@ class ExpertMegakernel:
             raise ValueError("the megakernel implements multi-head attention only (n_kv_heads == n_q_heads)")
         bf = torch.bfloat16
         st = lambda f: torch.stack([f(lay).detach().to(bf) for lay in layers]).contiguous()  # noqa: E731
-        wqkv = st(lambda m: torch.cat([m.self_attn.q_proj.weight, m.self_attn.k_proj.weight, m.self_attn.v_proj.weight], 0))
-        wo = st(lambda m: m.self_attn.o_proj.weight)
-        wqca = st(lambda m: m.cross_attn.q_proj.weight)
-        woca = st(lambda m: m.cross_attn.o_proj.weight)
-        wg = st(lambda m: m.mlp.gate_proj.weight)
-        wu = st(lambda m: m.mlp.up_proj.weight)
-        wd = st(lambda m: m.mlp.down_proj.weight)
+        # fp8 e4m3 linear weights (a ``weight_q`` tensor with per-output-channel ``weight_scale`` beside
+        # each linear): passed as bytes plus fp32 scales; otherwise bf16
+        q0 = getattr(layers[0].self_attn.q_proj, "weight_q", None)
+        self.fp8 = q0 is not None and q0.dtype == torch.float8_e4m3fn
+        lins = {
+            "qkv": lambda m: (m.self_attn.q_proj, m.self_attn.k_proj, m.self_attn.v_proj),
+            "o": lambda m: (m.self_attn.o_proj,), "qca": lambda m: (m.cross_attn.q_proj,),
+            "oca": lambda m: (m.cross_attn.o_proj,), "g": lambda m: (m.mlp.gate_proj,),
+            "u": lambda m: (m.mlp.up_proj,), "d": lambda m: (m.mlp.down_proj,),
+        }
+        ws, scs = {}, {}
+        for k, f in lins.items():
+            if self.fp8:
+                ws[k] = torch.stack([torch.cat([lin.weight_q.detach().view(torch.uint8) for lin in f(lay)], 0)
+                                     for lay in layers]).contiguous()
+                scs[k] = torch.stack([torch.cat([lin.weight_scale.detach().float().reshape(-1) for lin in f(lay)], 0)
+                                      for lay in layers]).contiguous()
+            else:
+                ws[k] = st(lambda m, f=f: torch.cat([lin.weight for lin in f(m)], 0))
+        wqkv, wo, wqca, woca, wg, wu, wd = (ws[k] for k in ("qkv", "o", "qca", "oca", "g", "u", "d"))
         qn = st(lambda m: m.self_attn.q_norm.weight)
         kn = st(lambda m: m.self_attn.k_norm.weight)
         qcan = st(lambda m: m.cross_attn.q_norm.weight)
@@ -71,10 +84,14 @@ class ExpertMegakernel:
         self.registers_in_loop = registers_in_loop
         dims = MkxDims(L=self.L, H=self.H, NH=self.NH, HD=self.HD, I=self.I, A=self.A, max_rows=max_rows,
                        max_batch=max_batch, max_mem_rows=max_mem_rows, max_src_rows=max_src_rows,
-                       weight_dtype=_lib.WEIGHTS_BF16, activation=self.activation, eps=self.eps, qk_eps=self.qk_eps)
+                       weight_dtype=_lib.WEIGHTS_FP8_E4M3 if self.fp8 else _lib.WEIGHTS_BF16, activation=self.activation,
+                       eps=self.eps, qk_eps=self.qk_eps)
         w = MkxWeights(wqkv=_ptr(wqkv), wo=_ptr(wo), wqca=_ptr(wqca), woca=_ptr(woca), wg=_ptr(wg), wu=_ptr(wu),
                        wd=_ptr(wd), qn=_ptr(qn), kn=_ptr(kn), qcan=_ptr(qcan), win=_ptr(win), bin=_ptr(b_in),
                        wout=_ptr(wout), bout=_ptr(bout))
+        if self.fp8:
+            w.wqkv_scale, w.wo_scale, w.wqca_scale, w.woca_scale, w.wg_scale, w.wu_scale, w.wd_scale = (
+                _ptr(scs[k]) for k in ("qkv", "o", "qca", "oca", "g", "u", "d"))
         h = ctypes.c_void_p()
         check(lib().mkx_create(ctypes.byref(dims), ctypes.byref(w), ctypes.c_void_p(_stream()), ctypes.byref(h)), "mkx_create")
         self._h = h

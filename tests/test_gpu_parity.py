@@ -107,6 +107,21 @@ def test_wide_expert_D_shape_bf16():
     _check_loop("D shape, bf16 weights", make_case(replace(SY.WORKLOADS["D"], weight_dtype="bf16")))
 
 
+def test_fp8_weights_tiny():
+    # e4m3 weights with per-output-channel scales: the kernel converts them to bf16 operands exactly and
+    # applies the scales in the epilogues, so it tracks the oracle run with the dequantised weights
+    from dataclasses import replace
+    _check_loop("tiny fp8", make_case(replace(TINY, weight_dtype="fp8_e4m3")))
+
+
+def test_wide_expert_D_fp8():
+    _check_loop("D (L16 H1024, fp8 weights)", make_case(SY.WORKLOADS["D"]))
+
+
+def test_wide_expert_D_fp8_batch_of_four():
+    _check_loop("D-b4 (fp8 weights, batch 4)", make_case(SY.WORKLOADS["D-b4"]))
+
+
 def test_long_context_C():
     _check_loop("C (S 1024, PM 256)", make_case(SY.WORKLOADS["C"]))
 
