@@ -601,15 +601,6 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   bf16x8 sh_h[KPW], sh_l[KPW];  // the split shift fragments of this wave's k-blocks (rows = samples)
   u32x4 ssv[S::HT / 16];  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
   if (ada) {
-    // lane l reads sample l % 16; the samples >= B fall outside the buffer and read zeros
-    const __amdgpu_buffer_rsrc_t rsh =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(d.shs), (short)0, p.B * S::H * 4, 0x00020000);
-#pragma unroll
-    for (int i = 0; i < KPW; ++i) {
-      const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + c.wave + NWAVES * i) * 4 + (c.lane >> 4)) * 32);
-      sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
-      sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
-    }
     const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
     const uint32_t so = (uint32_t)((min(rt0 * 16 + c.lane, NRP - 1) * S::HT + c.wave * (S::HT / 4)) * 4);
 #pragma unroll
@@ -622,6 +613,18 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   epre = epi_preload(c, d, qkind, qj, tile, (rt0 + min(ert, NRT - 1)) * 16 + (eL & 15), eL);
   wait_vm0();  // activations, and the staged weights and modulation slices, have landed
   __syncthreads();
+  if (ada) {
+    // the split shift fragments, staged in LDS by the prefetch: lane l reads sample l % 16 (zeros for the
+    // samples >= B)
+    const char* shl = c.smem + S::MODS;
+    const bool has = (c.lane & 15) < p.B;
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int o = (((c.lane & 15) * S::NKB + c.wave + NWAVES * i) * 4 + (c.lane >> 4)) * 32;
+      sh_h[i] = has ? ldsfrag(shl + o) : bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      sh_l[i] = has ? ldsfrag(shl + o + 16) : bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
   MKX_TR(c, 1);
   if (ada) {
     float ssp = 0.f;
@@ -1691,6 +1694,18 @@ __device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_
   c.dn = NWAVES;
 }
 
+// AdaRMS GEMM stages: the stage's split shift slices (B H hi / lo pairs, written in the launch's first stage)
+// into LDS, by waves 1-3
+template <class S>
+__device__ __forceinline__ void prefetch_shifts(Ctx<S>& c, const Desc& d) {
+  if (c.wave == 0 || !(d.kind == K_QKV || d.kind == K_GU) || c.wg >= d.ntask || d.st == ST_TAIL || d.st == ST_SA || d.st == ST_CA) return;
+  c.dw = c.wave - 1;
+  c.dn = NWAVES - 1;
+  dma_f32(c, c.smem + S::MODS, (const float*)d.shs, c.p.B * S::H);
+  c.dw = c.wave;
+  c.dn = NWAVES;
+}
+
 // ------------------------------------------------------------------------------------------------
 template <int H, int I, bool W8>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
@@ -1749,12 +1764,17 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       cur = describe(c, 1);
       if (c.wave != 0) prefetch(c, cur, s_ks);
       bar_wait(bc, 1);
+      // the split shifts were written by every workgroup in this first stage: staged only after the barrier
+      prefetch_shifts(c, cur);
     } else {
       __syncthreads();  // this stage's LDS is no longer read: the next stage's prefetch may overwrite it
       if (g + 1 < total) {
         cur = describe(c, g + 1);
         // waves 1-3 issue the prefetch; wave 0, which polls the ready epochs, keeps no loads in flight
-        if (c.wave != 0) prefetch(c, cur, s_ks);
+        if (c.wave != 0) {
+          prefetch(c, cur, s_ks);
+          prefetch_shifts(c, cur);
+        }
       }
     }
     c.ep = (unsigned)(g + 1);
