@@ -481,13 +481,14 @@ struct EpiPre {
   f32x4 sa, sb;  // fp8 weights: output-channel scales of the item's columns (V tasks: one per 16-column tile)
 };
 
+// The constant part (RoPE tables, q/k norm weights, fp8 output-channel scales): loaded for a task's first
+// pass before its ready-epoch wait, the operands being inputs of the call, so that their latency (they are
+// often no longer in L2 when the stage comes round) overlaps the wait instead of following it.
 template <class S>
-__device__ __forceinline__ EpiPre epi_preload(Ctx<S>& c, const Desc& d, int kind, int j, int tile, int row, int L) {
+__device__ __forceinline__ EpiPre epi_const(Ctx<S>& c, const Desc& d, int kind, int j, int tile, int row, int L) {
   CP& p = c.p;
   EpiPre e;
-  if (d.kind == K_RES) {
-    e.c0 = as_f4(ld16((const char*)d.res + fpiece(row, tile * 16 + 4 * (L >> 4), c.RT)));
-  } else if (d.kind == K_QKV && kind < 2) {
+  if (d.kind == K_QKV && kind < 2) {
     const int d0 = 16 * j + 4 * (L >> 4);
     const bf16_t* nw = (kind == 0 ? p.qn : p.kn) + d.l * HD;
     e.w0 = *reinterpret_cast<const uint2*>(nw + d0);
@@ -521,6 +522,9 @@ __device__ __forceinline__ EpiPre epi_preload(Ctx<S>& c, const Desc& d, int kind
   }
   return e;
 }
+
+// row of the epilogue item of thread tid in a pass over nrt row tiles from rt0
+__device__ __forceinline__ int epi_row(int rt0, int nrt, int tid) { return (rt0 + min(tid >> 6, nrt - 1)) * 16 + (tid & 15); }
 
 template <class S>
 __device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int hd, int j, int row, int L, f32x4 xa, f32x4 xb,
@@ -580,7 +584,7 @@ __device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][2][2], const bf16
 // partial tiles written to the cross-wave reduction buffer.
 template <class S, int NRT>
 __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int kb0, bool vtask, int qkind, int qj,
-                                          int tile, EpiPre& epre) {
+                                          int tile, EpiPre& epre, bool have_const) {
   constexpr int KPW = S::KPW, RB = S::RBMAX;
   CP& p = c.p;
   const int RT = c.RT, NRP = p.NRP;
@@ -609,8 +613,9 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
 #pragma unroll
     for (int i = 0; i < KPW; ++i) sh_h[i] = sh_l[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
-  const int ert = c.tid >> 6, eL = c.tid & 63;
-  epre = epi_preload(c, d, qkind, qj, tile, (rt0 + min(ert, NRT - 1)) * 16 + (eL & 15), eL);
+  const int erow = epi_row(rt0, NRT, c.tid), eL = c.tid & 63;
+  if (!have_const) epre = epi_const(c, d, qkind, qj, tile, erow, eL);
+  if (d.kind == K_RES) epre.c0 = as_f4(ld16((const char*)d.res + fpiece(erow, tile * 16 + 4 * (eL >> 4), c.RT)));
   wait_vm0();  // activations, and the staged weights and modulation slices, have landed
   __syncthreads();
   if (ada) {
@@ -727,14 +732,16 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     const int kb0 = d.kind == K_SPLIT ? split * S::NKB : 0;
     const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
     const int rt_hi = d.kind == K_SPLIT ? RT : (split + 1) * RT / d.rgs;
+    // the first pass's constant epilogue operands, while the wait runs
+    EpiPre epre = epi_const(c, d, qkind, qj, tile, epi_row(rt_lo, min(RB, rt_hi - rt_lo), c.tid), c.tid & 63);
     gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
     MKX_TR(c, 0);
     for (int rt0 = rt_lo; rt0 < rt_hi; rt0 += RB) {
       const int nrt = min(RB, rt_hi - rt0);
-      EpiPre epre;
-      if (nrt == 1) gemm_pass<S, 1>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
-      else if (nrt == 2 || RB == 2) gemm_pass<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
-      else gemm_pass<S, RB>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+      const bool have_const = rt0 == rt_lo;
+      if (nrt == 1) gemm_pass<S, 1>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre, have_const);
+      else if (nrt == 2 || RB == 2) gemm_pass<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre, have_const);
+      else gemm_pass<S, RB>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre, have_const);
       __syncthreads();
       MKX_TR(c, 2);
       // epilogue: one (row tile, lane) item per thread: row (rt0 + rt) * 16 + L % 16, columns tile*16 + 4 (L / 16) + 0..3
@@ -1302,6 +1309,13 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       pre(hd);
     }
     const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
+    // step 1b item of this lane: row r = 4 wave + lane / 16 of the tile, columns 4 cg .. 4 cg + 3 of the
+    // head; its RoPE, norm weight (and fp8 scale) constants are loaded before the wait
+    const int r = 4 * c.wave + (c.lane >> 4), cg = c.lane & 15;
+    const int pos = min(qt * 16 + r, p.Mq - 1);
+    const f32x4 cs = ldf4(p.ca_cos + pos * HD + 4 * cg), sn = ldf4(p.ca_sin + pos * HD + 4 * cg);
+    const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
+    const f32x4 scq = S::W8 ? ldf4(p.sc_qca + (long long)l * S::H + hd * HD + 4 * cg) : f32x4{1.f, 1.f, 1.f, 1.f};
     // every out-projection tile of the row group holding the query rows (their sums of squares share lines)
     {
       const int rg = row_group_of(rq, RT, rgo);
@@ -1309,8 +1323,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     }
     if (v == u0 && c.wave == 0) pre(hd);
     MKX_TR(c, 0);
-    // 1a. operands: y2 fragments of the query rows, sums of squares; and for step 1b this lane's RoPE / norm
-    //     constants
+    // 1a. operands: y2 fragments of the query rows, sums of squares
     bf16x8 yh[KPW], ylo[KPW];
     u32x4 ssv[S::HT / 16];
     {
@@ -1327,13 +1340,6 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 #pragma unroll
       for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
     }
-    // step 1b item of this lane: row r = 4 wave + lane / 16 of the tile, columns 4 cg .. 4 cg + 3 of the head
-    const int r = 4 * c.wave + (c.lane >> 4), cg = c.lane & 15;
-    const int pos = min(qt * 16 + r, p.Mq - 1);
-    const f32x4 cs = ldf4(p.ca_cos + pos * HD + 4 * cg), sn = ldf4(p.ca_sin + pos * HD + 4 * cg);
-    const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
-    // fp8 weights: the output-channel scales of the head's columns 4 cg .. 4 cg + 3
-    const f32x4 scq = S::W8 ? ldf4(p.sc_qca + (long long)l * S::H + hd * HD + 4 * cg) : f32x4{1.f, 1.f, 1.f, 1.f};
     // shift Wq^T while the query rows are in flight
     f32x4 accb[4][2];
 #pragma unroll
