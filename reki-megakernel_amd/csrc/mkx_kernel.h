@@ -850,16 +850,34 @@ struct AttnState {
 // fp32 softmax (src/mk_expert.py:196-251).
 __device__ __forceinline__ void attn_block(AttnState& A, int lane, const char* K, const char* Kl, const char* V, const char* Vl,
                                            int klo, int khi, float qs, const float* rk) {
+  // every LDS operand of the block is read up front (distinct registers), so the reads overlap each other
+  // instead of each waiting for the MFMA before it
+  bf16x8 kf[4], kl[4], vf[4], vl[4];
+  f32x4 rkv[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kf[i] = ldsfrag(K + i * 1024 + lane * 16);
+    if (Kl) kl[i] = ldsfrag(Kl + i * 1024 + lane * 16);
+  }
+  // key RMS factors of the lane's 8 keys: 4 (lane / 16) + 0..3 and 16 + the same
+  if (rk) {
+    rkv[0] = *reinterpret_cast<const f32x4*>(rk + 4 * (lane >> 4));
+    rkv[1] = *reinterpret_cast<const f32x4*>(rk + 16 + 4 * (lane >> 4));
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    vf[dt] = ldsfrag(V + dt * 1024 + lane * 16);
+    if (Vl) vl[dt] = ldsfrag(Vl + dt * 1024 + lane * 16);
+  }
   f32x4 s[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
-      const bf16x8 kf = ldsfrag(K + (h * 2 + db) * 1024 + lane * 16);
-      s[h] = mfma16(kf, A.qh[db], s[h]);
-      s[h] = mfma16(kf, A.ql[db], s[h]);
-      if (Kl) s[h] = mfma16(ldsfrag(Kl + (h * 2 + db) * 1024 + lane * 16), A.qh[db], s[h]);
+      s[h] = mfma16(kf[h * 2 + db], A.qh[db], s[h]);
+      s[h] = mfma16(kf[h * 2 + db], A.ql[db], s[h]);
+      if (Kl) s[h] = mfma16(kl[h * 2 + db], A.qh[db], s[h]);
     }
   }
   float pv[8];
@@ -867,8 +885,7 @@ __device__ __forceinline__ void attn_block(AttnState& A, int lane, const char* K
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
-    float sc = qs;
-    if (rk) sc *= rk[key];
+    const float sc = qs * rkv[j >> 2][j & 3];
     pv[j] = s[j >> 2][j & 3] * sc + ((key >= klo && key < khi) ? 0.f : -INFINITY);
     mb = fmaxf(mb, pv[j]);
   }
@@ -888,11 +905,10 @@ __device__ __forceinline__ void attn_block(AttnState& A, int lane, const char* K
   split8(pv, ph, pl);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
-    const bf16x8 vf = ldsfrag(V + dt * 1024 + lane * 16);
     f32x4 a = A.acc[dt] * alpha;
-    a = mfma16(vf, ph, a);
-    a = mfma16(vf, pl, a);
-    if (Vl) a = mfma16(ldsfrag(Vl + dt * 1024 + lane * 16), ph, a);
+    a = mfma16(vf[dt], ph, a);
+    a = mfma16(vf[dt], pl, a);
+    if (Vl) a = mfma16(vl[dt], ph, a);
     A.acc[dt] = a;
   }
 }
