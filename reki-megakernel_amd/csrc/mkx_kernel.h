@@ -298,6 +298,13 @@ __device__ __forceinline__ void st_split4(void* base, uint32_t off, f32x4 v) {
   st_sc1_b64(base, off + 1024, l);
 }
 __device__ __forceinline__ u32x4 lds16(const char* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Marks LDS values as needed together: the reads that produced them are issued back to back and waited for
+// once, instead of the compiler reusing one register and waiting after every read.
+template <class T, int N>
+__device__ __forceinline__ void lds_batch(T (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
 __device__ __forceinline__ void sts16(char* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ bf16x8 ldsfrag(const char* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
@@ -749,9 +756,13 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
         const int rt = c.tid >> 6, L = c.tid & 63;
         if (rt < nrt) {
           auto wsum = [&](int r, int nt, int lane) {
-            f32x4 v = ldf4((const float*)(red + ((r * 2 + nt) * 64 + lane) * 16));
+            f32x4 pw[NWAVES];
 #pragma unroll
-            for (int w = 1; w < NWAVES; ++w) v += ldf4((const float*)(red + (((w * (RB + 1) + r) * 2 + nt) * 64 + lane) * 16));
+            for (int w = 0; w < NWAVES; ++w) pw[w] = ldf4((const float*)(red + (((w * (RB + 1) + r) * 2 + nt) * 64 + lane) * 16));
+            lds_batch(pw);
+            f32x4 v = pw[0];
+#pragma unroll
+            for (int w = 1; w < NWAVES; ++w) v += pw[w];
             return v;
           };
           const int row = (rt0 + rt) * 16 + (L & 15);
