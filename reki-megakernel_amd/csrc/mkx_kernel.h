@@ -697,19 +697,33 @@ __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc
   flag_wait(bc, F_DPART, S::TPR * S::SK, [&](int i) { return (i % S::SK) * S::HT + t0 + i / S::SK; }, (unsigned long long)g);
   wait_vm0();  // the staged gate and next AdaRMS scale (the prefetch's DMA) have landed
   __syncthreads();
-  // one (tile, row tile) block of 64 items per wave and round: lanes L, L^16, L^32, L^48 hold one row
-  for (int it = c.tid; it < S::TPR * RT * 64; it += NTHREADS) {
-    const int tile = t0 + it / (RT * 64), rem = it % (RT * 64), rtg = rem >> 6, L = rem & 63;
-    u32x4 xp[S::SK];
+  // one (tile, row tile) block of 64 items per wave and round (lanes L, L^16, L^32, L^48 hold one row);
+  // the loads of RR rounds are issued together, so their latencies overlap
+  constexpr int RR = 3;
+  const int nblk = S::TPR * RT;
+  for (int b0 = c.wave; b0 < nblk; b0 += NWAVES * RR) {
+    u32x4 xp[RR][S::SK];
+    f32x4 res[RR];
 #pragma unroll
-    for (int j = 0; j < S::SK; ++j) xp[j] = ld16((const char*)d.part + ((((j * S::HT + tile) * RT + rtg) * 64 + L) * 16));
-    const int row = rtg * 16 + (L & 15), col = tile * 16 + 4 * (L >> 4);
-    const f32x4 res = as_f4(ld16((const char*)d.res + fpiece(row, col, RT)));
-    f32x4 v = as_f4(xp[0]);
+    for (int k = 0; k < RR; ++k) {
+      const int blk = min(b0 + NWAVES * k, nblk - 1);
+      const int tile = t0 + blk / RT, rtg = blk % RT, L = c.lane;
 #pragma unroll
-    for (int j = 1; j < S::SK; ++j) v += as_f4(xp[j]);
-    if (S::W8) v *= ldf4(d.sc + col);  // the output channel's scale
-    res_piece(c, d, tile, row, col, L, v, res);
+      for (int j = 0; j < S::SK; ++j) xp[k][j] = ld16((const char*)d.part + ((((j * S::HT + tile) * RT + rtg) * 64 + L) * 16));
+      res[k] = as_f4(ld16((const char*)d.res + fpiece(rtg * 16 + (L & 15), tile * 16 + 4 * (L >> 4), RT)));
+    }
+#pragma unroll
+    for (int k = 0; k < RR; ++k) {
+      const int blk = b0 + NWAVES * k;
+      if (blk >= nblk) break;
+      const int tile = t0 + blk / RT, rtg = blk % RT, L = c.lane;
+      const int row = rtg * 16 + (L & 15), col = tile * 16 + 4 * (L >> 4);
+      f32x4 v = as_f4(xp[k][0]);
+#pragma unroll
+      for (int j = 1; j < S::SK; ++j) v += as_f4(xp[k][j]);
+      if (S::W8) v *= ldf4(d.sc + col);  // the output channel's scale
+      res_piece(c, d, tile, row, col, L, v, res[k]);
+    }
   }
   MKX_TR(c, 7);
   flag_publish(bc, F_DOWN, r, (unsigned long long)g + 1);
