@@ -788,10 +788,15 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
             const int ib = row0 - b * p.Mqp + 4 * (L >> 4);
             const int KBO = ceil_to(p.Mq, 32) / 32;
             float rs[4];
+            {
+              // the 4 rows' sums of squares from the 4 waves' partials (rows rt * 16 + 4 (L / 16) + 0..3)
+              f32x4 sw[NWAVES];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = rt * 16 + 4 * (L >> 4) + e;
-              rs[e] = rsqrtf((ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r]) * (1.0f / (float)S::H) + p.eps);
+              for (int w = 0; w < NWAVES; ++w) sw[w] = ldf4(ssw + 64 * w + rt * 16 + 4 * (L >> 4));
+              lds_batch(sw);
+              const f32x4 tot = ((sw[0] + sw[1]) + sw[2]) + sw[3];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) rs[e] = rsqrtf(tot[e] * (1.0f / (float)S::H) + p.eps);
             }
             const uint32_t vo = (uint32_t)(((b * S::NH + qhd) * KBO + (ib >> 5)) * 8192 + L * 16 + ((ib >> 4) & 1) * 8);
 #pragma unroll
@@ -813,8 +818,11 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
             res_piece(c, d, tile, row, col, L, S::W8 ? v * epre.sa : v, epre.c0);
           } else {
             const int r = rt * 16 + (L & 15);
-            const float tot = ssw[r] + ssw[64 + r] + ssw[128 + r] + ssw[192 + r];
-            const float rs = rsqrtf(tot * (1.0f / (float)S::H) + p.eps);
+            float sw[NWAVES];
+#pragma unroll
+            for (int w = 0; w < NWAVES; ++w) sw[w] = ssw[64 * w + r];
+            lds_batch(sw);
+            const float rs = rsqrtf((((sw[0] + sw[1]) + sw[2]) + sw[3]) * (1.0f / (float)S::H) + p.eps);
             const int bl = c.sample_of(row) + 16 * (L >> 4);
             v = v * rs + wsum(RB, 0, bl);
             f32x4 u = wsum(rt, 1, L) * rs + wsum(RB, 1, bl);
@@ -964,19 +972,26 @@ __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float*
   mm[c.wave * 64 + c.lane] = A.m;
   md[c.wave * 64 + c.lane] = A.den;
   __syncthreads();
-  float mw[NWAVES], M = -INFINITY;
+  float mw[NWAVES], mdv[NWAVES], M = -INFINITY;
+  f32x4 ma[NWAVES];
 #pragma unroll
   for (int w = 0; w < NWAVES; ++w) {
     mw[w] = mm[w * 64 + c.lane];
-    M = fmaxf(M, mw[w]);
+    mdv[w] = md[w * 64 + c.lane];
+    ma[w] = macc[(w * 4 + c.wave) * 64 + c.lane];
   }
+  lds_batch(mw);
+  lds_batch(mdv);
+  lds_batch(ma);
+#pragma unroll
+  for (int w = 0; w < NWAVES; ++w) M = fmaxf(M, mw[w]);
   float den = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 0; w < NWAVES; ++w) {
     const float f = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - M);
-    den += md[w * 64 + c.lane] * f;
-    acc += macc[(w * 4 + c.wave) * 64 + c.lane] * f;
+    den += mdv[w] * f;
+    acc += ma[w] * f;
   }
   den = xor32_sum(xor16_sum(den));
   const int q = qt * 16 + (c.lane & 15);
@@ -1423,16 +1438,26 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     {
       // 1b. q of row r, columns 4 cg .. 4 cg + 3 (accumulator lane r + 16 (cg % 4) of column tile cg / 4)
       const int nt = cg >> 2, lr = r + 16 * (cg & 3), lb = b + 16 * (cg & 3);
-      f32x4 qv = {0.f, 0.f, 0.f, 0.f};
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      f32x4 qa[NWAVES], ba[NWAVES];
+      float sw[NWAVES];
 #pragma unroll
       for (int w = 0; w < NWAVES; ++w) {
-        qv += ldf4((const float*)(red + (((w * 4 + nt) * 2 + 0) * 68 + lr + (lr >> 4)) * 16));
-        const f32x4 bb = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 68 + lb + (lb >> 4)) * 16));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] += bb[e];
+        qa[w] = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 0) * 68 + lr + (lr >> 4)) * 16));
+        ba[w] = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 68 + lb + (lb >> 4)) * 16));
+        sw[w] = ssw[16 * w + r];
       }
-      const float rs = rsqrtf((ssw[r] + ssw[16 + r] + ssw[32 + r] + ssw[48 + r]) * (1.0f / (float)S::H) + p.eps);
+      lds_batch(qa);
+      lds_batch(ba);
+      lds_batch(sw);
+      f32x4 qv = qa[0];
+      float bv[4] = {ba[0][0], ba[0][1], ba[0][2], ba[0][3]};
+#pragma unroll
+      for (int w = 1; w < NWAVES; ++w) {
+        qv += qa[w];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] += ba[w][e];
+      }
+      const float rs = rsqrtf((sw[0] + sw[1] + sw[2] + sw[3]) * (1.0f / (float)S::H) + p.eps);
       f32x4 x;
 #pragma unroll
       for (int e = 0; e < 4; ++e) x[e] = (qv[e] * rs + bv[e]) * scq[e];
