@@ -82,6 +82,18 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_base, 16, 0, CPOL);
 }
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0); }
+// Waits until at most N of this wave's vector memory operations are outstanding: they complete in issue
+// order, so every operation issued before the last N has completed (LDS DMAs included). Written as the
+// builtin (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt at their no-wait maxima) so that
+// the compiler's own wait-count tracking knows which loads are still pending and waits for the later ones
+// one by one where they are used; the empty asm statements keep memory accesses from moving across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_le() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is a 6-bit counter");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ unsigned xcc_id() {
   unsigned v;

@@ -600,11 +600,13 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   const uint32_t vlane = (uint32_t)c.lane * 16;
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
   char* red = c.smem + S::RED;                // [wave][RB + 1][2][64 lanes] x 16 bytes
+  // k-block major, in the order the MFMAs use them: the MFMAs of the first k-blocks start while the later
+  // blocks are still arriving
   bf16x8 ah[NRT][KPW], al[NRT][KPW];
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt)
+  for (int i = 0; i < KPW; ++i)
 #pragma unroll
-    for (int i = 0; i < KPW; ++i) {
+    for (int rt = 0; rt < NRT; ++rt) {
       const uint32_t blk = (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048);
       ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
       al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
@@ -623,8 +625,11 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   const int erow = epi_row(rt0, NRT, c.tid), eL = c.tid & 63;
   if (!have_const) epre = epi_const(c, d, qkind, qj, tile, erow, eL);
   if (d.kind == K_RES) epre.c0 = as_f4(ld16((const char*)d.res + fpiece(erow, tile * 16 + 4 * (eL >> 4), c.RT)));
-  wait_vm0();  // activations, and the staged weights and modulation slices, have landed
-  __syncthreads();
+  // The staged weights and modulation slices (the prefetch's LDS DMAs, issued before every load above) have
+  // landed once no more than the activation loads are outstanding; the activations are waited for where the
+  // MFMAs use them.
+  wait_vm_le<2 * NRT * KPW>();
+  exec_barrier();
   if (ada) {
     // the split shift fragments, staged in LDS by the prefetch: lane l reads sample l % 16 (zeros for the
     // samples >= B)
@@ -638,15 +643,6 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
     }
   }
   MKX_TR(c, 1);
-  if (ada) {
-    float ssp = 0.f;
-#pragma unroll
-    for (int i = 0; i < S::HT / 16; ++i) {
-      const f32x4 x = as_f4(ssv[i]);
-      ssp += (x[0] + x[1]) + (x[2] + x[3]);
-    }
-    ssw[c.wave * 64 + c.lane] = ssp;
-  }
   f32x4 acc[NRT + 1][2][2];
 #pragma unroll
   for (int rt = 0; rt <= NRT; ++rt)
@@ -656,6 +652,15 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   if (vtask) gemm_mma<S, NRT, 2, true, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
   else if (d.nt == 2) gemm_mma<S, NRT, 2, false, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
   else gemm_mma<S, NRT, 1, false, false>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
+  if (ada) {
+    float ssp = 0.f;
+#pragma unroll
+    for (int i = 0; i < S::HT / 16; ++i) {
+      const f32x4 x = as_f4(ssv[i]);
+      ssp += (x[0] + x[1]) + (x[2] + x[3]);
+    }
+    ssw[c.wave * 64 + c.lane] = ssp;
+  }
   // cross-wave reduction through LDS (the shift tile at slot RB)
 #pragma unroll
   for (int rt = 0; rt <= NRT; ++rt)
