@@ -1189,7 +1189,14 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
       }, (unsigned long long)g);
     }
     MKX_TR(c, 0);
-    // own-row operands: Q tile (hi, lo), K tiles of all own keys, V^T blocks (all DMA, one batch)
+    // The query rows' sums of squares (two column halves; DMA'd into the merge area, read before the merge
+    // reuses it), then the own-row operands: each wave's next DMA is a piece of the Q tile (hi, lo), then K
+    // tiles of all own keys and V^T blocks. All are DMAs, so one counted wait covers the first phase.
+    float* sq_l = mrg;
+    if (c.wave == 0) {
+      const int qq = qt * 16 + (c.lane & 15), j = (c.lane >> 4) & 1;
+      __builtin_amdgcn_global_load_lds(ssqk + (long long)(hd * 2 + j) * NRP + b * Mqp + qq, (lds_void*)sq_l, 4, 0, 0);
+    }
     const int rt0 = b * Mqp / 16;
     for (int k = c.wave; k < 4 + 4 * NKT + 8 * KBO; k += NWAVES) {
       if (k < 4) {
@@ -1204,17 +1211,29 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
         dma16(vt + ((long long)at.hh * KBO * 8 + vv) * 1024 + c.lane * 16, ((vv & 1) ? Vl : Vh) + (vv >> 1) * 1024);
       }
     }
-    // RMS factors: query row of this lane, and (threads < NOWN32) own keys
-    const int q = qt * 16 + (c.lane & 15);
-    const float ssq = ssqk[(long long)(hd * 2) * NRP + b * Mqp + q] + ssqk[(long long)(hd * 2 + 1) * NRP + b * Mqp + q];
-    float ssk = 0.f;
-    if (c.tid < NOWN32) {
-      const int rowk = b * Mqp + min(c.tid, Mqp - 1);
-      ssk = ssqk[(long long)((S::NH + hd) * 2) * NRP + rowk] + ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + rowk];
+    // RMS factors of the own keys (threads < NOWN32; the others load a valid row and discard it). Loaded with
+    // no branch and summed only after the own-key wait, so that nothing waits for these loads earlier.
+    const int rowk = b * Mqp + min(c.tid, Mqp - 1);
+    const float ssk0 = ssqk[(long long)((S::NH + hd) * 2) * NRP + rowk];
+    const float ssk1 = ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + rowk];
+    // The memory blocks need only the Q tile and the memory K/V (prefetched before it): every wave issued at
+    // least 4 own-key DMAs after its Q piece (M >= 1 gives NKT >= 2 and KBO >= 1, 20 DMAs over 4 waves), so
+    // at most 4 outstanding operations means its Q piece has landed.
+    wait_vm_le<4>();
+    exec_barrier();
+    MKX_TR(c, 1);
+    AttnState A;
+    attn_begin(A, Qh, Ql, c.lane);
+    const float ssq = sq_l[c.lane & 15] + sq_l[16 + (c.lane & 15)];
+    const float qsc = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
+    const int mb0 = kvs >> 5, nmb = PMP / 32 - mb0;
+    for (int beta = c.wave; beta < nmb; beta += NWAVES) {
+      const int kb = mb0 + beta;
+      attn_block(A, c.lane, memK + kb * 4096, nullptr, memVt + kb * 4096, nullptr, kvs - kb * 32, PM - kb * 32, qsc, nullptr);
     }
-    wait_vm0();  // memory K/V (prefetched) and the own-row operands have landed
+    wait_vm0();  // the own keys' K and V^T have landed
     __syncthreads();
-    if (c.tid < NOWN32) rk[c.tid] = rsqrtf(ssk / 64.f + p.qk_eps);
+    if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
     // own keys beyond the sample's rows have no producer: zero their V
     for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
       const int key = Mqp + it / HD, dd = it % HD;
@@ -1222,19 +1241,10 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
       *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
     }
     __syncthreads();
-    MKX_TR(c, 1);
-    AttnState A;
-    attn_begin(A, Qh, Ql, c.lane);
-    const float qsc = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
-    const int mb0 = kvs >> 5, nmb = PMP / 32 - mb0;
-    for (int beta = c.wave; beta < nmb + KBO; beta += NWAVES) {
-      if (beta < nmb) {
-        const int kb = mb0 + beta;
-        attn_block(A, c.lane, memK + kb * 4096, nullptr, memVt + kb * 4096, nullptr, kvs - kb * 32, PM - kb * 32, qsc, nullptr);
-      } else {
-        const int kb = beta - nmb;
-        attn_block(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
-      }
+    // own-key blocks continue the round-robin over the waves (block beta on wave beta % 4)
+    for (int beta = nmb + ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES; beta < nmb + KBO; beta += NWAVES) {
+      const int kb = beta - nmb;
+      attn_block(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
     }
     MKX_TR(c, 2);
     attn_merge_store(c, A, mrg, ysa, b, hd, qt);
