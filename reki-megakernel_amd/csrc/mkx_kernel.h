@@ -1364,8 +1364,9 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
         wf[nt][i] = wfrag_glb<S>(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * S::CH, c.lane);
     }
   };
-  // (wave 0 polls the ready epochs first: its loads would delay the poll, so it issues its share after)
-  if (u0 < cnt && c.wave != 0) pre(attn_task(u0, NQT, NHB).hh % S::NH);
+  // (wave 0 too, although its poll then completes only after these loads: the workgroups of this stage
+  // enter it two stages before their operands are ready, which leaves the loads several microseconds)
+  if (u0 < cnt) pre(attn_task(u0, NQT, NHB).hh % S::NH);
   const int rgo = rgs_of(RT, c.G, S::HT);
   for (int v = u0; v < cnt; v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
@@ -1387,12 +1388,22 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     const f32x4 cs = ldf4(p.ca_cos + pos * HD + 4 * cg), sn = ldf4(p.ca_sin + pos * HD + 4 * cg);
     const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
     const f32x4 scq = S::W8 ? ldf4(p.sc_qca + (long long)l * S::H + hd * HD + 4 * cg) : f32x4{1.f, 1.f, 1.f, 1.f};
+    // shift Wq^T: both are inputs of the call, so it is computed before the wait (and the shift fragments'
+    // registers are free again before the query rows are loaded)
+    f32x4 accb[4][2];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) accb[nt][0] = accb[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KPW; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) accb[nt][h] = mfma16(wf[nt][i], h ? sh_l[i] : sh_h[i], accb[nt][h]);
     // every out-projection tile of the row group holding the query rows (their sums of squares share lines)
     {
       const int rg = row_group_of(rq, RT, rgo);
       flag_wait(bc, F_O, S::HT, [&](int i) { return rg * S::HT + i; }, (unsigned long long)g);
     }
-    if (v == u0 && c.wave == 0) pre(hd);
     MKX_TR(c, 0);
     // 1a. operands: y2 fragments of the query rows, sums of squares
     bf16x8 yh[KPW], ylo[KPW];
@@ -1411,26 +1422,12 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 #pragma unroll
       for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
     }
-    // shift Wq^T while the query rows are in flight
-    f32x4 accb[4][2];
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) accb[nt][0] = accb[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < KPW; ++i)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) accb[nt][h] = mfma16(wf[nt][i], h ? sh_l[i] : sh_h[i], accb[nt][h]);
-    wait_vm0();  // the prefetched chunks and the query operands have landed
+    // Everything but the query rows and their sums of squares has landed (the prefetched K/V chunks were
+    // issued before them); the query rows are waited for where the MFMAs use them.
+    wait_vm_le<2 * KPW + S::HT / 16>();
+    __builtin_amdgcn_sched_barrier(0);  // every query-row load is issued before the first MFMA
     MKX_TR(c, 3);
     {
-      float ssp = 0.f;
-#pragma unroll
-      for (int i = 0; i < S::HT / 16; ++i) {
-        const f32x4 x = as_f4(ssv[i]);
-        ssp += (x[0] + x[1]) + (x[2] + x[3]);
-      }
-      if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
       // [column tile][hi, lo]: 8 independent accumulation chains
       f32x4 acc[4][2];
 #pragma unroll
@@ -1441,6 +1438,13 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int nt = 0; nt < 4; ++nt) acc[nt][h] = mfma16(wf[nt][i], h ? ylo[i] : yh[i], acc[nt][h]);
+      float ssp = 0.f;
+#pragma unroll
+      for (int i = 0; i < S::HT / 16; ++i) {
+        const f32x4 x = as_f4(ssv[i]);
+        ssp += (x[0] + x[1]) + (x[2] + x[3]);
+      }
+      if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const int sl = c.lane + (c.lane >> 4);
