@@ -774,63 +774,84 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       {
         const int rt = c.tid >> 6, L = c.tid & 63;
         if (rt < nrt) {
-          auto wsum = [&](int r, int nt, int lane) {
-            f32x4 pw[NWAVES];
-#pragma unroll
-            for (int w = 0; w < NWAVES; ++w) pw[w] = ldf4((const float*)(red + (((w * (RB + 1) + r) * 2 + nt) * 64 + lane) * 16));
-            lds_batch(pw);
-            f32x4 v = pw[0];
-#pragma unroll
-            for (int w = 1; w < NWAVES; ++w) v += pw[w];
-            return v;
-          };
+          // every LDS operand of the item is read as one batch (the 4 waves' partial tiles, the shift tile's
+          // rows, the partial sums of squares), then summed in wave order
+          auto sum4 = [](const f32x4 (&pw)[NWAVES]) { return ((pw[0] + pw[1]) + pw[2]) + pw[3]; };
+          constexpr int WS = (RB + 1) * 2 * 64 * 16;  // bytes per wave's partial tiles
           const int row = (rt0 + rt) * 16 + (L & 15);
           const int col = tile * 16 + 4 * (L >> 4);
-          f32x4 v = wsum(rt, 0, L);
           if (vtask) {
             // lane L: d = 16 j + 32 nt + L % 16, rows (keys) 4 (L / 16) + e of a 16-row tile of one sample
             const int row0 = (rt0 + rt) * 16, b = c.sample_of(row0);
             const int ib = row0 - b * p.Mqp + 4 * (L >> 4);
             const int KBO = ceil_to(p.Mq, 32) / 32;
-            float rs[4];
-            {
-              // the 4 rows' sums of squares from the 4 waves' partials (rows rt * 16 + 4 (L / 16) + 0..3)
-              f32x4 sw[NWAVES];
+            const int cl = L & 15, bl = b + 16 * (cl >> 2);
+            // the 4 rows' sums of squares (rows rt * 16 + 4 (L / 16) + 0..3), both column tiles' partials and
+            // the shift tile's entries of this lane's column
+            f32x4 sw[NWAVES], a0[NWAVES], a1[NWAVES];
+            float b0[NWAVES], b1[NWAVES];
 #pragma unroll
-              for (int w = 0; w < NWAVES; ++w) sw[w] = ldf4(ssw + 64 * w + rt * 16 + 4 * (L >> 4));
-              lds_batch(sw);
-              const f32x4 tot = ((sw[0] + sw[1]) + sw[2]) + sw[3];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) rs[e] = rsqrtf(tot[e] * (1.0f / (float)S::H) + p.eps);
+            for (int w = 0; w < NWAVES; ++w) {
+              const char* rw = red + w * WS;
+              sw[w] = ldf4(ssw + 64 * w + rt * 16 + 4 * (L >> 4));
+              a0[w] = ldf4((const float*)(rw + ((rt * 2 + 0) * 64 + L) * 16));
+              a1[w] = ldf4((const float*)(rw + ((rt * 2 + 1) * 64 + L) * 16));
+              b0[w] = ((const float*)(rw + ((RB * 2 + 0) * 64 + bl) * 16))[cl & 3];
+              b1[w] = ((const float*)(rw + ((RB * 2 + 1) * 64 + bl) * 16))[cl & 3];
             }
+            lds_batch(sw);
+            lds_batch(a0);
+            lds_batch(a1);
+            lds_batch(b0);
+            lds_batch(b1);
+            const f32x4 tot = sum4(sw);
+            float rs[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rs[e] = rsqrtf(tot[e] * (1.0f / (float)S::H) + p.eps);
             const uint32_t vo = (uint32_t)(((b * S::NH + qhd) * KBO + (ib >> 5)) * 8192 + L * 16 + ((ib >> 4) & 1) * 8);
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-              const f32x4 a = wsum(rt, nt, L);
-              const int cl = L & 15, bl = b + 16 * (cl >> 2);
-              float bias = 0.f;
-#pragma unroll
-              for (int w = 0; w < NWAVES; ++w) bias += ((const float*)(red + (((w * (RB + 1) + RB) * 2 + nt) * 64 + bl) * 16))[cl & 3];
+              const f32x4 a = sum4(nt ? a1 : a0);
+              const float* bb = nt ? b1 : b0;
+              const float bias = ((bb[0] + bb[1]) + bb[2]) + bb[3];
               const float sv = S::W8 ? epre.sa[nt] : 1.0f;  // fp8: the output channel's scale
               f32x4 x;
 #pragma unroll
               for (int e = 0; e < 4; ++e) x[e] = ib + e < p.Mq ? (a[e] * rs[e] + bias) * sv : 0.f;
               st_split4(d.part, vo + (uint32_t)((qj + 2 * nt) * 2048), x);
             }
-          } else if (d.kind == K_SPLIT) {
-            st_sc1(d.part, (uint32_t)((((split * d.tiles + tile) * RT + rt0 + rt) * 64 + L) * 16), as_u4(v));
-          } else if (d.kind == K_RES) {
-            res_piece(c, d, tile, row, col, L, S::W8 ? v * epre.sa : v, epre.c0);
+          } else if (d.kind == K_SPLIT || d.kind == K_RES) {
+            f32x4 pw[NWAVES];
+#pragma unroll
+            for (int w = 0; w < NWAVES; ++w) pw[w] = ldf4((const float*)(red + w * WS + ((rt * 2) * 64 + L) * 16));
+            lds_batch(pw);
+            const f32x4 v = sum4(pw);
+            if (d.kind == K_SPLIT) st_sc1(d.part, (uint32_t)((((split * d.tiles + tile) * RT + rt0 + rt) * 64 + L) * 16), as_u4(v));
+            else res_piece(c, d, tile, row, col, L, S::W8 ? v * epre.sa : v, epre.c0);
           } else {
+            // the two column tiles' partials, the shift tile's rows of this lane's sample and the row's partial
+            // sums of squares
             const int r = rt * 16 + (L & 15);
+            const int bl = c.sample_of(row) + 16 * (L >> 4);
+            f32x4 pv[NWAVES], pu[NWAVES], pb0[NWAVES], pb1[NWAVES];
             float sw[NWAVES];
 #pragma unroll
-            for (int w = 0; w < NWAVES; ++w) sw[w] = ssw[64 * w + r];
+            for (int w = 0; w < NWAVES; ++w) {
+              const char* rw = red + w * WS;
+              pv[w] = ldf4((const float*)(rw + ((rt * 2 + 0) * 64 + L) * 16));
+              pu[w] = ldf4((const float*)(rw + ((rt * 2 + 1) * 64 + L) * 16));
+              pb0[w] = ldf4((const float*)(rw + ((RB * 2 + 0) * 64 + bl) * 16));
+              pb1[w] = ldf4((const float*)(rw + ((RB * 2 + 1) * 64 + bl) * 16));
+              sw[w] = ssw[64 * w + r];
+            }
+            lds_batch(pv);
+            lds_batch(pu);
+            lds_batch(pb0);
+            lds_batch(pb1);
             lds_batch(sw);
             const float rs = rsqrtf((((sw[0] + sw[1]) + sw[2]) + sw[3]) * (1.0f / (float)S::H) + p.eps);
-            const int bl = c.sample_of(row) + 16 * (L >> 4);
-            v = v * rs + wsum(RB, 0, bl);
-            f32x4 u = wsum(rt, 1, L) * rs + wsum(RB, 1, bl);
+            f32x4 v = sum4(pv) * rs + sum4(pb0);
+            f32x4 u = sum4(pu) * rs + sum4(pb1);
             if (S::W8) {  // output-channel scales (the shift row tile used the same weights)
               v *= epre.sa;
               u *= epre.sb;
