@@ -760,6 +760,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     const int rt_hi = d.kind == K_SPLIT ? RT : (split + 1) * RT / d.rgs;
     // the first pass's constant epilogue operands, while the wait runs
     EpiPre epre = epi_const(c, d, qkind, qj, tile, epi_row(rt_lo, min(RB, rt_hi - rt_lo), c.tid), c.tid & 63);
+    MKX_TR(c, 14);
     gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
     MKX_TR(c, 0);
     for (int rt0 = rt_lo; rt0 < rt_hi; rt0 += RB) {
@@ -1420,6 +1421,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) accb[nt][h] = mfma16(wf[nt][i], h ? sh_l[i] : sh_h[i], accb[nt][h]);
+    MKX_TR(c, 14);
     // every out-projection tile of the row group holding the query rows (their sums of squares share lines)
     {
       const int rg = row_group_of(rq, RT, rgo);
