@@ -224,6 +224,34 @@ class ExpertMegakernel:
         self._keep = keep
         return x_out, cur_k, cur_v
 
+    def can_run_all(self, past) -> bool:
+        """Whether Euler step 1 and steps 2..N can share one launch: every step has the same own rows (the
+        register rows are in the loop), so step 1's RoPE tables are the later steps' tables."""
+        st = past.register_step
+        if "sa_pe_first" not in st:
+            return True
+        pairs = list(zip(st["sa_pe_first"], st["sa_pe"])) + list(zip(st["ca_pe_first"], st["ca_pe"]))
+        key = tuple((a.data_ptr(), b.data_ptr(), tuple(a.shape), tuple(b.shape)) for a, b in pairs)
+        cache = self.__dict__.setdefault("_run_all_ok", {})
+        if key not in cache:  # compared once per set of tables (the comparison synchronises the device)
+            cache[key] = all(a.shape == b.shape and torch.equal(a, b) for a, b in pairs)
+        return cache[key]
+
+    def run_all(self, noise: torch.Tensor, mods: torch.Tensor, dt, past, action_dim: int):
+        """Euler steps 1..N in one launch (mods rows 0..N-1): returns (x after step N, cur_k, cur_v) like
+        ``run_first`` followed by ``run``, which it matches bit for bit. Requires ``can_run_all(past)``."""
+        if not self.can_run_all(past):
+            raise ValueError("step 1 has other own rows than steps 2..N (register rows outside the loop): use run_first + run")
+        n_steps = mods.shape[-2]
+        R = 0 if self.register_tokens is None else self.register_tokens.shape[0]
+        B = noise.shape[0]
+        cur_k = torch.empty(self.L, B, R, self.NH, self.HD, device=noise.device, dtype=torch.bfloat16) if R else None
+        cur_v = torch.empty_like(cur_k) if R else None
+        a, x_out, keep = self._args(noise, mods, dt, past, action_dim, n_steps, 0, first=True, cur_k=cur_k, cur_v=cur_v)
+        check(lib().mkx_run(self._h, ctypes.byref(a), ctypes.c_void_p(_stream())), "mkx_run")
+        self._keep = keep
+        return x_out, cur_k, cur_v
+
     def barriers(self, n_steps: int) -> int:
         return int(lib().mkx_barriers(self._h, n_steps))
 
@@ -268,14 +296,17 @@ class LaunchPlan:
         return self.x_out
 
 
-def install(model) -> ExpertMegakernel:
+def install(model, fold_first_step: bool = False) -> ExpertMegakernel:
     """Route the model's ``_expert_actions`` through the megakernel for steps 2..N; modulations and step 1
-    stay the model's own callables (src/mk_expert.py:521-536)."""
+    stay the model's own callables (src/mk_expert.py:521-536). With ``fold_first_step`` (and when the
+    register rows are in the loop) step 1 runs in the same launch as steps 2..N instead."""
     mk = ExpertMegakernel(model)
     model._mk = mk
 
     def _expert_actions(noise, cross_attn_cache, register_cache, state_cond, action_dim, num_steps):
         mods, dt = model._step_modulations(num_steps, state_cond)
+        if fold_first_step and num_steps > 1 and mk.can_run_all(cross_attn_cache):
+            return mk.run_all(noise, mods, dt, cross_attn_cache, action_dim)
         x_t, cur_k, cur_v = model._expert_first_step(noise, cross_attn_cache, register_cache, mods[..., :1, :], dt, action_dim)
         if num_steps > 1:
             x_t = mk.run(x_t, mods, dt, cross_attn_cache, action_dim)

@@ -177,6 +177,54 @@ def test_graph_capture_replays_match_eager():
     _report("graph replays", replays=3, max_abs_x=float(x_eager.abs().max()))
 
 
+def test_run_all_folds_step_one_into_the_launch():
+    """Euler steps 1..N as one launch (register rows in the loop) equal step 1's launch followed by the
+    launch of steps 2..N, bit for bit, including the register rows' K/V of step 1; and install(...,
+    fold_first_step=True) returns the same."""
+    import time
+    case = make_case(TINY)
+    cfg = case["cfg"]
+    model = case["model"]
+    mk = ExpertMegakernel(model)
+    assert mk.can_run_all(case["past"])
+    x1, ck1, cv1 = model._expert_first_step(case["noise"], case["past"], None, case["mods"][..., :1, :], case["dt"], cfg.action_dim)
+    x_two = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    x_all, ck, cv = mk.run_all(case["noise"], case["mods"], case["dt"], case["past"], cfg.action_dim)
+    mk.check()
+    torch.cuda.synchronize()
+    assert torch.equal(x_all, x_two)
+    assert torch.equal(ck, ck1) and torch.equal(cv, cv1)
+    inst = install(model, fold_first_step=True)
+    x_i, ck_i, cv_i = model._expert_actions(case["noise"], case["past"], None, case["inp"]["state_cond"].cuda(), cfg.action_dim,
+                                            cfg.num_steps)
+    torch.cuda.synchronize()
+    assert torch.equal(x_i, x_all) and torch.equal(ck_i, ck)
+    # wall time of the two forms (reported, not asserted)
+    def wall(fn, n=20):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3
+    t_two = wall(lambda: mk.run(model._expert_first_step(case["noise"], case["past"], None, case["mods"][..., :1, :], case["dt"],
+                                                         cfg.action_dim)[0], case["mods"], case["dt"], case["past"], cfg.action_dim))
+    t_all = wall(lambda: mk.run_all(case["noise"], case["mods"], case["dt"], case["past"], cfg.action_dim))
+    _report("run_all", ms_step1_then_rest=round(t_two, 3), ms_one_launch=round(t_all, 3))
+    # the reference layout (register rows only in step 1) cannot share a launch
+    ref_case = make_case(replace_cfg(TINY, registers_in_loop=False))
+    mk_ref = ExpertMegakernel(ref_case["model"])
+    assert not mk_ref.can_run_all(ref_case["past"])
+    with pytest.raises(ValueError):
+        mk_ref.run_all(ref_case["noise"], ref_case["mods"], ref_case["dt"], ref_case["past"], cfg.action_dim)
+
+
+def replace_cfg(cfg, **kw):
+    from dataclasses import replace
+    return replace(cfg, **kw)
+
+
 def test_install_matches_first_step_plus_run():
     case = make_case(TINY)
     cfg = case["cfg"]
