@@ -973,6 +973,75 @@ __device__ __forceinline__ void attn_block(AttnState& A, int lane, const char* K
   }
 }
 
+// Two blocks of 32 bf16 keys (K0/V0 with keys [0, khi0) valid, K1/V1 with [0, khi1)) as one 64-key step of the
+// online softmax: the two blocks' MFMA chains and softmax arithmetic are independent until the shared
+// maximum, so their latencies overlap (the same result as two attn_block calls up to rounding).
+__device__ __forceinline__ void attn_block2(AttnState& A, int lane, const char* K0, const char* V0, int khi0, const char* K1,
+                                            const char* V1, int khi1, float qs) {
+  bf16x8 kf[2][4], vf[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kf[0][i] = ldsfrag(K0 + i * 1024 + lane * 16);
+    kf[1][i] = ldsfrag(K1 + i * 1024 + lane * 16);
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    vf[0][dt] = ldsfrag(V0 + dt * 1024 + lane * 16);
+    vf[1][dt] = ldsfrag(V1 + dt * 1024 + lane * 16);
+  }
+  f32x4 s[2][2];
+#pragma unroll
+  for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) s[bk][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+      for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) s[bk][h] = mfma16(kf[bk][h * 2 + db], hl ? A.ql[db] : A.qh[db], s[bk][h]);
+  float pv[2][8];
+  float mb = -INFINITY;
+#pragma unroll
+  for (int bk = 0; bk < 2; ++bk) {
+    const int khi = bk ? khi1 : khi0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+      pv[bk][j] = s[bk][j >> 2][j & 3] * qs + (key < khi ? 0.f : -INFINITY);
+      mb = fmaxf(mb, pv[bk][j]);
+    }
+  }
+  mb = xor32_max(xor16_max(mb));
+  const float mn = fmaxf(A.m, mb);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float alpha = __expf(A.m - mu);
+  A.m = mn;
+  float ps[2] = {0.f, 0.f};
+#pragma unroll
+  for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pv[bk][j] = __expf(pv[bk][j] - mu);
+      ps[bk] += pv[bk][j];
+    }
+  A.den = A.den * alpha + (ps[0] + ps[1]);
+  bf16x8 ph[2], pl[2];
+  split8(pv[0], ph[0], pl[0]);
+  split8(pv[1], ph[1], pl[1]);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    f32x4 a = A.acc[dt] * alpha;
+    a = mfma16(vf[0][dt], ph[0], a);
+    a = mfma16(vf[1][dt], ph[1], a);
+    a = mfma16(vf[0][dt], pl[0], a);
+    a = mfma16(vf[1][dt], pl[1], a);
+    A.acc[dt] = a;
+  }
+}
+
 __device__ __forceinline__ void attn_begin(AttnState& A, const char* Qh, const char* Ql, int lane) {
 #pragma unroll
   for (int db = 0; db < 2; ++db) {
@@ -1530,7 +1599,21 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     MKX_TR(c, 1);
     AttnState A;
     attn_begin(A, Qh, Ql, c.lane);
-    for (int cc = 0; cc < nch; ++cc) {
+    if (nch <= 3) {
+      // every chunk is resident: wave w's 32-key blocks w, w + 4 (one 64-key step) and w + 8
+      const int k0 = c.wave * 32, k1 = 128 + c.wave * 32, k2 = 256 + c.wave * 32;
+      char* s0 = ca_slot(c, 0);
+      char* s1 = ca_slot(c, 1);
+      char* s2 = ca_slot(c, 2);
+      if (k1 < S_len)
+        attn_block2(A, c.lane, s0 + c.wave * 4096, s0 + 16384 + c.wave * 4096, S_len - k0, s1 + c.wave * 4096,
+                    s1 + 16384 + c.wave * 4096, S_len - k1, p.sm_scale);
+      else if (k0 < S_len)
+        attn_block(A, c.lane, s0 + c.wave * 4096, nullptr, s0 + 16384 + c.wave * 4096, nullptr, 0, S_len - k0, p.sm_scale, nullptr);
+      if (k2 < S_len)
+        attn_block(A, c.lane, s2 + c.wave * 4096, nullptr, s2 + 16384 + c.wave * 4096, nullptr, 0, S_len - k2, p.sm_scale, nullptr);
+    }
+    for (int cc = 0; nch > 3 && cc < nch; ++cc) {
       if (cc >= 3) {
         // chunk cc was issued three iterations ago; the younger chunks cc + 1, cc + 2 may still be in
         // flight: 8 DMAs per wave each, except the last chunk, which may issue fewer
