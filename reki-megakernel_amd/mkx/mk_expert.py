@@ -16,6 +16,7 @@ import torch
 
 from . import _lib
 from ._lib import MkxDims, MkxStepArgs, MkxWeights, check, lib
+from .pack import LINEARS, PackedExpert, pack_expert, validate
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -31,73 +32,54 @@ class ExpertMegakernel:
 
     def __init__(self, model, registers_in_loop: bool | None = None, max_rows: int = 128, max_batch: int = 16,
                  max_mem_rows: int = 256, max_src_rows: int = 1 << 16):
-        vwe = model.vlm_with_expert
-        layers = list(vwe.action_expert.layers)
-        sa0 = layers[0].self_attn
-        self.L, self.NH, self.HD = len(layers), sa0.n_q_heads, sa0.head_dim
+        # stacked exactly as the reference stacks them (src/mk_expert.py:445-460); fp8 e4m3 linear weights
+        # (a ``weight_q`` tensor with per-output-channel ``weight_scale`` beside each linear) go as bytes
+        # plus fp32 scales, otherwise bf16
+        packed = pack_expert(model)
+        packed.tensors.pop("reg_tok", None)
+        self._create(packed, getattr(model, "register_tokens", None), registers_in_loop, max_rows, max_batch,
+                     max_mem_rows, max_src_rows)
+
+    @classmethod
+    def from_packed(cls, packed: PackedExpert, registers_in_loop: bool | None = None, max_rows: int = 128,
+                    max_batch: int = 16, max_mem_rows: int = 256, max_src_rows: int = 1 << 16) -> "ExpertMegakernel":
+        """A handle built from a packed expert (``pack.load_packed(path, device)``) instead of a model; its
+        ``reg_tok`` tensor, when present, gives the register rows' layer-0 input."""
+        self = cls.__new__(cls)
+        self._create(packed, packed.tensors.get("reg_tok"), registers_in_loop, max_rows, max_batch, max_mem_rows,
+                     max_src_rows)
+        return self
+
+    def _create(self, packed: PackedExpert, register_tokens, registers_in_loop, max_rows, max_batch, max_mem_rows,
+                max_src_rows) -> None:
+        validate(packed)
+        m, t = packed.meta, packed.tensors
+        self.L, self.NH, self.HD, self.I, self.A = (int(m[k]) for k in ("L", "NH", "HD", "I", "A"))
         self.H = self.NH * self.HD
-        self.I = layers[0].mlp.gate_proj.out_features
-        self.A = model.action_in_proj.in_features
-        if sa0.n_kv_heads != self.NH or layers[0].cross_attn.n_kv_heads != self.NH:
-            raise ValueError("the megakernel implements multi-head attention only (n_kv_heads == n_q_heads)")
-        bf = torch.bfloat16
-        st = lambda f: torch.stack([f(lay).detach().to(bf) for lay in layers]).contiguous()  # noqa: E731
-        # fp8 e4m3 linear weights (a ``weight_q`` tensor with per-output-channel ``weight_scale`` beside
-        # each linear): passed as bytes plus fp32 scales; otherwise bf16
-        q0 = getattr(layers[0].self_attn.q_proj, "weight_q", None)
-        self.fp8 = q0 is not None and q0.dtype == torch.float8_e4m3fn
-        lins = {
-            "qkv": lambda m: (m.self_attn.q_proj, m.self_attn.k_proj, m.self_attn.v_proj),
-            "o": lambda m: (m.self_attn.o_proj,), "qca": lambda m: (m.cross_attn.q_proj,),
-            "oca": lambda m: (m.cross_attn.o_proj,), "g": lambda m: (m.mlp.gate_proj,),
-            "u": lambda m: (m.mlp.up_proj,), "d": lambda m: (m.mlp.down_proj,),
-        }
-        ws, scs = {}, {}
-        for k, f in lins.items():
-            if self.fp8:
-                ws[k] = torch.stack([torch.cat([lin.weight_q.detach().view(torch.uint8) for lin in f(lay)], 0)
-                                     for lay in layers]).contiguous()
-                scs[k] = torch.stack([torch.cat([lin.weight_scale.detach().float().reshape(-1) for lin in f(lay)], 0)
-                                      for lay in layers]).contiguous()
-            else:
-                ws[k] = st(lambda m, f=f: torch.cat([lin.weight for lin in f(m)], 0))
-        wqkv, wo, wqca, woca, wg, wu, wd = (ws[k] for k in ("qkv", "o", "qca", "oca", "g", "u", "d"))
-        qn = st(lambda m: m.self_attn.q_norm.weight)
-        kn = st(lambda m: m.self_attn.k_norm.weight)
-        qcan = st(lambda m: m.cross_attn.q_norm.weight)
-        win = model.action_in_proj.weight.detach().float().t().contiguous()  # [A, H]
-        b_in = model.action_in_proj.bias.detach().float().contiguous()
-        wout = model.action_out_proj.weight.detach().float().contiguous()
-        bout = model.action_out_proj.bias.detach().float().contiguous()
-        self.eps = float(layers[0].input_layernorm.eps)
-        if float(vwe.action_expert.norm.eps) != self.eps:
-            raise ValueError("final norm eps differs from the layer norm eps")
-        self.qk_eps = float(sa0.q_norm.eps)
-        act = layers[0].mlp.act_fn
-        if isinstance(act, torch.nn.SiLU) or type(act).__name__ in ("SiLU", "SiLUActivation"):
-            self.activation = _lib.ACT_SILU
-        elif isinstance(act, torch.nn.GELU) and getattr(act, "approximate", "none") == "tanh":
-            self.activation = _lib.ACT_GELU_TANH
-        else:
-            raise ValueError(f"unsupported MLP activation {type(act).__name__}")
-        self.register_tokens = getattr(model, "register_tokens", None)
+        self.fp8 = packed.fp8
+        self.eps, self.qk_eps = float(m["eps"]), float(m["qk_eps"])
+        self.activation = _lib.ACT_SILU if m["activation"] == "silu" else _lib.ACT_GELU_TANH
+        self.register_tokens = register_tokens
         self.registers_in_loop = registers_in_loop
+        dev = t["wqkv"].device
+        if dev.type != "cuda" or any(v.device != dev for v in t.values()):
+            raise ValueError("packed expert tensors must all sit on one GPU")
+        # the library reads e4m3 weights as bytes
+        t = {k: (v.view(torch.uint8) if v.dtype == torch.float8_e4m3fn else v).contiguous() for k, v in t.items()}
         dims = MkxDims(L=self.L, H=self.H, NH=self.NH, HD=self.HD, I=self.I, A=self.A, max_rows=max_rows,
                        max_batch=max_batch, max_mem_rows=max_mem_rows, max_src_rows=max_src_rows,
                        weight_dtype=_lib.WEIGHTS_FP8_E4M3 if self.fp8 else _lib.WEIGHTS_BF16, activation=self.activation,
                        eps=self.eps, qk_eps=self.qk_eps)
-        w = MkxWeights(wqkv=_ptr(wqkv), wo=_ptr(wo), wqca=_ptr(wqca), woca=_ptr(woca), wg=_ptr(wg), wu=_ptr(wu),
-                       wd=_ptr(wd), qn=_ptr(qn), kn=_ptr(kn), qcan=_ptr(qcan), win=_ptr(win), bin=_ptr(b_in),
-                       wout=_ptr(wout), bout=_ptr(bout))
+        w = MkxWeights(**{k: _ptr(t[k]) for k in LINEARS + ("qn", "kn", "qcan", "win", "bin", "wout", "bout")})
         if self.fp8:
-            w.wqkv_scale, w.wo_scale, w.wqca_scale, w.woca_scale, w.wg_scale, w.wu_scale, w.wd_scale = (
-                _ptr(scs[k]) for k in ("qkv", "o", "qca", "oca", "g", "u", "d"))
+            for k in LINEARS:
+                setattr(w, k + "_scale", _ptr(t[k + "_scale"]))
         h = ctypes.c_void_p()
         check(lib().mkx_create(ctypes.byref(dims), ctypes.byref(w), ctypes.c_void_p(_stream()), ctypes.byref(h)), "mkx_create")
         self._h = h
         self.nprog = int(lib().mkx_query(h, _lib.Q_GRID))
         self.weight_bytes = int(lib().mkx_query(h, _lib.Q_WEIGHT_BYTES))
-        self.device = wqkv.device
+        self.device = dev
         self.cfg = {"block": int(lib().mkx_query(h, _lib.Q_BLOCK)), "lds_bytes": int(lib().mkx_query(h, _lib.Q_LDS_BYTES)),
                     "grid": self.nprog, "PROFILE": False}
 

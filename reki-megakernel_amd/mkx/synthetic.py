@@ -24,6 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
+from .pack import dequantize_e4m3, quantize_e4m3
 
 
 @dataclass(frozen=True)
@@ -127,9 +128,8 @@ def make_weights(cfg: ExpertConfig, seed: int = 0) -> dict:
     def lin(*shape):
         w = n(*shape)
         if cfg.weight_dtype == "fp8_e4m3":
-            scale = w.abs().amax(-1, keepdim=True).clamp_min(1e-12) / 448.0
-            q = (w / scale).to(torch.float8_e4m3fn)
-            return {"w": (q.to(torch.float32) * scale), "q": q, "scale": scale.squeeze(-1).float()}
+            q, scale = quantize_e4m3(w)
+            return {"w": dequantize_e4m3(q, scale), "q": q, "scale": scale}
         return {"w": w.to(torch.bfloat16)}
 
     layers = []

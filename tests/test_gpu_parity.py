@@ -13,6 +13,7 @@ import torch
 from _cases import TINY, diff, make_case, oracle_steps
 from mkx import ExpertMegakernel, install, synthetic as SY
 from mkx._lib import MkxError
+from mkx.pack import attach_fp8, load_packed, pack_expert, save_packed
 
 pytestmark = pytest.mark.gpu
 torch.set_grad_enabled(False)
@@ -236,6 +237,44 @@ def test_install_matches_first_step_plus_run():
     torch.cuda.synchronize()
     assert torch.equal(x, x_ref)
     assert ck.shape == (cfg.L, 1, cfg.R_reg, cfg.NH, cfg.HD)
+
+
+def test_packed_fp8_file_drives_the_kernel(tmp_path):
+    """An fp8 file packed offline from a bf16 model: the handle built from the loaded file equals, bit for
+    bit, the one built from the model with the file's codes attached, and tracks the fp32 oracle run on
+    the file's dequantised weights."""
+    case = make_case(TINY)
+    cfg = case["cfg"]
+    path = str(tmp_path / "expert_fp8.safetensors")
+    save_packed(pack_expert(case["model"], "fp8_e4m3"), path)
+    p = load_packed(path, "cuda")
+    x1, _, _ = case["model"]._expert_first_step(case["noise"], case["past"], None, case["mods"][..., :1, :], case["dt"], cfg.action_dim)
+    mk_file = ExpertMegakernel.from_packed(p)
+    assert mk_file.fp8
+    x_file = mk_file.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    mk_file.check()
+    attach_fp8(case["model"], p)
+    mk_model = ExpertMegakernel(case["model"])
+    x_model = mk_model.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    mk_model.check()
+    torch.cuda.synchronize()
+    assert torch.equal(x_file, x_model)
+    pc = p.to("cpu")
+    split = {"wqkv": ("q", "k", "v"), "wo": ("o",), "wqca": ("ca_q",), "woca": ("ca_o",), "wg": ("gate",),
+             "wu": ("up",), "wd": ("down",)}
+    layers = []
+    for l, ly in enumerate(case["W"]["layers"]):
+        ly = dict(ly)
+        for stack, names in split.items():
+            deq = pc.dequantized(stack)[l]
+            for i, nm in enumerate(names):
+                ly[nm] = deq[i * ly[nm].shape[0]: (i + 1) * ly[nm].shape[0]]
+        layers.append(ly)
+    case_q = dict(case, W={**case["W"], "layers": layers})
+    r32 = oracle_steps(case_q, x1, 1, cfg.num_steps - 1, "fp32")
+    m32, a32 = diff(x_file, r32, cfg.action_dim)
+    _report("packed fp8 file (tiny)", vs_fp32_max=m32, vs_fp32_mean=a32)
+    assert m32 <= TIGHT_MAX and a32 <= TIGHT_MEAN, (m32, a32)
 
 
 def test_invalid_arguments_raise():
