@@ -9,6 +9,8 @@
  *   mkx_barriers <- ExpertMegakernel.barriers   (src/mk_expert.py:517-518: stage boundaries per launch)
  *   mkx_query    <- attributes the reference reads off the object (nprog, bar, prof; test_mk.py:44-45,
  *                   tune_mk.py:131-153)
+ *   mkx_ring_append <- the register cache's per-frame append after each expert call (append_frame,
+ *                   src/profile_breakdown.py:97-104) that refills past.register_step['mem_kv'] / cu_kv
  *   mkx_destroy, mkx_last_error, mkx_status_string: lifetime and error reporting the Python object
  *                   had implicitly (the reference only asserts, src/mk_expert.py:444, 464, 480, 488, 496).
  *
@@ -148,6 +150,38 @@ int64_t mkx_barriers(const mkx_handle* h, int32_t n_steps);
  * workgroup 0, the ns clock when it passes stage boundary nb into buf[nb] (buf[0] = launch start). buf is a caller-owned
  * device int64 array of len entries (>= mkx_barriers(n_steps) + 1); NULL turns profiling off. */
 int mkx_set_profile(mkx_handle* h, int64_t* buf, int32_t len);
+
+/* Register-memory ring append, the step after an expert call (no handle needed). Reference: the memory
+ * the expert reads, past.register_step['mem_kv'] with kv_start = cu_kv[0] (src/mk_expert.py:489-490, 321),
+ * which REKI's register cache refills after every call from the call's register rows (append_frame,
+ * timed at src/profile_breakdown.py:97-104; 32 register tokens per frame kept over 3 frames, README.md:27).
+ * Per layer l and sample b, memory rows [kv_start, PM) are valid, K normed and rotated at the row index.
+ * Out row j = in row j + R for j < PM - R (K rotated by shift_cos/shift_sin, normally -R positions),
+ * else the call's register row j - (PM - R) of cur_k/cur_v (K rotated by new_cos/new_sin, from its
+ * position in the call to row j); rows below kv_start_out = max(kv_start_in - R, 0) are zeroed. kv_start_in
+ * is clamped to [0, PM]. NULL tables mean no rotation. Rotations are fp32 products and one sum per
+ * element (no fused multiply-add), rounded to bf16 to nearest even. Out buffers must not overlap the in
+ * buffers (ping-pong two sets); asynchronous on `stream`. */
+typedef struct {
+  int32_t L, B, NH, HD;   /* HD must be 64 */
+  int32_t PM;             /* memory rows per sample */
+  int32_t R;              /* rows appended per call, 1 <= R <= PM */
+  const void* cur_k;      /* [L, B, R, NH, HD] bf16 register-row K of the call (normed, rotated; run_first's cur_k) */
+  const void* cur_v;      /* [L, B, R, NH, HD] bf16 */
+  const void* memk_in[MKX_MAX_LAYERS];  /* per layer [B, PM, NH, HD] bf16 */
+  const void* memv_in[MKX_MAX_LAYERS];
+  void* memk_out[MKX_MAX_LAYERS];       /* per layer [B, PM, NH, HD] bf16 */
+  void* memv_out[MKX_MAX_LAYERS];
+  int64_t mem_stride_b;                  /* elements between samples, in and out buffers */
+  const int32_t* kv_start_in;            /* [B] device */
+  int32_t* kv_start_out;                 /* [B] device, not aliasing kv_start_in */
+  const float* shift_cos;                /* [HD] fp32 rotation of kept rows, or NULL */
+  const float* shift_sin;
+  const float* new_cos;                  /* [HD] fp32 rotation of appended rows, or NULL */
+  const float* new_sin;
+} mkx_ring_args;
+
+int mkx_ring_append(const mkx_ring_args* args, void* stream);
 
 int64_t mkx_query(const mkx_handle* h, int32_t key);
 int mkx_destroy(mkx_handle* h);

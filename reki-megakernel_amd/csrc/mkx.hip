@@ -10,6 +10,7 @@
 
 #include "mkx.h"
 #include "mkx_kernel.h"
+#include "mkx_ring.h"
 
 using namespace mkx;
 
@@ -443,6 +444,51 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
     HIPCHK(hipLaunchCooperativeKernel(h->kernel, dim3(h->G), dim3(NTHREADS), args, 0, stream));
   }
   h->last_nbar = mkx_barriers(h, a->n_steps);
+  return MKX_OK;
+}
+
+int mkx_ring_append(const mkx_ring_args* a, void* stream_) {
+  if (!a) return fail(MKX_EINVAL, "mkx_ring_append: args is NULL");
+  if (a->L < 1 || a->L > MKX_MAX_LAYERS || a->B < 1 || a->NH < 1 || a->HD != 64 || a->PM < 1 || a->R < 1 ||
+      a->R > a->PM)
+    return fail(MKX_EINVAL, "mkx_ring_append: need 1 <= L <= 32, B >= 1, NH >= 1, HD == 64, 1 <= R <= PM");
+  if ((int64_t)a->PM * a->NH * 4 > (int64_t)1 << 30 || a->B > 65535)
+    return fail(MKX_EINVAL, "mkx_ring_append: shape too large");
+  const int64_t row_elems = (int64_t)a->NH * 64;
+  if (a->mem_stride_b < a->PM * row_elems && a->B > 1)
+    return fail(MKX_EINVAL, "mkx_ring_append: mem_stride_b smaller than one sample's memory");
+  if (!a->cur_k || !a->cur_v || !a->kv_start_in || !a->kv_start_out)
+    return fail(MKX_EINVAL, "mkx_ring_append: cur_k, cur_v, kv_start_in and kv_start_out are required");
+  if (a->kv_start_in == a->kv_start_out) return fail(MKX_EINVAL, "mkx_ring_append: kv_start_out aliases kv_start_in");
+  if ((a->shift_cos == nullptr) != (a->shift_sin == nullptr) || (a->new_cos == nullptr) != (a->new_sin == nullptr))
+    return fail(MKX_EINVAL, "mkx_ring_append: pass both or neither of each cos/sin pair");
+  auto misaligned = [](const void* p) { return ((uintptr_t)p & 15u) != 0; };
+  if (misaligned(a->cur_k) || misaligned(a->cur_v) || (a->mem_stride_b & 7))
+    return fail(MKX_EINVAL, "mkx_ring_append: caches must be 16-byte aligned (mem_stride_b a multiple of 8)");
+  // one sample's memory spans [p, p + (B - 1) stride + PM row) elements; out must not overlap any input
+  const uint64_t span = (uint64_t)(((int64_t)a->B - 1) * a->mem_stride_b + a->PM * row_elems) * 2;
+  for (int l = 0; l < a->L; ++l) {
+    const void* ins[2] = {a->memk_in[l], a->memv_in[l]};
+    const void* outs[2] = {a->memk_out[l], a->memv_out[l]};
+    for (const void* p : ins)
+      if (!p || misaligned(p)) return fail(MKX_EINVAL, "mkx_ring_append: memory input NULL or misaligned");
+    for (const void* p : outs)
+      if (!p || misaligned(p)) return fail(MKX_EINVAL, "mkx_ring_append: memory output NULL or misaligned");
+    for (int l2 = 0; l2 < a->L; ++l2)
+      for (const void* o : outs)
+        for (const void* i : {a->memk_in[l2], a->memv_in[l2], a->cur_k, a->cur_v}) {
+          const uint64_t po = (uint64_t)(uintptr_t)o, pi = (uint64_t)(uintptr_t)i;
+          const uint64_t ispan = (i == a->cur_k || i == a->cur_v)
+                                     ? (uint64_t)a->L * a->B * a->R * row_elems * 2 : span;
+          if (po < pi + ispan && pi < po + span)
+            return fail(MKX_EINVAL, "mkx_ring_append: an output buffer overlaps an input (use two buffer sets)");
+        }
+  }
+  hipStream_t stream = (hipStream_t)stream_;
+  const int lanes = a->PM * a->NH * 4;
+  dim3 grid((lanes + RING_BLOCK - 1) / RING_BLOCK, 2 * a->L, a->B);
+  hipLaunchKernelGGL(ring_append_kernel, grid, dim3(RING_BLOCK), 0, stream, *a);
+  HIPCHK(hipGetLastError());
   return MKX_OK;
 }
 

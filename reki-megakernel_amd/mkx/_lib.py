@@ -14,7 +14,7 @@ ACT_SILU, ACT_GELU_TANH = 0, 1
 Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WEIGHT_BYTES, Q_LDS_BYTES = range(8)
 
 EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
-           "mkx_last_error", "mkx_status_string", "mkx_abi_version")
+           "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append")
 
 _vp = ctypes.c_void_p
 
@@ -42,6 +42,14 @@ class MkxStepArgs(ctypes.Structure):
                 ("ca_cos", _vp), ("ca_sin", _vp), ("reg_tok", _vp), ("cur_k", _vp), ("cur_v", _vp),
                 ("n_steps", ctypes.c_int32), ("action_dim", ctypes.c_int32), ("T_act", ctypes.c_int32),
                 ("R_reg", ctypes.c_int32), ("B", ctypes.c_int32), ("PM", ctypes.c_int32), ("SP", ctypes.c_int32)]
+
+
+class MkxRingArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("L", "B", "NH", "HD", "PM", "R")] + \
+               [("cur_k", _vp), ("cur_v", _vp), ("memk_in", _vp * MAX_LAYERS), ("memv_in", _vp * MAX_LAYERS),
+                ("memk_out", _vp * MAX_LAYERS), ("memv_out", _vp * MAX_LAYERS), ("mem_stride_b", ctypes.c_int64),
+                ("kv_start_in", _vp), ("kv_start_out", _vp), ("shift_cos", _vp), ("shift_sin", _vp),
+                ("new_cos", _vp), ("new_sin", _vp)]
 
 
 class MkxError(RuntimeError):
@@ -73,6 +81,7 @@ def lib() -> ctypes.CDLL:
         L.mkx_status_string.argtypes = [ctypes.c_int]
         L.mkx_status_string.restype = ctypes.c_char_p
         L.mkx_abi_version.restype = ctypes.c_int32
+        L.mkx_ring_append.argtypes = [ctypes.POINTER(MkxRingArgs), _vp]
         _LIB = L
     return _LIB
 

@@ -363,6 +363,18 @@ class SyntheticReki:
         }
         return Past(step, ca_kv)
 
+    def register_ring(self, past: Past):
+        """A ``RegisterRing`` over ``past``'s memory for this model's position convention: memory K is rotated
+        at its row index and a call's register row r at PM + T_act + r (step 1's own rows are
+        [T_act action rows || R_reg register rows] at PM + i), so kept rows turn by -R_reg and appended
+        rows by -(T_act + R_reg). ``ring.append_frame(cur_k, cur_v)`` after a call, then
+        ``ring.update_past(past)`` before the next."""
+        from .ring import RegisterRing
+        cfg = self.cfg
+        st = past.register_step
+        return RegisterRing(st["mem_kv"], st["kv_start"], cfg.R_reg, kept_delta=-cfg.R_reg,
+                            new_delta=-(cfg.T_act + cfg.R_reg))
+
     # -- REKI: _expert_first_step(noise, past, register_cache, mods[:1], dt, action_dim) -> (x_t, cur_k, cur_v)
     def _expert_first_step(self, noise, past: Past, register_cache, mods1, dt, action_dim: int):
         """Euler step 1 over [action rows || register rows], run by the megakernel with one step and
