@@ -46,6 +46,41 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def ring_append_bench(cfg, n: int) -> int:
+    """Times the register-memory ring append (one launch for all layers and samples) over the workload's
+    memory: per (layer, sample) K and V of PM rows are read (PM - R kept rows and the R new ones) and
+    written, 2 x 2 x PM x NH x 64 x 2 bytes."""
+    import torch
+    from mkx.ring import RegisterRing
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    L, B, PM, NH, R = cfg.L, cfg.B, cfg.PM, cfg.NH, cfg.R_reg
+    mem_kv = [(torch.randn(B, PM, NH, 64, device=dev, generator=g).to(torch.bfloat16),
+               torch.randn(B, PM, NH, 64, device=dev, generator=g).to(torch.bfloat16)) for _ in range(L)]
+    ring = RegisterRing(mem_kv, [0] * B, R, kept_delta=-R, new_delta=-(cfg.T_act + R))
+    ck = torch.randn(L, B, R, NH, 64, device=dev, generator=g).to(torch.bfloat16)
+    cv = torch.randn(L, B, R, NH, 64, device=dev, generator=g).to(torch.bfloat16)
+    for _ in range(10):
+        ring.append_frame(ck, cv)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        starts[i].record(stream)
+        ring.append_frame(ck, cv)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends)) * 1e3
+    nbytes = 2 * 2 * L * B * PM * NH * 64 * 2
+    print(json.dumps({"ring_append": {"workload": {"L": L, "B": B, "PM": PM, "NH": NH, "R": R}, "launches": n,
+                                      "us_per_launch_median": round(us, 3), "algorithmic_bytes": nbytes,
+                                      "GB_s": round(nbytes / us / 1e3, 1), "frac_of_8TB_s": round(nbytes / us / 8e6, 4)}}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -57,6 +92,8 @@ def main() -> int:
     ap.add_argument("--stage-profile", action="store_true", help="also print per-stage barrier timestamps (stderr)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (reference kernel for the HBM traffic counters)")
+    ap.add_argument("--ring-append", type=int, default=0, metavar="N",
+                    help="only time N register-memory ring appends over the workload's memory (L, B, PM, NH; R rows)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the megakernel runs on a single MI355X (batch samples would shard "
@@ -78,6 +115,8 @@ def main() -> int:
 
     torch.set_grad_enabled(False)
     cfg = SY.WORKLOADS[args.workload]
+    if args.ring_append:
+        return ring_append_bench(cfg, args.ring_append)
     dev = torch.device("cuda:0")
     W = SY.make_weights(cfg, seed=0)
     model = SY.SyntheticReki(cfg, W, device=dev)
