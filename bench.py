@@ -81,6 +81,42 @@ def ring_append_bench(cfg, n: int) -> int:
     return 0
 
 
+def prepare_source_bench(cfg, n: int) -> int:
+    """Times the cross-attention source preparation (one launch: every layer's K and V projection of the
+    context, K norm and RoPE): algorithmic bytes = the K/V weights (L x 2H x C x 2) + the context
+    (B x SP x C x 2) + the caches written (L x 2 x B x SP x H x 2); flops = 2 x B x SP x C x 2H x L."""
+    import torch
+    from mkx import synthetic as SY
+    from mkx.prepare import SourcePrepare
+
+    dev = torch.device("cuda:0")
+    model = SY.SyntheticReki(cfg, SY.make_weights(cfg, seed=0), device=dev)
+    ctx = SY.make_inputs(cfg)["ctx"].to(dev)
+    prep = SourcePrepare(model)
+    ca_len = [cfg.S] * cfg.B
+    for _ in range(5):
+        prep(ctx, ca_len)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        starts[i].record(stream)
+        prep(ctx, ca_len)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends)) * 1e3
+    H, C = cfg.H, cfg.ctx_dim
+    nbytes = cfg.L * 2 * H * C * 2 + cfg.B * cfg.SP * C * 2 + cfg.L * 2 * cfg.B * cfg.SP * H * 2
+    flops = 2 * cfg.B * cfg.SP * C * 2 * H * cfg.L
+    print(json.dumps({"prepare_source": {"workload": {"L": cfg.L, "B": cfg.B, "SP": cfg.SP, "C": C, "H": H},
+                                         "launches": n, "us_per_launch_median": round(us, 3),
+                                         "algorithmic_bytes": nbytes, "flops": flops,
+                                         "GB_s": round(nbytes / us / 1e3, 1), "TFLOP_s": round(flops / us / 1e6, 2)}}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,6 +130,8 @@ def main() -> int:
                     help="only run 5 device copies of MIB MiB (reference kernel for the HBM traffic counters)")
     ap.add_argument("--ring-append", type=int, default=0, metavar="N",
                     help="only time N register-memory ring appends over the workload's memory (L, B, PM, NH; R rows)")
+    ap.add_argument("--prepare-source", type=int, default=0, metavar="N",
+                    help="only time N cross-attention source preparations of the workload's context")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the megakernel runs on a single MI355X (batch samples would shard "
@@ -117,6 +155,8 @@ def main() -> int:
     cfg = SY.WORKLOADS[args.workload]
     if args.ring_append:
         return ring_append_bench(cfg, args.ring_append)
+    if args.prepare_source:
+        return prepare_source_bench(cfg, args.prepare_source)
     dev = torch.device("cuda:0")
     W = SY.make_weights(cfg, seed=0)
     model = SY.SyntheticReki(cfg, W, device=dev)

@@ -11,6 +11,8 @@
  *                   tune_mk.py:131-153)
  *   mkx_ring_append <- the register cache's per-frame append after each expert call (append_frame,
  *                   src/profile_breakdown.py:97-104) that refills past.register_step['mem_kv'] / cu_kv
+ *   mkx_source_create / _run / _destroy <- the cross-attention source K/V of REKI's register_prepare
+ *                   (mk_expert.py:22-24, 491-492: past.cross_attn_kv, which the expert call reads)
  *   mkx_destroy, mkx_last_error, mkx_status_string: lifetime and error reporting the Python object
  *                   had implicitly (the reference only asserts, src/mk_expert.py:444, 464, 480, 488, 496).
  *
@@ -182,6 +184,42 @@ typedef struct {
 } mkx_ring_args;
 
 int mkx_ring_append(const mkx_ring_args* args, void* stream);
+
+/* Cross-attention source caches: per layer l, K = norm_rope(bf16(ctx Wk[l]^T)) and V = bf16(ctx Wv[l]^T)
+ * as bf16 [B, SP, NH, 64], rows >= ca_len[b] zero. Reference: past.cross_attn_kv (src/mk_expert.py:491-492),
+ * made by REKI's register_prepare (mk_expert.py:22-24; README.md:279-281: "the cross-attention K/V
+ * projections of the VLM source (31 M weights)"). norm_rope: per head, x * rsqrt(mean(x^2) + eps) *
+ * (1 + k_norm[l]) rounded to bf16, then x * cos + rotate_half(x) * sin at the row's source position,
+ * rounded to bf16. fp32 accumulation on bf16 MFMA.
+ * mkx_source_create copies and repacks the weights once (synchronising `stream`) and owns a context
+ * staging buffer of max_rows rows; mkx_source_run is asynchronous on `stream`, and calls on one handle
+ * share that buffer (one handle per stream). */
+typedef struct mkx_source mkx_source;
+
+typedef struct {
+  int32_t L, NH, HD;       /* HD must be 64 */
+  int32_t C;               /* context width, a multiple of 32 */
+  int32_t max_rows;        /* max B * SP per call */
+  float eps;               /* k-norm eps (cross_attn.k_norm.eps) */
+} mkx_source_dims;
+
+typedef struct {
+  int32_t B, SP;           /* samples, source rows per sample (padded); B * SP <= max_rows */
+  const void* ctx;         /* [B, SP, C] bf16 VLM context, 16-byte aligned */
+  const int32_t* ca_len;   /* [B] device: valid source rows (clamped to [0, SP]) */
+  const float* cos;        /* [SP, 64] fp32 RoPE table of source positions */
+  const float* sin;
+  void* kca[MKX_MAX_LAYERS]; /* per layer [B, SP, NH, 64] bf16 out, 8-byte aligned */
+  void* vca[MKX_MAX_LAYERS];
+  int64_t src_stride_b;    /* elements between samples of kca / vca */
+} mkx_source_args;
+
+/* wk, wv: [L, NH * 64, C] bf16 cross_attn.k_proj / v_proj weights stacked over layers; k_norm: [L, 64]
+ * bf16 cross_attn.k_norm.weight (used as 1 + w). All device pointers. */
+int mkx_source_create(const mkx_source_dims* dims, const void* wk, const void* wv, const void* k_norm, void* stream,
+                      mkx_source** out);
+int mkx_source_run(mkx_source* h, const mkx_source_args* args, void* stream);
+int mkx_source_destroy(mkx_source* h);
 
 int64_t mkx_query(const mkx_handle* h, int32_t key);
 int mkx_destroy(mkx_handle* h);

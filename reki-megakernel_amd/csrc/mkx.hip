@@ -11,6 +11,7 @@
 #include "mkx.h"
 #include "mkx_kernel.h"
 #include "mkx_ring.h"
+#include "mkx_prepare.h"
 
 using namespace mkx;
 
@@ -146,6 +147,21 @@ static void free_handle(mkx_handle* h) {
   void* ptrs[] = {h->wqkv, h->wo, h->wqca, h->woca, h->wgu, h->wd, h->qn, h->kn, h->qcan, h->win, h->bin,
                   h->wout, h->bout, h->frames, h->steps, h->vts, h->bar, h->flags, h->scales};
   for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  delete h;
+}
+
+struct mkx_source {
+  mkx_source_dims dims{};
+  bf16_t* wkp = nullptr;   // [L][NH][C/32][4][64][8] fragment-order K weights
+  bf16_t* wvp = nullptr;
+  bf16_t* kn = nullptr;    // [L, 64]
+  bf16_t* ctxp = nullptr;  // staging: the call's context in fragment order
+};
+
+static void free_source(mkx_source* h) {
+  if (!h) return;
+  for (void* p : {(void*)h->wkp, (void*)h->wvp, (void*)h->kn, (void*)h->ctxp})
     if (p) (void)hipFree(p);
   delete h;
 }
@@ -489,6 +505,86 @@ int mkx_ring_append(const mkx_ring_args* a, void* stream_) {
   dim3 grid((lanes + RING_BLOCK - 1) / RING_BLOCK, 2 * a->L, a->B);
   hipLaunchKernelGGL(ring_append_kernel, grid, dim3(RING_BLOCK), 0, stream, *a);
   HIPCHK(hipGetLastError());
+  return MKX_OK;
+}
+
+int mkx_source_create(const mkx_source_dims* d, const void* wk, const void* wv, const void* k_norm, void* stream_,
+                      mkx_source** out) {
+  if (!out) return fail(MKX_EINVAL, "mkx_source_create: out is NULL");
+  *out = nullptr;
+  if (!d) return fail(MKX_EINVAL, "mkx_source_create: dims is NULL");
+  if (d->L < 1 || d->L > MKX_MAX_LAYERS || d->NH < 1 || d->HD != 64 || d->C < 32 || (d->C & 31) || d->max_rows < 1)
+    return fail(MKX_EINVAL, "mkx_source_create: need 1 <= L <= 32, NH >= 1, HD == 64, C a multiple of 32, max_rows >= 1");
+  if ((int64_t)d->L * 2 * d->NH > 65535 || (int64_t)d->max_rows * d->C > ((int64_t)1 << 34) ||
+      (int64_t)d->L * d->NH * 64 * d->C > ((int64_t)1 << 34))
+    return fail(MKX_EINVAL, "mkx_source_create: shape too large");
+  if (!(d->eps >= 0.f)) return fail(MKX_EINVAL, "mkx_source_create: eps must be >= 0");
+  auto bad16 = [](const void* p) { return p == nullptr || ((uintptr_t)p & 15u) != 0; };
+  if (bad16(wk) || bad16(wv) || k_norm == nullptr || ((uintptr_t)k_norm & 1u))
+    return fail(MKX_EINVAL, "mkx_source_create: wk / wv NULL or not 16-byte aligned, or k_norm NULL / misaligned");
+  hipStream_t stream = (hipStream_t)stream_;
+  mkx_source* h = new mkx_source();
+  h->dims = *d;
+  const int64_t wel = (int64_t)d->L * d->NH * 64 * d->C;
+  const int64_t rows_pad = ((int64_t)d->max_rows + 63) / 64 * 64;
+  auto cleanup = [&](int code, const std::string& msg) {
+    free_source(h);
+    return fail(code, msg);
+  };
+  if (hipMalloc(&h->wkp, wel * 2) != hipSuccess || hipMalloc(&h->wvp, wel * 2) != hipSuccess ||
+      hipMalloc(&h->kn, (size_t)d->L * 64 * 2) != hipSuccess || hipMalloc(&h->ctxp, rows_pad * d->C * 2) != hipSuccess)
+    return cleanup(MKX_ENOMEM, "mkx_source_create: device allocation failed");
+  // weights in fragment order: 16-row groups of one head (S = 4) per head of every layer
+  const long long n_w = wel / 8;
+  const int S = 4, rows_w = d->L * d->NH * 64;
+  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((n_w + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)wk,
+                     h->wkp, rows_w, d->C, S, n_w);
+  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((n_w + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)wv,
+                     h->wvp, rows_w, d->C, S, n_w);
+  if (hipGetLastError() != hipSuccess ||
+      hipMemcpyAsync(h->kn, k_norm, (size_t)d->L * 64 * 2, hipMemcpyDeviceToDevice, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return cleanup(MKX_EHIP, "mkx_source_create: weight packing failed");
+  *out = h;
+  return MKX_OK;
+}
+
+int mkx_source_run(mkx_source* h, const mkx_source_args* a, void* stream_) {
+  if (!h || !a) return fail(MKX_EINVAL, "mkx_source_run: handle or args is NULL");
+  const mkx_source_dims& d = h->dims;
+  if (a->B < 1 || a->SP < 1 || (int64_t)a->B * a->SP > d.max_rows)
+    return fail(MKX_EINVAL, "mkx_source_run: need B, SP >= 1 and B * SP <= max_rows");
+  const int64_t row_elems = (int64_t)d.NH * 64;
+  if (a->B > 1 && a->src_stride_b < a->SP * row_elems)
+    return fail(MKX_EINVAL, "mkx_source_run: src_stride_b smaller than one sample's cache");
+  if (a->src_stride_b & 3) return fail(MKX_EINVAL, "mkx_source_run: src_stride_b must be a multiple of 4");
+  auto bad = [](const void* p, uintptr_t align) { return p == nullptr || ((uintptr_t)p & (align - 1)) != 0; };
+  if (bad(a->ctx, 16) || bad(a->ca_len, 4) || bad(a->cos, 4) || bad(a->sin, 4))
+    return fail(MKX_EINVAL, "mkx_source_run: ctx, ca_len, cos, sin: NULL or misaligned");
+  for (int l = 0; l < d.L; ++l)
+    if (bad(a->kca[l], 8) || bad(a->vca[l], 8))
+      return fail(MKX_EINVAL, "mkx_source_run: kca / vca NULL or not 8-byte aligned");
+  hipStream_t stream = (hipStream_t)stream_;
+  const int nrows = a->B * a->SP;
+  const int tiles = (nrows + 63) / 64;
+  const long long n_x = (long long)tiles * 64 * d.C / 8;  // packed pieces, rows padded to 64 with zeros
+  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((n_x + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)a->ctx,
+                     h->ctxp, nrows, d.C, 1, n_x);
+  SourceParams p{};
+  p.L = d.L; p.NH = d.NH; p.C = d.C; p.B = a->B; p.SP = a->SP;
+  p.ctxp = h->ctxp; p.wkp = h->wkp; p.wvp = h->wvp; p.k_norm = h->kn;
+  p.ca_len = a->ca_len; p.cos = a->cos; p.sin = a->sin;
+  for (int l = 0; l < d.L; ++l) { p.kca[l] = a->kca[l]; p.vca[l] = a->vca[l]; }
+  p.src_sb = a->src_stride_b;
+  p.eps = d.eps;
+  hipLaunchKernelGGL(prepare_source_kernel, dim3((unsigned)tiles, (unsigned)(d.L * 2 * d.NH)), dim3(PREP_BLOCK), 0,
+                     stream, p);
+  HIPCHK(hipGetLastError());
+  return MKX_OK;
+}
+
+int mkx_source_destroy(mkx_source* h) {
+  free_source(h);
   return MKX_OK;
 }
 

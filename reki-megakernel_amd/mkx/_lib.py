@@ -14,7 +14,7 @@ ACT_SILU, ACT_GELU_TANH = 0, 1
 Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WEIGHT_BYTES, Q_LDS_BYTES = range(8)
 
 EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
-           "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append")
+           "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append", "mkx_source_create", "mkx_source_run", "mkx_source_destroy")
 
 _vp = ctypes.c_void_p
 
@@ -52,6 +52,15 @@ class MkxRingArgs(ctypes.Structure):
                 ("new_cos", _vp), ("new_sin", _vp)]
 
 
+class MkxSourceDims(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("L", "NH", "HD", "C", "max_rows")] + [("eps", ctypes.c_float)]
+
+
+class MkxSourceArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("SP", ctypes.c_int32), ("ctx", _vp), ("ca_len", _vp), ("cos", _vp), ("sin", _vp),
+                ("kca", _vp * MAX_LAYERS), ("vca", _vp * MAX_LAYERS), ("src_stride_b", ctypes.c_int64)]
+
+
 class MkxError(RuntimeError):
     def __init__(self, status: int, where: str, detail: str):
         super().__init__(f"{where}: mkx status {status} ({detail})")
@@ -82,6 +91,9 @@ def lib() -> ctypes.CDLL:
         L.mkx_status_string.restype = ctypes.c_char_p
         L.mkx_abi_version.restype = ctypes.c_int32
         L.mkx_ring_append.argtypes = [ctypes.POINTER(MkxRingArgs), _vp]
+        L.mkx_source_create.argtypes = [ctypes.POINTER(MkxSourceDims), _vp, _vp, _vp, _vp, ctypes.POINTER(_vp)]
+        L.mkx_source_run.argtypes = [_vp, ctypes.POINTER(MkxSourceArgs), _vp]
+        L.mkx_source_destroy.argtypes = [_vp]
         _LIB = L
     return _LIB
 

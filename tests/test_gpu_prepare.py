@@ -1,0 +1,125 @@
+"""GPU: ``mkx_prepare_source`` (through the C ABI, via mkx.prepare.SourcePrepare) against the CPU oracle's
+``register_prepare`` in ``mirror`` mode (bf16 rounding after the projection, the norm and the rotation,
+the points the kernel rounds at), and the expert run on the kernel's caches against the fp32 oracle.
+
+Tolerance: accumulation order (MFMA vs the CPU's) and rsqrt can move a bf16 rounding by one unit, and the
+rotation mixes the two halves of a head, so K is bounded per RoPE pair, |delta| <= 2^-6 |(x_d, x_d+32)|,
+and V per element, |delta| <= 2^-7 |v| + 2^-12. A wrong position, sign, norm weight or head fails both by
+orders of magnitude."""
+import json
+from dataclasses import replace
+
+import pytest
+import torch
+
+from _cases import TINY, diff, make_case, oracle_dims, oracle_steps
+from mkx import ExpertMegakernel, synthetic as SY
+from mkx.prepare import SourcePrepare
+from oracle import expert_ref as ER
+
+pytestmark = pytest.mark.gpu
+torch.set_grad_enabled(False)
+
+
+def _report(name, **kv):
+    print(json.dumps({"case": name, **kv}), flush=True)
+
+
+def _check_prepare(name, cfg, ca_len=None):
+    W = SY.make_weights(cfg, 0)
+    model = SY.SyntheticReki(cfg, W, device="cuda")
+    inp = SY.make_inputs(cfg)
+    ca_len = [cfg.S] * cfg.B if ca_len is None else ca_len
+    ctx = inp["ctx"]
+    prep = SourcePrepare(model)
+    kv = prep(ctx.cuda(), ca_len)
+    torch.cuda.synchronize()
+    ref = ER.register_prepare(ctx, ca_len, inp["mem_states"][:, :0], [0] * cfg.B, SY.oracle_weights(W), oracle_dims(cfg),
+                              cfg.m_q, mode="mirror")
+    gk = torch.stack([k for k, _ in kv]).float().cpu()  # [L, B, SP, NH, 64]
+    gv = torch.stack([v for _, v in kv]).float().cpu()
+    rk, rv = ref["kca"].float(), ref["vca"].float()
+    pn = torch.sqrt(rk[..., :32] ** 2 + rk[..., 32:] ** 2).repeat(1, 1, 1, 1, 2)
+    dk, dv = (gk - rk).abs(), (gv - rv).abs()
+    exact_k = float((dk == 0).float().mean())
+    exact_v = float((dv == 0).float().mean())
+    _report(name, k_max=float(dk.max()), v_max=float(dv.max()), k_exact_frac=exact_k, v_exact_frac=exact_v)
+    assert (dk <= 2.0 ** -6 * pn + 1e-6).all()
+    assert (dv <= 2.0 ** -7 * rv.abs() + 2.0 ** -12).all()
+    for b, n in enumerate(ca_len):
+        n = min(max(n, 0), cfg.SP)
+        assert (gk[:, b, n:] == 0).all() and (gv[:, b, n:] == 0).all()
+    return model, kv
+
+
+def test_prepare_tiny():
+    _check_prepare("prepare tiny (C 96, SP 48)", TINY)
+
+
+def test_prepare_config_A_context():
+    _check_prepare("prepare A (L10, C 2048, S 300)", SY.WORKLOADS["A"])
+
+
+def test_prepare_batch_with_ragged_lengths():
+    cfg = replace(SY.WORKLOADS["A"], B=4, L=3)
+    _check_prepare("prepare B4 ragged", cfg, ca_len=[300, 1, 0, 150])
+
+
+def test_prepare_wide_expert():
+    cfg = replace(SY.WORKLOADS["D"], L=4)
+    _check_prepare("prepare D shape (NH16, 4 layers)", cfg)
+
+
+def test_expert_on_kernel_prepared_caches():
+    """Euler steps 2..N on caches from the kernel: within the tight bound of the fp32 oracle run on the
+    same caches, and close to the run on the PyTorch-prepared caches."""
+    case = make_case(SY.WORKLOADS["A"])
+    cfg, model, past = case["cfg"], case["model"], case["past"]
+    x1, _, _ = model._expert_first_step(case["noise"], past, None, case["mods"][..., :1, :], case["dt"], cfg.action_dim)
+    mk = ExpertMegakernel(model)
+    x_torch = mk.run(x1, case["mods"], case["dt"], past, cfg.action_dim)
+    past.cross_attn_kv = SourcePrepare(model)(case["inp"]["ctx"].cuda()[0], [cfg.S])
+    x_kern = mk.run(x1, case["mods"], case["dt"], past, cfg.action_dim)
+    mk.check()
+    torch.cuda.synchronize()
+    r32 = oracle_steps(case, x1, 1, cfg.num_steps - 1, "fp32")
+    m, a = diff(x_kern, r32, cfg.action_dim)
+    mt, _ = diff(x_kern, x_torch, cfg.action_dim)
+    _report("expert on kernel caches (A)", vs_fp32_max=m, vs_fp32_mean=a, vs_torch_caches_max=mt)
+    assert m <= 1e-3 and a <= 2e-4
+    assert mt <= 1e-2
+
+
+def test_prepare_timing_config_A():
+    """Times one preparation of config A's source (10 layers, 300 x 2048 context); reported, not asserted."""
+    cfg = SY.WORKLOADS["A"]
+    model = SY.SyntheticReki(cfg, SY.make_weights(cfg, 0), device="cuda")
+    ctx = SY.make_inputs(cfg)["ctx"].cuda()
+    prep = SourcePrepare(model)
+    for _ in range(3):
+        prep(ctx, [cfg.S])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        prep(ctx, [cfg.S])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / 20
+    inp = SY.make_inputs(cfg)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(5):
+        model.register_prepare(inp["ctx"], inp["mem_states"])
+    t1.record()
+    torch.cuda.synchronize()
+    _report("prepare timing A", kernel_us=us, torch_register_prepare_us=t0.elapsed_time(t1) * 1e3 / 5)
+
+
+def test_prepare_rejects_more_rows_than_the_handle_stages():
+    from mkx._lib import MkxError
+    model = SY.SyntheticReki(TINY, SY.make_weights(TINY, 0), device="cuda")
+    prep = SourcePrepare(model, max_rows=TINY.SP - 1)
+    with pytest.raises(MkxError):
+        prep(SY.make_inputs(TINY)["ctx"].cuda(), [TINY.S])
+    prep.close()

@@ -1,4 +1,5 @@
-"""The register-memory ring's oracle (CPU) and the C ABI's argument checks for ``mkx_ring_append``.
+"""The register-memory ring's oracle (CPU), and the C ABI's argument checks for ``mkx_ring_append`` and
+``mkx_source_create`` / ``mkx_source_run``.
 
 The oracle is pinned by a row-by-row restatement, by RoPE's composition law, by the memory that
 ``register_prepare`` builds from shifted states, and by the kv_start sequence over frames."""
@@ -126,3 +127,24 @@ def test_ring_append_rejects_bad_arguments_before_touching_the_device(over):
     assert rc == _lib.EINVAL, L.mkx_last_error()
     assert L.mkx_last_error().decode().startswith("mkx_ring_append")
     assert L.mkx_ring_append(None, None) == _lib.EINVAL
+
+
+def test_source_create_rejects_bad_dims_before_touching_the_device():
+    L = _lib.lib()
+    good = dict(L=2, NH=2, HD=64, C=64, max_rows=64, eps=1e-6)
+    for over in (dict(L=0), dict(L=33), dict(HD=32), dict(C=48), dict(C=0), dict(NH=0), dict(max_rows=0),
+                 dict(eps=-1.0), dict(eps=float("nan"))):
+        h = ctypes.c_void_p()
+        d = _lib.MkxSourceDims(**{**good, **over})
+        rc = L.mkx_source_create(ctypes.byref(d), ctypes.c_void_p(0x100000), ctypes.c_void_p(0x200000),
+                                 ctypes.c_void_p(0x300000), None, ctypes.byref(h))
+        assert rc == _lib.EINVAL and not h.value, (over, L.mkx_last_error())
+        assert L.mkx_last_error().decode().startswith("mkx_source_create")
+    h = ctypes.c_void_p()
+    d = _lib.MkxSourceDims(**good)
+    for wk, wv, kn in ((0, 0x200000, 0x300000), (0x100008, 0x200000, 0x300000), (0x100000, 0x200000, 0)):
+        rc = L.mkx_source_create(ctypes.byref(d), ctypes.c_void_p(wk), ctypes.c_void_p(wv), ctypes.c_void_p(kn), None,
+                                 ctypes.byref(h))
+        assert rc == _lib.EINVAL and not h.value
+    assert L.mkx_source_create(None, None, None, None, None, ctypes.byref(h)) == _lib.EINVAL
+    assert L.mkx_source_run(None, None, None) == _lib.EINVAL
