@@ -117,6 +117,38 @@ def prepare_source_bench(cfg, n: int) -> int:
     return 0
 
 
+def modulations_bench(cfg, n: int) -> int:
+    """Times the modulation projection (B x num_steps rows, MODW outputs): algorithmic bytes = the bf16
+    weights (MODW x H x 2) + bias + the rows read and written."""
+    import torch
+    from mkx import synthetic as SY
+    from mkx.modulations import ModulationProjection
+
+    dev = torch.device("cuda:0")
+    W = SY.make_weights(cfg, seed=0)
+    proj = ModulationProjection(W["mod_w"].to(dev), W["mod_b"].float().to(dev))
+    g = torch.Generator(device=dev).manual_seed(5)
+    c = torch.randn(cfg.B, cfg.num_steps, cfg.H, device=dev, generator=g)
+    for _ in range(5):
+        proj(c)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        starts[i].record(stream)
+        proj(c)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends)) * 1e3
+    R = cfg.B * cfg.num_steps
+    nbytes = cfg.modw * cfg.H * 2 + cfg.modw * 4 + R * (cfg.H + cfg.modw) * 4
+    print(json.dumps({"modulations": {"workload": {"rows": R, "H": cfg.H, "MODW": cfg.modw}, "launches": n,
+                                      "us_per_launch_median": round(us, 3), "algorithmic_bytes": nbytes,
+                                      "GB_s": round(nbytes / us / 1e3, 1)}}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,6 +164,8 @@ def main() -> int:
                     help="only time N register-memory ring appends over the workload's memory (L, B, PM, NH; R rows)")
     ap.add_argument("--prepare-source", type=int, default=0, metavar="N",
                     help="only time N cross-attention source preparations of the workload's context")
+    ap.add_argument("--modulations", type=int, default=0, metavar="N",
+                    help="only time N modulation projections of the workload's rows (samples x Euler steps)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the megakernel runs on a single MI355X (batch samples would shard "
@@ -157,6 +191,8 @@ def main() -> int:
         return ring_append_bench(cfg, args.ring_append)
     if args.prepare_source:
         return prepare_source_bench(cfg, args.prepare_source)
+    if args.modulations:
+        return modulations_bench(cfg, args.modulations)
     dev = torch.device("cuda:0")
     W = SY.make_weights(cfg, seed=0)
     model = SY.SyntheticReki(cfg, W, device=dev)

@@ -13,6 +13,8 @@
  *                   src/profile_breakdown.py:97-104) that refills past.register_step['mem_kv'] / cu_kv
  *   mkx_source_create / _run / _destroy <- the cross-attention source K/V of REKI's register_prepare
  *                   (mk_expert.py:22-24, 491-492: past.cross_attn_kv, which the expert call reads)
+ *   mkx_modulations <- the final projection of REKI's _step_modulations (mk_expert.py:529), the mods rows
+ *                   the kernel reads (mk_expert.py:336-340)
  *   mkx_destroy, mkx_last_error, mkx_status_string: lifetime and error reporting the Python object
  *                   had implicitly (the reference only asserts, src/mk_expert.py:444, 464, 480, 488, 496).
  *
@@ -220,6 +222,25 @@ int mkx_source_create(const mkx_source_dims* dims, const void* wk, const void* w
                       mkx_source** out);
 int mkx_source_run(mkx_source* h, const mkx_source_args* args, void* stream);
 int mkx_source_destroy(mkx_source* h);
+
+/* Modulation projection: out[r][n] = sum_k silu(c[r][k]) w[n][k] + bias[n], every AdaRMS scale, shift and
+ * gate of every layer and Euler step of a call in one product (N = MODW = 9 L H + 2 H). Reference: the
+ * mods rows the expert reads (src/mk_expert.py:336-340), made by REKI's _step_modulations
+ * (mk_expert.py:529: mods, dt = model._step_modulations(num_steps, state_cond)), whose last layer this is.
+ * fp32 in and out, bf16 weights; silu(c) is split into bf16 hi + lo MFMA operands. Asynchronous. */
+typedef struct {
+  int32_t R;               /* rows: samples x Euler steps */
+  int32_t K;               /* input width H: 256, 512, 768 or 1024 */
+  int32_t N;               /* output columns, a multiple of 16 */
+  const float* c;          /* [R, c_stride] fp32, 16-byte aligned: the input before the final SiLU */
+  int64_t c_stride;        /* a multiple of 4 */
+  const void* w;           /* [N, K] bf16, 16-byte aligned */
+  const float* bias;       /* [N] fp32, 16-byte aligned */
+  float* out;              /* [R, out_stride] fp32, 16-byte aligned */
+  int64_t out_stride;      /* a multiple of 4 */
+} mkx_modproj_args;
+
+int mkx_modulations(const mkx_modproj_args* args, void* stream);
 
 int64_t mkx_query(const mkx_handle* h, int32_t key);
 int mkx_destroy(mkx_handle* h);

@@ -279,12 +279,18 @@ def step_modulations(num_steps: int, state_cond: torch.Tensor, W: dict, d: Exper
     t_k = 1 - k/N, dt = -1/N. c = silu(temb(t) W1^T + b1) W2^T + b2 + state_cond;
     mods = silu(c) Wmod^T + bmod (fp32). The kernel only sees mods and dt
     (mk_expert.py:336-340, 529)."""
+    c = modulation_input(num_steps, state_cond, W, d)
+    mods = F.silu(c) @ W["mod_w"].float().T + W["mod_b"].float()
+    return mods, -1.0 / num_steps
+
+
+def modulation_input(num_steps: int, state_cond: torch.Tensor, W: dict, d: ExpertDims) -> torch.Tensor:
+    """c [B, N, H] = silu(temb(t) W1^T + b1) W2^T + b2 + state_cond, the input of the modulation
+    projection (``step_modulations``)."""
     t = 1.0 - torch.arange(num_steps, dtype=torch.float64) / num_steps
     e = timestep_embedding(t, d.tdim).to(torch.float32)
     c = F.silu(e @ W["t1_w"].float().T + W["t1_b"].float()) @ W["t2_w"].float().T + W["t2_b"].float()
-    c = c[None, :, :] + state_cond.float()[:, None, :]
-    mods = F.silu(c) @ W["mod_w"].float().T + W["mod_b"].float()
-    return mods, -1.0 / num_steps
+    return c[None, :, :] + state_cond.float()[:, None, :]
 
 
 def rope_cos_sin(pos: torch.Tensor, hd: int, theta: float = 10000.0):

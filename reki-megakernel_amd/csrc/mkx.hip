@@ -12,6 +12,7 @@
 #include "mkx_kernel.h"
 #include "mkx_ring.h"
 #include "mkx_prepare.h"
+#include "mkx_modproj.h"
 
 using namespace mkx;
 
@@ -585,6 +586,29 @@ int mkx_source_run(mkx_source* h, const mkx_source_args* a, void* stream_) {
 
 int mkx_source_destroy(mkx_source* h) {
   free_source(h);
+  return MKX_OK;
+}
+
+int mkx_modulations(const mkx_modproj_args* a, void* stream_) {
+  if (!a) return fail(MKX_EINVAL, "mkx_modulations: args is NULL");
+  if (a->R < 1 || a->N < 16 || (a->N & 15) || a->R > (1 << 20))
+    return fail(MKX_EINVAL, "mkx_modulations: need R >= 1 and N a positive multiple of 16");
+  if (a->K != 256 && a->K != 512 && a->K != 768 && a->K != 1024)
+    return fail(MKX_EUNSUPPORTED, "mkx_modulations: K must be 256, 512, 768 or 1024");
+  if (a->c_stride < a->K || (a->c_stride & 3) || a->out_stride < a->N || (a->out_stride & 3))
+    return fail(MKX_EINVAL, "mkx_modulations: strides must cover a row and be multiples of 4");
+  auto bad16 = [](const void* p) { return p == nullptr || ((uintptr_t)p & 15u) != 0; };
+  if (bad16(a->c) || bad16(a->w) || bad16(a->bias) || bad16(a->out))
+    return fail(MKX_EINVAL, "mkx_modulations: c, w, bias, out: NULL or not 16-byte aligned");
+  hipStream_t stream = (hipStream_t)stream_;
+  const dim3 grid((unsigned)((a->N / 16 + 3) / 4));
+  switch (a->K / 32) {
+    case 8: hipLaunchKernelGGL(modproj_kernel<8>, grid, dim3(MODP_BLOCK), 8 * 64 * 32, stream, *a); break;
+    case 16: hipLaunchKernelGGL(modproj_kernel<16>, grid, dim3(MODP_BLOCK), 16 * 64 * 32, stream, *a); break;
+    case 24: hipLaunchKernelGGL(modproj_kernel<24>, grid, dim3(MODP_BLOCK), 24 * 64 * 32, stream, *a); break;
+    default: hipLaunchKernelGGL(modproj_kernel<32>, grid, dim3(MODP_BLOCK), 32 * 64 * 32, stream, *a); break;
+  }
+  HIPCHK(hipGetLastError());
   return MKX_OK;
 }
 

@@ -14,7 +14,8 @@ ACT_SILU, ACT_GELU_TANH = 0, 1
 Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WEIGHT_BYTES, Q_LDS_BYTES = range(8)
 
 EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
-           "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append", "mkx_source_create", "mkx_source_run", "mkx_source_destroy")
+           "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append", "mkx_source_create", "mkx_source_run", "mkx_source_destroy",
+           "mkx_modulations")
 
 _vp = ctypes.c_void_p
 
@@ -61,6 +62,11 @@ class MkxSourceArgs(ctypes.Structure):
                 ("kca", _vp * MAX_LAYERS), ("vca", _vp * MAX_LAYERS), ("src_stride_b", ctypes.c_int64)]
 
 
+class MkxModprojArgs(ctypes.Structure):
+    _fields_ = [("R", ctypes.c_int32), ("K", ctypes.c_int32), ("N", ctypes.c_int32), ("c", _vp), ("c_stride", ctypes.c_int64),
+                ("w", _vp), ("bias", _vp), ("out", _vp), ("out_stride", ctypes.c_int64)]
+
+
 class MkxError(RuntimeError):
     def __init__(self, status: int, where: str, detail: str):
         super().__init__(f"{where}: mkx status {status} ({detail})")
@@ -94,6 +100,7 @@ def lib() -> ctypes.CDLL:
         L.mkx_source_create.argtypes = [ctypes.POINTER(MkxSourceDims), _vp, _vp, _vp, _vp, ctypes.POINTER(_vp)]
         L.mkx_source_run.argtypes = [_vp, ctypes.POINTER(MkxSourceArgs), _vp]
         L.mkx_source_destroy.argtypes = [_vp]
+        L.mkx_modulations.argtypes = [ctypes.POINTER(MkxModprojArgs), _vp]
         _LIB = L
     return _LIB
 

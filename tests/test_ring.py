@@ -1,5 +1,5 @@
 """The register-memory ring's oracle (CPU), and the C ABI's argument checks for ``mkx_ring_append`` and
-``mkx_source_create`` / ``mkx_source_run``.
+``mkx_source_create`` / ``mkx_source_run`` and ``mkx_modulations``.
 
 The oracle is pinned by a row-by-row restatement, by RoPE's composition law, by the memory that
 ``register_prepare`` builds from shifted states, and by the kv_start sequence over frames."""
@@ -148,3 +148,18 @@ def test_source_create_rejects_bad_dims_before_touching_the_device():
         assert rc == _lib.EINVAL and not h.value
     assert L.mkx_source_create(None, None, None, None, None, ctypes.byref(h)) == _lib.EINVAL
     assert L.mkx_source_run(None, None, None) == _lib.EINVAL
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(R=0), _lib.EINVAL), (dict(N=8), _lib.EINVAL), (dict(N=24), _lib.EINVAL), (dict(K=384), _lib.EUNSUPPORTED),
+    (dict(c_stride=100), _lib.EINVAL), (dict(out_stride=30), _lib.EINVAL), (dict(c=0x100008), _lib.EINVAL),
+    (dict(w=0), _lib.EINVAL), (dict(bias=0x300004), _lib.EINVAL), (dict(out=0), _lib.EINVAL),
+])
+def test_modulations_reject_bad_arguments_before_touching_the_device(over, status):
+    L = _lib.lib()
+    kw = dict(R=10, K=256, N=32, c=0x100000, c_stride=256, w=0x200000, bias=0x300000, out=0x400000, out_stride=32)
+    kw.update(over)
+    rc = L.mkx_modulations(ctypes.byref(_lib.MkxModprojArgs(**kw)), None)
+    assert rc == status, L.mkx_last_error()
+    assert L.mkx_last_error().decode().startswith("mkx_modulations")
+    assert L.mkx_modulations(None, None) == _lib.EINVAL
