@@ -149,6 +149,68 @@ def modulations_bench(cfg, n: int) -> int:
     return 0
 
 
+def expert_call_bench(cfg, n: int, name: str) -> int:
+    """Times one whole expert call as a policy step runs it, on this library's kernels: the modulation
+    MLP (small layers in PyTorch, the MODW-wide projection on mkx_modulations), the cross-attention source
+    caches (mkx_source_run), Euler steps 1..N in one launch (run_all) and the register-memory append
+    (mkx_ring_append); beside it the same call with the modulations and source caches in PyTorch and
+    step 1 as its own launch (the reference's split, src/mk_expert.py:527-533)."""
+    import torch
+    from mkx import ExpertMegakernel, synthetic as SY
+    from mkx.modulations import ModulationProjection
+    from mkx.prepare import SourcePrepare
+
+    dev = torch.device("cuda:0")
+    W = SY.make_weights(cfg, seed=0)
+    model = SY.SyntheticReki(cfg, W, device=dev)
+    inp = SY.make_inputs(cfg)
+    past = model.register_prepare(inp["ctx"], inp["mem_states"])
+    noise, ctx, sc = inp["noise"].to(dev), inp["ctx"].to(dev), inp["state_cond"].to(dev)
+    mk = ExpertMegakernel(model)
+    prep = SourcePrepare(model)
+    proj = ModulationProjection(W["mod_w"].to(dev), W["mod_b"].float().to(dev))
+    ring = model.register_ring(past)
+    dt = torch.full((1,), -1.0 / cfg.num_steps, device=dev)
+    ca_len = [cfg.S] * cfg.B
+
+    def kernels():
+        mods = proj(model.modulation_input(cfg.num_steps, sc))
+        mods = mods[0] if cfg.B == 1 else mods
+        cross = prep(ctx, ca_len)
+        past.cross_attn_kv = [(k[0], v[0]) for k, v in cross] if cfg.B == 1 else cross
+        x, ck, cv = mk.run_all(noise, mods, dt, past, cfg.action_dim)
+        ring.append_frame(ck, cv)
+        ring.update_past(past)
+        return x
+
+    def torch_side():
+        mods, dt_ = model._step_modulations(cfg.num_steps, sc)
+        p2 = model.register_prepare(inp["ctx"], inp["mem_states"])
+        x1, _, _ = model._expert_first_step(noise, p2, None, mods[..., :1, :], dt_, cfg.action_dim)
+        return mk.run(x1, mods, dt_, p2, cfg.action_dim)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return statistics.median(ts)
+
+    ms_k = timed(kernels)
+    ms_t = timed(torch_side)
+    print(json.dumps({"expert_call": {"workload": name, "calls": n,
+                                      "ms_median_kernels": round(ms_k, 3), "ms_median_pytorch_prep": round(ms_t, 3),
+                                      "parts": "modulations + source caches + steps 1-10 + ring append"}}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +228,8 @@ def main() -> int:
                     help="only time N cross-attention source preparations of the workload's context")
     ap.add_argument("--modulations", type=int, default=0, metavar="N",
                     help="only time N modulation projections of the workload's rows (samples x Euler steps)")
+    ap.add_argument("--expert-call", type=int, default=0, metavar="N",
+                    help="only time N whole expert calls (modulations, source caches, steps 1..N, ring append)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the megakernel runs on a single MI355X (batch samples would shard "
@@ -193,6 +257,8 @@ def main() -> int:
         return prepare_source_bench(cfg, args.prepare_source)
     if args.modulations:
         return modulations_bench(cfg, args.modulations)
+    if args.expert_call:
+        return expert_call_bench(cfg, args.expert_call, args.workload)
     dev = torch.device("cuda:0")
     W = SY.make_weights(cfg, seed=0)
     model = SY.SyntheticReki(cfg, W, device=dev)

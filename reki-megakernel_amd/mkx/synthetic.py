@@ -300,6 +300,17 @@ class SyntheticReki:
         c = silu(temb(t) W1^T + b1) W2^T + b2 + state_cond; mods = silu(c) Wmod^T + bmod."""
         cfg = self.cfg
         dev = self.device
+        c = self.modulation_input(num_steps, state_cond)
+        sc = state_cond.reshape(-1, cfg.H)
+        mods = F.silu(c) @ self._mod[0].T + self._mod[1]
+        dt = torch.full((1,), -1.0 / num_steps, device=dev, dtype=torch.float32)
+        return (mods[0] if sc.shape[0] == 1 else mods.contiguous()), dt
+
+    def modulation_input(self, num_steps: int, state_cond: torch.Tensor) -> torch.Tensor:
+        """c [B, N, H] fp32 = silu(temb(t) W1^T + b1) W2^T + b2 + state_cond, the input of the final
+        modulation projection (mods = silu(c) Wmod^T + bmod)."""
+        cfg = self.cfg
+        dev = self.device
         t = 1.0 - torch.arange(num_steps, dtype=torch.float64, device=dev) / num_steps
         half = cfg.tdim // 2
         freqs = torch.exp(-math.log(10000.0) * torch.arange(half, dtype=torch.float64, device=dev) / half)
@@ -307,10 +318,7 @@ class SyntheticReki:
         e = torch.cat([torch.cos(args), torch.sin(args)], -1).float()
         c = F.silu(e @ self._t1[0].T + self._t1[1]) @ self._t2[0].T + self._t2[1]
         sc = state_cond.to(dev).float().reshape(-1, cfg.H)
-        c = c[None] + sc[:, None, :]
-        mods = F.silu(c) @ self._mod[0].T + self._mod[1]
-        dt = torch.full((1,), -1.0 / num_steps, device=dev, dtype=torch.float32)
-        return (mods[0] if sc.shape[0] == 1 else mods.contiguous()), dt
+        return c[None] + sc[:, None, :]
 
     # -- REKI: register_prepare -> past
     def register_prepare(self, ctx: torch.Tensor, mem_states: torch.Tensor, ca_len=None, kv_start=None) -> Past:
