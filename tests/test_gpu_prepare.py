@@ -123,3 +123,53 @@ def test_prepare_rejects_more_rows_than_the_handle_stages():
     with pytest.raises(MkxError):
         prep(SY.make_inputs(TINY)["ctx"].cuda(), [TINY.S])
     prep.close()
+
+
+def test_whole_call_captured_in_one_graph_replays_match_eager():
+    """Modulation projection, source caches and Euler steps 1..N captured as one HIP graph: every replay,
+    with eager work and a synchronisation between replays, equals the eager call bit for bit."""
+    from mkx.modulations import ModulationProjection
+    case = make_case(SY.WORKLOADS["A"])
+    cfg, model, past, W = case["cfg"], case["model"], case["past"], case["W"]
+    mk = ExpertMegakernel(model)
+    prep = SourcePrepare(model)
+    proj = ModulationProjection(W["mod_w"].cuda(), W["mod_b"].float().cuda())
+    sc = case["inp"]["state_cond"].cuda()
+    ctx = case["inp"]["ctx"].cuda()
+    ca_len = torch.tensor([cfg.S], dtype=torch.int32, device="cuda")
+    dt = torch.full((1,), -1.0 / cfg.num_steps, device="cuda")
+    out = {}
+
+    def call():
+        mods = proj(model.modulation_input(cfg.num_steps, sc))[0]
+        past.cross_attn_kv = [(k[0], v[0]) for k, v in prep(ctx, ca_len)]
+        out["x"], out["k"], out["v"] = mk.run_all(case["noise"], mods, dt, past, cfg.action_dim)
+
+    call()
+    mk.check()
+    torch.cuda.synchronize()
+    x_e, k_e = out["x"].clone(), out["k"].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()  # warm-up on a side stream, as capture requires
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    torch.cuda.synchronize()
+    times = []
+    for i in range(3):
+        out["x"].zero_()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        noise = torch.randn(4096, device="cuda").square().sum()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        times.append(e0.elapsed_time(e1))
+        assert torch.equal(out["x"], x_e) and torch.equal(out["k"], k_e), f"replay {i} differs from the eager call"
+    mk.check()
+    _report("whole call graph replays (A)", replays=3, ms=times)
