@@ -44,7 +44,7 @@ typedef enum {
   MKX_EHIP = 3,          /* a HIP runtime call failed; mkx_last_error() names it */
   MKX_ETIMEOUT = 4,      /* a barrier or ready-epoch wait exceeded its spin bound; results are invalid */
   MKX_ENOMEM = 5,
-  MKX_EUNSUPPORTED = 6   /* a shape this build has no kernel instantiation for */
+  MKX_EUNSUPPORTED = 6   /* a shape the library has no kernel instantiation for */
 } mkx_status;
 
 typedef enum { MKX_WEIGHTS_BF16 = 0, MKX_WEIGHTS_FP8_E4M3 = 1 } mkx_weight_dtype;

@@ -1,6 +1,6 @@
 """CPU oracle for the flow-matching action expert's Euler loop.
 
-TEST INFRASTRUCTURE ONLY. This module is the checker for the HIP megakernel: only ``tests/``,
+TEST INFRASTRUCTURE ONLY. This module is the reference result the HIP megakernel is tested against: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` import it. The product path
 (``reki-megakernel_amd/``) never imports, calls or links it, and must fail loudly when its HIP
 library is missing instead of falling back here.
@@ -19,12 +19,12 @@ Modes.
              citations), including the residual stream.
   ``mixed``  rounds where a bf16 MFMA kernel must (GEMM inputs and outputs, attention operands) but keeps
              the residual stream (h0, h2, h3, h_l and the gated branch added to it) in fp32 — the
-             numerics of this build's HIP kernel, used for tight GPU checks.
+             numerics of this library's HIP kernel, used for tight GPU checks.
   ``fp64``   like ``fp32`` but in float64; used by the oracle's own pin tests.
 
 Parts REKI would have supplied (its code is not available offline): the timestep embedding and
 modulation MLP (``step_modulations``), the cache preparation (``register_prepare``), RoPE positions
-and the register-row layout. They are defined here and in ``mkx.synthetic`` by this build, are pinned
+and the register-row layout. They are defined here and in ``mkx.synthetic`` by this library, are pinned
 by closed forms and invariants in tests/test_oracle_pins.py, and are *parity unpinned against REKI*.
 
 Pinning (tests/test_oracle_pins.py): ``rstd``/``adarms`` against ``torch.nn.functional.rms_norm``
@@ -262,7 +262,7 @@ def _cast_tree(t, dtp):
 
 # ---------------------------------------------------------------------------------------------
 # Parts REKI supplies outside the megakernel (step modulations, cache preparation). REKI's code is
-# unavailable offline, so these are this build's own definitions (parity unpinned against REKI);
+# unavailable offline, so these are this library's own definitions (parity unpinned against REKI);
 # mkx.synthetic computes the same on the GPU.
 # ---------------------------------------------------------------------------------------------
 

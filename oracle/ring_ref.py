@@ -1,14 +1,14 @@
 """CPU oracle for the register-memory ring append (the step after an expert call).
 
-TEST INFRASTRUCTURE ONLY: only ``tests/`` imports it, as the checker of ``mkx_ring_append``; the product
-path never imports, calls or links it.
+TEST INFRASTRUCTURE ONLY: only ``tests/`` imports it, for the expected results of ``mkx_ring_append``;
+the product path never imports, calls or links it.
 
 What it restates. The expert reads its self-attention memory from ``past.register_step['mem_kv']``, per
 layer K and V of PM rows, valid from ``kv_start = cu_kv[0]`` (src/mk_expert.py:489-490, :321). After each
 call REKI's register cache appends the call's register rows to that memory (``append_frame``, timed at
 src/profile_breakdown.py:97-104; "32 register tokens per frame are cached over 3 frames as memory",
 README.md:27). The cache itself is Kyutai's code, absent from the reference, so the rule below is this
-build's, with memory K normed and rotated at its row index (as ``register_prepare`` in ``mkx.synthetic``
+library's, with memory K normed and rotated at its row index (as ``register_prepare`` in ``mkx.synthetic``
 prepares it):
 
     out row j = in row j + R               for kv_start' <= j < PM - R  (K turned by the ``shift`` angles)

@@ -362,7 +362,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   const int Mqp = ceil16(Mq);  // each sample's rows start on a 16-row tile
   const int NR = a->B * Mqp;
   const int NRP = ceil16(NR);
-  if (NRP > MAX_ROWS_PADDED) return fail(MKX_EUNSUPPORTED, "B * (T_act + R_reg) too large for this build");
+  if (NRP > MAX_ROWS_PADDED) return fail(MKX_EUNSUPPORTED, "B * (T_act + R_reg) too large for this library");
   if ((long long)a->B * (H / 64) * (Mqp / 16) > FLAG_MAX) return fail(MKX_EUNSUPPORTED, "too many attention tasks for the ready-epoch table");
   {
     // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes)

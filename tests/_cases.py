@@ -1,5 +1,5 @@
 """Case builder shared by the parity tests: a synthetic expert, its call inputs, and the same inputs in
-the CPU oracle's format. The oracle is only the checker here."""
+the CPU oracle's format. The oracle only supplies the expected results here."""
 from __future__ import annotations
 
 import torch
