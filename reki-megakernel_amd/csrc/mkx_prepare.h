@@ -11,7 +11,8 @@
 // lane. Both operands are read in fragment order, one 1 KB contiguous block per wave and load: the
 // weights are packed so once at creation and the context at each call (pack_rows_kernel). Read in place,
 // the rows of a fragment sit C * 2 bytes apart and the same kernel ran 2.6x slower (221 us against 84 us
-// for 10 layers of a 300 x 2048 context).
+// for 10 layers of a 300 x 2048 context). Chunks of 2 k-steps keep it at 80 VGPRs, so a whole grid of that
+// size is resident at once (75 us; chunks of 4: 132 VGPRs, 83 us).
 #pragma once
 
 #include "mkx.h"
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams
   // k in chunks of KU steps of 32, two chunks in flight: the loads of chunk c + 1 are issued before the
   // MFMAs of chunk c. Steps past C load the last valid step (in bounds) and multiply a zeroed context
   // fragment, so every wave runs the same straight-line code.
-  constexpr int KU = 4;
+  constexpr int KU = 2;
   u32x4 xs[2][KU], ws[2][KU][4];
   auto load = [&](int buf, int k0) {
 #pragma unroll
