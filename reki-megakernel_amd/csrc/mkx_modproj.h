@@ -24,6 +24,7 @@ constexpr int MODP_MAX_KT = 32;  // H <= 1024
 template <int KT>
 __device__ __forceinline__ void modproj_stage(const mkx_modproj_args& a, int r0, char* lds) {
   constexpr int PIECES = KT * 64;
+#pragma unroll 1
   for (int p = threadIdx.x; p < PIECES; p += MODP_BLOCK) {
     const int t = p >> 6, ln = p & 63;
     const int r = min(r0 + (ln & 15), a.R - 1);  // rows past R stage a valid row, never stored
