@@ -277,6 +277,22 @@ def test_packed_fp8_file_drives_the_kernel(tmp_path):
     assert m32 <= TIGHT_MAX and a32 <= TIGHT_MEAN, (m32, a32)
 
 
+def test_packed_fp8_file_of_the_wide_expert_D(tmp_path):
+    """The wide fp8 expert (L16 H1024) written to a packed file and read back: a handle from the file gives
+    the same result, bit for bit, as one from the model."""
+    case = make_case(SY.WORKLOADS["D"])
+    cfg = case["cfg"]
+    path = str(tmp_path / "expert_D.safetensors")
+    save_packed(pack_expert(case["model"]), path)
+    mk_file = ExpertMegakernel.from_packed(load_packed(path, "cuda"))
+    mk_model, x1, x_model = _steps_2_to_n(case)
+    x_file = mk_file.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    mk_file.check()
+    torch.cuda.synchronize()
+    _report("packed fp8 file (D)", equal=bool(torch.equal(x_file, x_model)), weight_bytes=mk_file.weight_bytes)
+    assert mk_file.fp8 and torch.equal(x_file, x_model)
+
+
 def test_invalid_arguments_raise():
     case = make_case(TINY)
     cfg = case["cfg"]
