@@ -56,7 +56,8 @@ class RegisterRing:
         ks = torch.as_tensor(kv_start, dtype=torch.int32).reshape(-1)
         if ks.numel() != B:
             raise ValueError("kv_start needs one entry per sample")
-        self._ks = [ks.to(dev).contiguous(), torch.empty(B, dtype=torch.int32, device=dev)]
+        # a copy: the two kv_start buffers alternate as append outputs, so the caller's tensor must not be one
+        self._ks = [ks.to(dev).clone(), torch.empty(B, dtype=torch.int32, device=dev)]
         self._cur = 0
         self._shift = None if kept_delta is None else rope_delta(kept_delta, HD, theta, dev)
         self._new = None if new_delta is None else rope_delta(new_delta, HD, theta, dev)

@@ -173,3 +173,68 @@ def test_whole_call_captured_in_one_graph_replays_match_eager():
         assert torch.equal(out["x"], x_e) and torch.equal(out["k"], k_e), f"replay {i} differs from the eager call"
     mk.check()
     _report("whole call graph replays (A)", replays=3, ms=times)
+
+
+def test_frames_with_ring_append_as_two_graphs_match_eager():
+    """Four calls (frames) of modulations + source caches + steps 1..N + register append, replayed as two
+    captured graphs, one per buffer parity of the ring (G0 reads set 0 and appends into set 1, G1 the
+    reverse): every frame's result equals the eager sequence's, bit for bit, and kv_start evolves on the
+    device (from an empty memory: kv_start = PM, then PM - R, ... 0)."""
+    from mkx.modulations import ModulationProjection
+    from mkx.ring import RegisterRing
+    case = make_case(replace(SY.WORKLOADS["A"], kv_start=SY.WORKLOADS["A"].PM))
+    cfg, model, past, W = case["cfg"], case["model"], case["past"], case["W"]
+    mk = ExpertMegakernel(model)
+    prep = SourcePrepare(model)
+    proj = ModulationProjection(W["mod_w"].cuda(), W["mod_b"].float().cuda())
+    sc = case["inp"]["state_cond"].cuda()
+    ctx = case["inp"]["ctx"].cuda()
+    ca_len = torch.tensor([cfg.S], dtype=torch.int32, device="cuda")
+    dt = torch.full((1,), -1.0 / cfg.num_steps, device="cuda")
+    mem0 = [(k.clone(), v.clone()) for k, v in past.register_step["mem_kv"]]
+    ks0 = past.register_step["kv_start"].clone()
+    R, T = cfg.R_reg, cfg.T_act
+    out = {}
+
+    def call():
+        mods = proj(model.modulation_input(cfg.num_steps, sc))[0]
+        past.cross_attn_kv = [(k[0], v[0]) for k, v in prep(ctx, ca_len)]
+        out["x"], out["k"], out["v"] = mk.run_all(case["noise"], mods, dt, past, cfg.action_dim)
+
+    ring_e = RegisterRing(mem0, ks0, R, kept_delta=-R, new_delta=-(T + R))
+    ring_e.update_past(past)
+    xs, kss = [], []
+    for _ in range(4):
+        call()
+        xs.append(out["x"].clone())
+        ring_e.append_frame(out["k"], out["v"])
+        ring_e.update_past(past)
+        kss.append(int(ring_e.kv_start[0]))
+    mk.check()
+    torch.cuda.synchronize()
+    assert not torch.equal(xs[0], xs[1])  # the memory changes between frames
+
+    ring_g = RegisterRing(mem0, ks0, R, kept_delta=-R, new_delta=-(T + R))
+    ring_g.update_past(past)
+    call()  # warm-up (no append: the ring's state is untouched)
+    torch.cuda.synchronize()
+    graphs, x_of = [], []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            call()
+            ring_g.append_frame(out["k"], out["v"])
+        ring_g.update_past(past)  # the next graph reads the other buffer set
+        graphs.append(g)
+        x_of.append(out["x"])
+    torch.cuda.synchronize()
+    for f in range(4):
+        graphs[f % 2].replay()
+        noise = torch.randn(4096, device="cuda").square().sum()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        assert torch.equal(x_of[f % 2], xs[f]), f"frame {f} differs from the eager sequence"
+        assert int(ring_g._ks[(f + 1) % 2][0]) == kss[f]
+    mk.check()
+    assert kss == [max(cfg.PM - (f + 1) * R, 0) for f in range(4)]
+    _report("frames as two graphs (A)", frames=4, kv_start=kss)
