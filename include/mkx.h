@@ -238,6 +238,8 @@ typedef struct {
   const float* bias;       /* [N] fp32, 16-byte aligned */
   float* out;              /* [R, out_stride] fp32, 16-byte aligned */
   int64_t out_stride;      /* a multiple of 4 */
+  int32_t w_fragment_order; /* 0: w row-major [N, K]; 1: w pre-packed as [N / 16][K / 32][64][8] with
+                               element (g, t, l, e) = W[16 g + l % 16][32 t + 8 (l / 16) + e] */
 } mkx_modproj_args;
 
 int mkx_modulations(const mkx_modproj_args* args, void* stream);

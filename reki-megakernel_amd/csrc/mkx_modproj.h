@@ -55,10 +55,15 @@ __global__ __launch_bounds__(MODP_BLOCK) void modproj_kernel(mkx_modproj_args a)
   const bool active = n0 < a.N;  // inactive waves still stage rows and meet the barriers
   const int K = a.K;
   // weight fragments: row n0 + (lane & 15), k = 32 t + 8 (lane >> 4), all issued before the first tile
-  const bf16_t* wp = (const bf16_t*)a.w + (int64_t)(active ? n0 + (lane & 15) : 0) * K + 8 * (lane >> 4);
+  // (fragment order: one 1 KB contiguous block per load and wave; row-major: 16 rows x 64 B per load)
+  const int g = active ? n0 / 16 : 0;
+  const bool fo = a.w_fragment_order != 0;
+  const bf16_t* wp = (const bf16_t*)a.w + (fo ? ((int64_t)g * KT * 64 + lane) * 8
+                                              : (int64_t)(g * 16 + (lane & 15)) * K + 8 * (lane >> 4));
+  const int wstep = fo ? 64 * 8 : 32;
   bf16x8 wf[KT];
 #pragma unroll
-  for (int t = 0; t < KT; ++t) wf[t] = __builtin_bit_cast(bf16x8, ld16(wp + 32 * t));
+  for (int t = 0; t < KT; ++t) wf[t] = __builtin_bit_cast(bf16x8, ld16(wp + (int64_t)t * wstep));
   const int nout = active ? n0 + 4 * (lane >> 4) : 0;
   const f32x4 bias = *reinterpret_cast<const f32x4*>(a.bias + nout);
   for (int r0 = 0; r0 < a.R; r0 += 16) {

@@ -64,7 +64,7 @@ class MkxSourceArgs(ctypes.Structure):
 
 class MkxModprojArgs(ctypes.Structure):
     _fields_ = [("R", ctypes.c_int32), ("K", ctypes.c_int32), ("N", ctypes.c_int32), ("c", _vp), ("c_stride", ctypes.c_int64),
-                ("w", _vp), ("bias", _vp), ("out", _vp), ("out_stride", ctypes.c_int64)]
+                ("w", _vp), ("bias", _vp), ("out", _vp), ("out_stride", ctypes.c_int64), ("w_fragment_order", ctypes.c_int32)]
 
 
 class MkxError(RuntimeError):

@@ -3,7 +3,8 @@
 AdaRMS scale, shift and gate of every layer and Euler step of a call — the rows the expert kernel reads
 (src/mk_expert.py:336-340).
 
-``ModulationProjection(weight, bias)`` keeps W as bf16 and b as fp32 on the GPU; ``proj(c)`` runs
+``ModulationProjection(weight, bias)`` keeps W as bf16 (repacked once into MFMA fragment order, so every
+weight load of the kernel is one contiguous 1 KB block per wave) and b as fp32 on the GPU; ``proj(c)`` runs
 ``mkx_modulations`` (one launch, each weight byte read once) on fp32 c [..., H] and returns fp32
 [..., MODW]. Nothing here runs without libmkx.so.
 """
@@ -17,12 +18,18 @@ from ._lib import MkxModprojArgs, check, lib
 
 
 class ModulationProjection:
-    def __init__(self, weight: torch.Tensor, bias: torch.Tensor):
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor, fragment_order: bool = True):
         if weight.dim() != 2 or bias.shape != (weight.shape[0],):
             raise ValueError("weight must be [N, K] and bias [N]")
-        self.w = weight.detach().to(torch.bfloat16).contiguous()
+        w = weight.detach().to(torch.bfloat16).contiguous()
+        self.N, self.K = w.shape
+        if self.N % 16 or self.K % 32:
+            raise ValueError("N must be a multiple of 16 and K of 32")
+        self.fragment_order = fragment_order
+        # fragment order [N/16][K/32][64 lanes][8]: lane l of k-step t holds W[16 g + l % 16][32 t + 8 (l / 16) ..]
+        self.w = (w.view(self.N // 16, 16, self.K // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous()
+                  if fragment_order else w)
         self.b = bias.detach().float().contiguous()
-        self.N, self.K = self.w.shape
 
     def __call__(self, c: torch.Tensor) -> torch.Tensor:
         if c.shape[-1] != self.K:
@@ -31,7 +38,8 @@ class ModulationProjection:
         x = c.float().reshape(-1, self.K).contiguous()
         out = torch.empty(x.shape[0], self.N, dtype=torch.float32, device=x.device)
         a = MkxModprojArgs(R=x.shape[0], K=self.K, N=self.N, c=x.data_ptr(), c_stride=self.K, w=self.w.data_ptr(),
-                           bias=self.b.data_ptr(), out=out.data_ptr(), out_stride=self.N)
+                           bias=self.b.data_ptr(), out=out.data_ptr(), out_stride=self.N,
+                           w_fragment_order=int(self.fragment_order))
         check(lib().mkx_modulations(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
               "mkx_modulations")
         self._keep = x  # the input outlives the asynchronous launch

@@ -28,7 +28,9 @@ def _check(name, cfg, n_steps=10):
     ref, _ = ER.step_modulations(n_steps, sc, W, d)
     proj = ModulationProjection(W["mod_w"].cuda(), W["mod_b"].float().cuda())
     out = proj(c.cuda())
+    out_rm = ModulationProjection(W["mod_w"].cuda(), W["mod_b"].float().cuda(), fragment_order=False)(c.cuda())
     torch.cuda.synchronize()
+    assert torch.equal(out, out_rm)  # both weight layouts give the same bits
     dd = (out.cpu() - ref).abs()
     _report(name, max=float(dd.max()), mean=float(dd.mean()), max_abs_ref=float(ref.abs().max()))
     assert out.shape == ref.shape
@@ -87,6 +89,7 @@ def test_modulations_timing_config_A():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / n
 
-    _report("modulations timing A", kernel_us=t(lambda: proj(c)),
+    proj_rm = ModulationProjection(W["mod_w"].cuda(), W["mod_b"].float().cuda(), fragment_order=False)
+    _report("modulations timing A", kernel_us=t(lambda: proj(c)), kernel_row_major_us=t(lambda: proj_rm(c)),
             torch_fp32_us=t(lambda: torch.nn.functional.silu(c) @ wf.T + bf),
             weight_bytes=int(proj.w.numel() * 2))

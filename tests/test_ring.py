@@ -157,7 +157,8 @@ def test_source_create_rejects_bad_dims_before_touching_the_device():
 ])
 def test_modulations_reject_bad_arguments_before_touching_the_device(over, status):
     L = _lib.lib()
-    kw = dict(R=10, K=256, N=32, c=0x100000, c_stride=256, w=0x200000, bias=0x300000, out=0x400000, out_stride=32)
+    kw = dict(R=10, K=256, N=32, c=0x100000, c_stride=256, w=0x200000, bias=0x300000, out=0x400000, out_stride=32,
+              w_fragment_order=1)
     kw.update(over)
     rc = L.mkx_modulations(ctypes.byref(_lib.MkxModprojArgs(**kw)), None)
     assert rc == status, L.mkx_last_error()
