@@ -488,9 +488,9 @@ struct EpiPre {
   f32x4 sa, sb;  // fp8 weights: output-channel scales of the item's columns (V tasks: one per 16-column tile)
 };
 
-// The constant part (RoPE tables, q/k norm weights, fp8 output-channel scales): loaded for a task's first
-// pass before its ready-epoch wait, the operands being inputs of the call, so that their latency (they are
-// often no longer in L2 when the stage comes round) overlaps the wait instead of following it.
+// The constant part (RoPE tables, q/k norm weights, fp8 output-channel scales), loaded in each pass right
+// after the operand loads: issued before the ready-epoch poll, these loads would delay the poll, since loads
+// return in issue order per CU (3.33 to 3.28 ms for workload A).
 template <class S>
 __device__ __forceinline__ EpiPre epi_const(Ctx<S>& c, const Desc& d, int kind, int j, int tile, int row, int L) {
   CP& p = c.p;
@@ -591,7 +591,7 @@ __device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][2][2], const bf16
 // partial tiles written to the cross-wave reduction buffer.
 template <class S, int NRT>
 __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int kb0, bool vtask, int qkind, int qj,
-                                          int tile, EpiPre& epre, bool have_const) {
+                                          int tile, EpiPre& epre) {
   constexpr int KPW = S::KPW, RB = S::RBMAX;
   CP& p = c.p;
   const int RT = c.RT, NRP = p.NRP;
@@ -623,7 +623,7 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
     for (int i = 0; i < KPW; ++i) sh_h[i] = sh_l[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
   const int erow = epi_row(rt0, NRT, c.tid), eL = c.tid & 63;
-  if (!have_const) epre = epi_const(c, d, qkind, qj, tile, erow, eL);
+  epre = epi_const(c, d, qkind, qj, tile, erow, eL);
   if (d.kind == K_RES) epre.c0 = as_f4(ld16((const char*)d.res + fpiece(erow, tile * 16 + 4 * (eL >> 4), c.RT)));
   // The staged weights and modulation slices (the prefetch's LDS DMAs, issued before every load above) have
   // landed once no more than the activation loads are outstanding; the activations are waited for where the
@@ -758,17 +758,17 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     const int kb0 = d.kind == K_SPLIT ? split * S::NKB : 0;
     const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
     const int rt_hi = d.kind == K_SPLIT ? RT : (split + 1) * RT / d.rgs;
-    // the first pass's constant epilogue operands, while the wait runs
-    EpiPre epre = epi_const(c, d, qkind, qj, tile, epi_row(rt_lo, min(RB, rt_hi - rt_lo), c.tid), c.tid & 63);
+    // The epilogue's constant operands are loaded in each pass after its operand loads, not before the
+    // wait: loads return in issue order per CU, so a load issued before the ready-epoch poll delays the poll.
+    EpiPre epre;
     MKX_TR(c, 14);
     gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
     MKX_TR(c, 0);
     for (int rt0 = rt_lo; rt0 < rt_hi; rt0 += RB) {
       const int nrt = min(RB, rt_hi - rt0);
-      const bool have_const = rt0 == rt_lo;
-      if (nrt == 1) gemm_pass<S, 1>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre, have_const);
-      else if (nrt == 2 || RB == 2) gemm_pass<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre, have_const);
-      else gemm_pass<S, RB>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre, have_const);
+      if (nrt == 1) gemm_pass<S, 1>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+      else if (nrt == 2 || RB == 2) gemm_pass<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+      else gemm_pass<S, RB>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
       __syncthreads();
       MKX_TR(c, 2);
       // epilogue: one (row tile, lane) item per thread: row (rt0 + rt) * 16 + L % 16, columns tile*16 + 4 (L / 16) + 0..3
