@@ -140,11 +140,24 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* weights, void* stream, m
 /* ExpertMegakernel.run (src/mk_expert.py:483-515): one persistent launch on `stream` (a hipStream_t;
  * NULL = default stream). Inputs are borrowed for the duration of the call. A handle's scratch is shared
  * by its calls: use one handle per stream (the reference is not re-entrant either). Asynchronous; call
- * mkx_check after synchronising to learn whether a barrier or ready-epoch wait timed out. */
+ * mkx_check after synchronising to learn whether a barrier or ready-epoch wait timed out.
+ * Scratch grows on the first call at a larger shape (n_steps, B * (T_act + R_reg), PM, SP), which
+ * allocates and synchronises: under stream capture such a call returns MKX_EINVAL, and once any launch of
+ * the handle has been captured a growing call returns MKX_EUNSUPPORTED (the graph holds the current
+ * scratch). Warm up eagerly at the largest shape before capturing, or use a second handle.
+ * A launch whose waits gave up writes NaN into x_out, and so does every later launch on the handle (doing no
+ * other work) until mkx_check resets the synchronisation state. */
 int mkx_run(mkx_handle* h, const mkx_step_args* args, void* stream);
 
-/* Reads the device error flag of the last launch (synchronises `stream`): MKX_OK or MKX_ETIMEOUT. */
+/* Reads the device error flag of the last launch (synchronises `stream`): MKX_OK or MKX_ETIMEOUT (and then
+ * resets the handle's synchronisation state, so the next launch runs normally). */
 int mkx_check(mkx_handle* h, void* stream);
+
+/* Spin bound of every grid-barrier and ready-epoch wait of later launches, in polls (0 = the default,
+ * 2^20 polls, about 0.5 s). A wait that exceeds it sets the error flag and every later wait of the launch
+ * returns at once, so a launch that cannot complete still drains. No counterpart in the reference, whose
+ * grid barrier spins without bound (README.md:262-263); tests use a tiny bound to exercise the path. */
+int mkx_set_spin_limit(mkx_handle* h, uint32_t polls);
 
 /* ExpertMegakernel.barriers (src/mk_expert.py:517-518): stage boundaries one launch of n_steps passes
  * (1 + n_steps (7 L + 1); the first is a grid barrier, the others per-task ready epochs). */

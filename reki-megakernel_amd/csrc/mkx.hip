@@ -31,7 +31,7 @@ int fail(int code, const std::string& msg) {
     if (e_ != hipSuccess) return fail(MKX_EHIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
   } while (0)
 
-constexpr unsigned SPIN_LIMIT = 1u << 20;
+constexpr unsigned SPIN_LIMIT = 1u << 20;  // default spin bound of a wait (polls), about 0.5 s
 constexpr int MAX_ROWS_PADDED = 512;
 
 // W [L][N][K] row-major -> chunks (l, t, kb): dst[l*dls + (t'*tstride + toff + kb)*512 + lane*8 + j] =
@@ -138,6 +138,8 @@ struct mkx_handle {
   int prof_len = 0;
   int profile = 0;
   int plain_launch = 0;  // MKX_PLAIN_LAUNCH=1 at creation: hipLaunchKernel instead of the cooperative launch
+  unsigned spin_limit = SPIN_LIMIT;
+  int captured = 0;      // a launch of this handle was captured into a graph: its scratch pointers are frozen
   unsigned long long gen_before = 0;
   long long last_nbar = 0;
   long long weight_bytes = 0;
@@ -319,6 +321,12 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   return MKX_OK;
 }
 
+int mkx_set_spin_limit(mkx_handle* h, uint32_t polls) {
+  if (!h) return fail(MKX_EINVAL, "null handle");
+  h->spin_limit = polls ? polls : SPIN_LIMIT;
+  return MKX_OK;
+}
+
 int64_t mkx_barriers(const mkx_handle* h, int32_t n_steps) {
   if (!h || n_steps < 0) return -1;
   return 1 + (int64_t)n_steps * (mkx::STAGES_PER_LAYER * h->d.L + 1);
@@ -389,7 +397,20 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   // V^T copies (bf16) and the split AdaRMS shift operands (B * H * 4 bytes per step, layer and AdaRMS)
   const size_t vt_bytes = (size_t)L * a->B * (H / 64) * (PMP + SPP) * 128;
   const size_t need_v = vt_bytes + (size_t)a->n_steps * L * 3 * a->B * H * 4;
-  if (need_f > h->frames_cap || need_s > h->steps_cap || need_v > h->vts_cap) {
+  // Capture status first: growing the scratch synchronises the stream and reallocates, which a capturing
+  // stream cannot do, and a graph captured earlier keeps the old scratch pointers in its kernel arguments.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIPCHK(hipStreamIsCapturing(stream, &cs));
+  const bool capturing = cs == hipStreamCaptureStatusActive;
+  const bool grow = need_f > h->frames_cap || need_s > h->steps_cap || need_v > h->vts_cap;
+  if (grow && capturing)
+    return fail(MKX_EINVAL, "mkx_run under stream capture needs more scratch than the handle holds: run once eagerly "
+                            "at this shape (or a larger one) before capturing");
+  if (grow && h->captured)
+    return fail(MKX_EUNSUPPORTED, "mkx_run: this shape needs more scratch, but a launch of this handle was captured and "
+                                  "its graph holds the current scratch; warm up at the largest shape before capturing, or "
+                                  "use a second handle");
+  if (grow) {
     HIPCHK(hipStreamSynchronize(stream));
     if (need_f > h->frames_cap) {
       if (h->frames) HIPCHK(hipFree(h->frames));
@@ -450,11 +471,10 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   for (int x = 0; x < MAX_XCD; ++x) p.nx[x] = h->nx[x];
   p.xmask = h->xmask;
   p.prof = h->prof; p.profile = h->profile;
-  p.spin_limit = SPIN_LIMIT;
+  p.spin_limit = h->spin_limit;
   void* args[] = {&p};
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  HIPCHK(hipStreamIsCapturing(stream, &cs));
-  if (cs == hipStreamCaptureStatusActive || h->plain_launch) {
+  if (capturing) h->captured = 1;
+  if (capturing || h->plain_launch) {
     // co-residency was established at creation (one workgroup per CU fits); capture a plain launch
     HIPCHK(hipLaunchKernel(h->kernel, dim3(h->G), dim3(NTHREADS), args, 0, stream));
   } else {

@@ -1716,6 +1716,8 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       const int a_lo = inproj ? 0 : a_out * TAIL_AC, a_hi = inproj ? adim : min(a_lo + TAIL_AC, p.A);
       const float bo = p.bout[min(c.lane, p.A - 1)];
       float* xn = d.last ? p.x_out : c.xstep(d.s + 1);
+      // a launch whose synchronisation gave up (a wait exceeded its spin bound) returns NaN, not a result
+      const bool poisoned = d.last && __hip_atomic_load(&p.bar->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
       for (int r0 = c.wave; r0 < nrows; r0 += NWAVES * R) {
         f32x4 x[R][NP];
         float xc[R];
@@ -1781,7 +1783,8 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
               } else {
                 // x after the step: x + dt v on the real dims, dt v on the padded ones
                 const float xa = c.lane < adim ? xc[k] : 0.f;
-                st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + c.lane) * 4), __float_as_uint(xa + c.dt * (sel[k] + bo)));
+                st_sc1_b32(xn, (uint32_t)(((long long)ri * p.A + c.lane) * 4),
+                           poisoned ? 0x7fc00000u : __float_as_uint(xa + c.dt * (sel[k] + bo)));
               }
             }
           }
@@ -1916,6 +1919,13 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   if (c.tid < p.B) {
     s_ks[c.tid] = min(max(p.kv_start[c.tid], 0), p.PM);
     s_ks[MAX_BATCH + c.tid] = min(max(p.ca_len[c.tid], 0), p.SP);
+  }
+  // A launch after one that timed out (error flag still set: the caller has not run mkx_check, which resets
+  // the synchronisation state) does no work and returns NaN, so the failure cannot pass unnoticed.
+  if (__hip_atomic_load(&p.bar->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+    if (c.wg == 0)
+      for (int i = c.tid; i < p.B * p.T * p.A; i += NTHREADS) p.x_out[i] = __uint_as_float(0x7fc00000u);
+    return;
   }
   BarCtx bc;
   bc.bs = p.bar;

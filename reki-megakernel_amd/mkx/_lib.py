@@ -15,7 +15,7 @@ Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WE
 
 EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
            "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append", "mkx_source_create", "mkx_source_run", "mkx_source_destroy",
-           "mkx_modulations")
+           "mkx_modulations", "mkx_set_spin_limit")
 
 _vp = ctypes.c_void_p
 
@@ -101,8 +101,18 @@ def lib() -> ctypes.CDLL:
         L.mkx_source_run.argtypes = [_vp, ctypes.POINTER(MkxSourceArgs), _vp]
         L.mkx_source_destroy.argtypes = [_vp]
         L.mkx_modulations.argtypes = [ctypes.POINTER(MkxModprojArgs), _vp]
+        L.mkx_set_spin_limit.argtypes = [_vp, ctypes.c_uint32]
         _LIB = L
     return _LIB
+
+
+def require_device(device, **tensors) -> None:
+    """Raise ValueError unless every given tensor (None skipped) sits on ``device``, the GPU the handle was
+    made for: the library takes raw device pointers, so a host or other-device tensor would be read or
+    written by the GPU as if it were this device's memory."""
+    for name, t in tensors.items():
+        if t is not None and t.device != device:
+            raise ValueError(f"{name} is on {t.device}, the handle's tensors must be on {device}")
 
 
 def check(status: int, where: str) -> None:

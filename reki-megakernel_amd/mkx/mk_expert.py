@@ -15,7 +15,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import MkxDims, MkxStepArgs, MkxWeights, check, lib
+from ._lib import MkxDims, MkxStepArgs, MkxWeights, check, lib, require_device
 from .pack import LINEARS, PackedExpert, pack_expert, validate
 
 
@@ -97,7 +97,28 @@ class ExpertMegakernel:
             pass
 
     # ------------------------------------------------------------------------------------------
+    def _check_devices(self, x_t, mods, dt, past) -> None:
+        """Every tensor the launch reads must sit on the handle's GPU (checked before anything is marshalled)."""
+        step = past.register_step
+        tensors = {"x_t": x_t, "mods": mods, "dt": dt if torch.is_tensor(dt) else None,
+                   "register_tokens": self.register_tokens}
+        for key in ("kv_start", "ca_len", "cu_kv", "cu_src"):
+            if torch.is_tensor(step.get(key)):
+                tensors[key] = step[key]
+        for key in ("sa_pe", "ca_pe", "sa_pe_first", "ca_pe_first"):
+            for i, t in enumerate(step.get(key, ())):
+                tensors[f"{key}[{i}]"] = t
+        for name, pairs in (("mem_kv", step["mem_kv"]), ("cross_attn_kv", past.cross_attn_kv)):
+            for l, (k, v) in enumerate(pairs):
+                tensors[f"{name}[{l}].k"], tensors[f"{name}[{l}].v"] = k, v
+        require_device(self.device, **tensors)
+
+    def set_spin_limit(self, polls: int | None) -> None:
+        """Spin bound (polls) of every wait of later launches; None restores the default (about 0.5 s)."""
+        check(lib().mkx_set_spin_limit(self._h, 0 if polls is None else int(polls)), "mkx_set_spin_limit")
+
     def _args(self, x_t, mods, dt, past, action_dim, n_steps, mod_row0, first, cur_k=None, cur_v=None):
+        self._check_devices(x_t, mods, dt, past)
         step = past.register_step
         if x_t.dim() != 3 or x_t.shape[2] != self.A:
             raise ValueError(f"x_t must be [B, T, {self.A}], got {tuple(x_t.shape)}")
@@ -148,15 +169,23 @@ class ExpertMegakernel:
         PM, SP = mk[0].shape[1], kc[0].shape[1]
         if any(t.shape != mk[0].shape for t in mk + mv) or any(t.shape != kc[0].shape for t in kc + vc):
             raise ValueError("per-layer caches must share one shape")
-        if "kv_start" in step and "ca_len" in step:
-            kvs, cal = step["kv_start"].to(torch.int32).contiguous(), step["ca_len"].to(torch.int32).contiguous()
-            kv_ptr, ca_ptr = kvs.data_ptr(), cal.data_ptr()
-        else:  # batch 1, reference layout: kv_start = cu_kv[0], S = cu_src[1] (src/mk_expert.py:321-322)
-            if B != 1:
-                raise ValueError("batched caches need register_step['kv_start'] and ['ca_len']")
+        # kv_start[B] / ca_len[B] when the past holds them (the register ring keeps kv_start in device buffers
+        # that its append updates, so a captured launch reads the current value); otherwise, batch 1 in the
+        # reference layout, kv_start = cu_kv[0] and S = cu_src[1] (src/mk_expert.py:321-322)
+        if B != 1 and not ("kv_start" in step and "ca_len" in step):
+            raise ValueError("batched caches need register_step['kv_start'] and ['ca_len']")
+        if "kv_start" in step:
+            kvs = step["kv_start"].to(torch.int32).contiguous()
+            kv_ptr = kvs.data_ptr()
+        else:
             kvs = step["cu_kv"].to(torch.int32).contiguous()
+            kv_ptr = kvs.data_ptr()
+        if "ca_len" in step:
+            cal = step["ca_len"].to(torch.int32).contiguous()
+            ca_ptr = cal.data_ptr()
+        else:
             cal = step["cu_src"].to(torch.int32).contiguous()
-            kv_ptr, ca_ptr = kvs.data_ptr(), cal.data_ptr() + 4
+            ca_ptr = cal.data_ptr() + 4
         x_out = torch.empty_like(x)
         dtt = dt.float().reshape(-1)[:1].contiguous() if torch.is_tensor(dt) else torch.full((1,), float(dt), device=x.device)
         a = MkxStepArgs()

@@ -14,13 +14,15 @@ import ctypes
 
 import torch
 
-from ._lib import MkxModprojArgs, check, lib
+from ._lib import MkxModprojArgs, check, lib, require_device
 
 
 class ModulationProjection:
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor, fragment_order: bool = True):
         if weight.dim() != 2 or bias.shape != (weight.shape[0],):
             raise ValueError("weight must be [N, K] and bias [N]")
+        if weight.device.type != "cuda" or bias.device != weight.device:
+            raise ValueError("weight and bias must sit on one GPU")
         w = weight.detach().to(torch.bfloat16).contiguous()
         self.N, self.K = w.shape
         if self.N % 16 or self.K % 32:
@@ -34,6 +36,7 @@ class ModulationProjection:
     def __call__(self, c: torch.Tensor) -> torch.Tensor:
         if c.shape[-1] != self.K:
             raise ValueError(f"c must end in {self.K}, got {tuple(c.shape)}")
+        require_device(self.w.device, c=c)
         lead = c.shape[:-1]
         x = c.float().reshape(-1, self.K).contiguous()
         out = torch.empty(x.shape[0], self.N, dtype=torch.float32, device=x.device)

@@ -16,7 +16,7 @@ import ctypes
 
 import torch
 
-from ._lib import MAX_LAYERS, MkxSourceArgs, MkxSourceDims, check, lib
+from ._lib import MAX_LAYERS, MkxSourceArgs, MkxSourceDims, check, lib, require_device
 
 
 def rope_table(n: int, hd: int = 64, theta: float = 10000.0, device="cuda"):
@@ -44,6 +44,9 @@ class SourcePrepare:
         self.wv = torch.stack([c.v_proj.weight.detach() for c in ca]).to(bf).contiguous()
         self.k_norm = torch.stack([c.k_norm.weight.detach() for c in ca]).to(bf).contiguous()  # [L, 64]
         self.eps = float(ca[0].k_norm.eps)
+        self.device = self.wk.device
+        if self.device.type != "cuda":
+            raise ValueError("the cross-attention projections must sit on the GPU")
         self.C = self.wk.shape[2]
         if self.wk.shape[1] != self.NH * 64 or self.C % 32:
             raise ValueError("k_proj must be [NH * 64, C] with C a multiple of 32")
@@ -72,6 +75,8 @@ class SourcePrepare:
             pass
 
     def __call__(self, ctx: torch.Tensor, ca_len, cos=None, sin=None):
+        require_device(self.device, ctx=ctx, ca_len=ca_len if torch.is_tensor(ca_len) else None,
+                       cos=cos, sin=sin)
         batched = ctx.dim() == 3
         x = (ctx if batched else ctx[None]).to(torch.bfloat16).contiguous()
         B, SP, C = x.shape

@@ -19,7 +19,7 @@ import ctypes
 
 import torch
 
-from ._lib import MkxRingArgs, check, lib
+from ._lib import MkxRingArgs, check, lib, require_device
 
 
 def rope_delta(delta: int, hd: int = 64, theta: float = 10000.0, device="cuda"):
@@ -51,6 +51,11 @@ class RegisterRing:
             raise ValueError("need 1 <= rows <= PM")
         self.B, self.PM, self.NH, self.HD, self.R = B, PM, NH, HD, rows
         dev = k0.device
+        if dev.type != "cuda":
+            raise ValueError("the register memory must sit on the GPU")
+        for l, (k, v) in enumerate(mem_kv):
+            require_device(dev, **{f"mem_kv[{l}].k": k, f"mem_kv[{l}].v": v})
+        self.device = dev
         self._k = [[as4(k).clone() for k, _ in mem_kv], [torch.empty(B, PM, NH, HD, dtype=torch.bfloat16, device=dev) for _ in mem_kv]]
         self._v = [[as4(v).clone() for _, v in mem_kv], [torch.empty(B, PM, NH, HD, dtype=torch.bfloat16, device=dev) for _ in mem_kv]]
         ks = torch.as_tensor(kv_start, dtype=torch.int32).reshape(-1)
@@ -79,6 +84,7 @@ class RegisterRing:
     def append_frame(self, cur_k: torch.Tensor, cur_v: torch.Tensor) -> None:
         """Append one call's register K/V ([L, B, R, NH, 64] bf16) on the current stream."""
         shape = (self.L, self.B, self.R, self.NH, self.HD)
+        require_device(self.device, cur_k=cur_k, cur_v=cur_v)
         for t, nm in ((cur_k, "cur_k"), (cur_v, "cur_v")):
             if tuple(t.shape) != shape or t.dtype != torch.bfloat16 or not t.is_contiguous():
                 raise ValueError(f"{nm} must be contiguous bf16 {shape}, got {tuple(t.shape)} {t.dtype}")

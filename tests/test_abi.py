@@ -72,3 +72,57 @@ def test_struct_layouts_match_header_sizes():
     assert ctypes.sizeof(_lib.MkxStepArgs) > 4 * 32 * 8
     assert ctypes.sizeof(_lib.MkxDims) == 14 * 4
     assert ctypes.sizeof(_lib.MkxWeights) == 21 * 8
+
+
+def test_every_args_struct_matches_the_header_layout(tmp_path):
+    # sizes and field offsets of every struct in include/mkx.h, as a C compiler lays them out, against the
+    # ctypes mirrors the Python side passes to the library
+    import subprocess
+    structs = {"mkx_dims": _lib.MkxDims, "mkx_weights": _lib.MkxWeights, "mkx_step_args": _lib.MkxStepArgs,
+               "mkx_ring_args": _lib.MkxRingArgs, "mkx_source_dims": _lib.MkxSourceDims,
+               "mkx_source_args": _lib.MkxSourceArgs, "mkx_modproj_args": _lib.MkxModprojArgs}
+    lines = ['#include <stdio.h>', '#include "mkx.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src, exe = tmp_path / "layout.c", tmp_path / "layout"
+    src.write_text("\n".join(lines))
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(ln.split()[:2]): int(ln.split()[2]) for ln in out if ln}
+    for cname, cls in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
+
+
+def test_spin_limit_setter_rejects_a_null_handle():
+    L = _lib.lib()
+    assert L.mkx_set_spin_limit(None, 5) == _lib.EINVAL
+
+
+class _Past:
+    def __init__(self, step, ca):
+        self.register_step, self.cross_attn_kv = step, ca
+
+
+def test_host_tensors_are_refused_before_any_launch():
+    # the library takes raw device pointers: host tensors must raise ValueError before anything is marshalled
+    import torch
+    from mkx.mk_expert import ExpertMegakernel
+    from mkx.modulations import ModulationProjection
+    mk = ExpertMegakernel.__new__(ExpertMegakernel)  # no handle: the check must come before any library call
+    mk.L, mk.NH, mk.HD, mk.H, mk.A, mk.register_tokens = 1, 1, 64, 64, 32, None
+    mk.device, mk._h = torch.device("cuda", 0), None
+    bf = torch.bfloat16
+    kv = (torch.zeros(1, 8, 1, 64, dtype=bf), torch.zeros(1, 8, 1, 64, dtype=bf))
+    pe = (torch.zeros(2, 64), torch.zeros(2, 64))
+    step = {"mem_kv": [kv], "cu_kv": torch.tensor([0, 8], dtype=torch.int32),
+            "cu_src": torch.tensor([0, 8], dtype=torch.int32), "sa_pe": pe, "ca_pe": pe}
+    past = _Past(step, [kv])
+    with pytest.raises(ValueError, match="x_t is on cpu"):
+        mk.run(torch.zeros(1, 2, 32), torch.zeros(2, 9 * 64 + 2 * 64), -0.1, past, 7)
+    with pytest.raises(ValueError, match="GPU"):
+        ModulationProjection(torch.zeros(32, 64), torch.zeros(32))

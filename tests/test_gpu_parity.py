@@ -132,6 +132,12 @@ def test_gelu_variant_tiny():
     _check_loop("tiny gelu_tanh", make_case(replace(TINY, act="gelu_tanh")))
 
 
+def test_gelu_variant_at_config_A_size():
+    # the GELU(tanh) MLP that BASELINE's text names, at the headline shape (H 768, I 3072, 10 layers)
+    from dataclasses import replace
+    _check_loop("A gelu_tanh", make_case(replace(SY.WORKLOADS["A"], act="gelu_tanh")))
+
+
 def test_barrier_count_invariant_and_determinism():
     case = make_case(TINY)
     cfg = case["cfg"]

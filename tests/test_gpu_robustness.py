@@ -1,0 +1,207 @@
+"""GPU tests of the boundary's failure handling and instrumentation, through the C ABI: bounded waits that
+give up (forced from the host with a tiny spin bound, so every kernel still exits normally), per-boundary
+timestamps, scratch growth under and after graph capture, and a reference-layout past captured with the
+register ring. The reference has none of these paths: its grid barrier spins without bound
+(README.md:262-263) and its timestamps are only binned by tune_mk.py (:82-95)."""
+import json
+import math
+from dataclasses import replace
+
+import pytest
+import torch
+
+from _cases import TINY, diff, make_case, oracle_steps
+from mkx import ExpertMegakernel, synthetic as SY
+from mkx import _lib
+from mkx._lib import MkxError
+
+pytestmark = pytest.mark.gpu
+torch.set_grad_enabled(False)
+
+
+def _report(name, **kv):
+    print(json.dumps({"case": name, **kv}), flush=True)
+
+
+def _first_step(case):
+    cfg = case["cfg"]
+    return case["model"]._expert_first_step(case["noise"], case["past"], None, case["mods"][..., :1, :], case["dt"],
+                                            cfg.action_dim)[0]
+
+
+def test_timeout_drains_returns_nan_and_recovers():
+    """A tiny spin bound makes waits give up: the launch still ends (every wait after the first failure
+    returns at once), its output is NaN, a second launch before mkx_check also returns NaN, mkx_check reports
+    MKX_ETIMEOUT and resets, and the next launch with the default bound matches the oracle."""
+    case = make_case(TINY)
+    cfg = case["cfg"]
+    x1 = _first_step(case)
+    mk = ExpertMegakernel(case["model"])
+    mk.set_spin_limit(1)
+    x_bad = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    torch.cuda.synchronize()
+    assert torch.isnan(x_bad).all(), "a launch whose waits gave up must return NaN"
+    x_bad2 = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)  # no mkx_check in between
+    torch.cuda.synchronize()
+    assert torch.isnan(x_bad2).all(), "a launch after an unchecked timeout must return NaN"
+    with pytest.raises(MkxError) as ei:
+        mk.check()
+    assert ei.value.status == _lib.ETIMEOUT
+    mk.check()  # reset: the flag is clear now
+    mk.set_spin_limit(None)
+    x = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    mk.check()
+    ref = oracle_steps(case, x1, 1, cfg.num_steps - 1, "fp32")
+    m, a = diff(x, ref, cfg.action_dim)
+    _report("timeout then recovery (tiny)", vs_fp32_max=m, vs_fp32_mean=a)
+    assert m <= 1e-3 and a <= 2e-4
+
+
+def test_boundary_timestamps_are_monotonic_and_inside_the_launch():
+    """mkx_set_profile: workgroup 0 stamps the launch start and every one of the barriers(n) stage boundaries
+    (the reference's prof buffer, src/mk_expert.py:66-69): nondecreasing, and spanning no more than the
+    launch's own duration on the HIP event clock."""
+    case = make_case(TINY)
+    cfg = case["cfg"]
+    x1 = _first_step(case)
+    mk = ExpertMegakernel(case["model"])
+    n = cfg.num_steps - 1
+    mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)  # warm (scratch sized)
+    mk.set_profile(n)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    x = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    e1.record()
+    mk.check()
+    ts = mk.barrier_timestamps()
+    nb = mk.barriers(n)
+    assert nb == 1 + n * (7 * cfg.L + 1)
+    stamps = ts[: nb + 1]
+    assert (stamps > 0).all(), "every boundary must be stamped"
+    d = stamps[1:] - stamps[:-1]
+    assert (d >= 0).all(), "timestamps must not decrease"
+    span_ns = float(stamps[-1] - stamps[0])
+    ev_ns = e0.elapsed_time(e1) * 1e6
+    _report("boundary timestamps (tiny)", boundaries=nb, span_us=span_ns / 1e3, event_us=ev_ns / 1e3,
+            median_stage_us=float(d.float().median()) / 1e3)
+    assert 0 < span_ns <= ev_ns + 2000.0, (span_ns, ev_ns)
+    mk.set_profile(None)
+    ref = oracle_steps(case, x1, 1, n, "fp32")
+    assert diff(x, ref, cfg.action_dim)[0] <= 1e-3  # profiling changes no result
+
+
+def test_scratch_growth_is_refused_under_and_after_capture():
+    """A call that needs more scratch than the handle holds reallocates it. Under stream capture that is
+    refused (MKX_EINVAL, nothing recorded); after a launch of the handle has been captured it is refused too
+    (MKX_EUNSUPPORTED), and the graph, which holds the current scratch, still replays the eager result."""
+    case = make_case(TINY)
+    cfg, model = case["cfg"], case["model"]
+    x1 = _first_step(case)
+    mods8, dt8 = model._step_modulations(8, case["inp"]["state_cond"])
+    # capture without an eager call at this shape first: refused before anything is recorded
+    fresh = ExpertMegakernel(model)
+    s = torch.cuda.Stream()
+    g0 = torch.cuda.CUDAGraph()
+    with pytest.raises(MkxError) as ei:
+        with torch.cuda.graph(g0, stream=s):
+            fresh.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    assert ei.value.status == _lib.EINVAL
+    torch.cuda.synchronize()
+    # eager at the small shape, capture it, then a larger eager call is refused
+    mk = ExpertMegakernel(model)
+    x_e = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim).clone()
+    mk.check()
+    g = torch.cuda.CUDAGraph()
+    out = {}
+    with torch.cuda.graph(g, stream=s):
+        out["x"] = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    torch.cuda.synchronize()
+    with pytest.raises(MkxError) as ei:
+        mk.run(x1, mods8, dt8, case["past"], cfg.action_dim)
+    assert ei.value.status == _lib.EUNSUPPORTED
+    # a call that fits the current scratch still runs, and the graph replays the eager result
+    x_small = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    torch.cuda.synchronize()
+    assert torch.equal(x_small, x_e)
+    out["x"].zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    mk.check()
+    assert torch.equal(out["x"], x_e)
+    # a second handle warmed at the larger shape runs it
+    big = ExpertMegakernel(model)
+    x8 = big.run(x1, mods8, dt8, case["past"], cfg.action_dim)
+    big.check()
+    assert torch.isfinite(x8).all()
+
+
+def test_reference_layout_past_with_ring_as_two_graphs_matches_eager():
+    """A past in the reference's layout (memory validity in cu_kv[0], source length in cu_src[1], no
+    kv_start / ca_len keys) refilled by the register ring between calls and captured as one graph per ring
+    parity: the kernel reads kv_start from the ring's device buffer (which the captured append updates), not
+    from a cu_kv snapshot, so every replayed frame equals the eager frame."""
+    from mkx.ring import RegisterRing
+    cfg = replace(SY.WORKLOADS["A"], kv_start=SY.WORKLOADS["A"].PM)
+    case = make_case(cfg)
+    model, past = case["model"], case["past"]
+    st = past.register_step
+    cu_kv = torch.tensor([int(st["kv_start"][0]), cfg.PM], dtype=torch.int32, device="cuda")
+    cu_src = torch.tensor([0, int(st["ca_len"][0])], dtype=torch.int32, device="cuda")
+    del st["kv_start"], st["ca_len"]
+    st["cu_kv"], st["cu_src"] = cu_kv, cu_src
+    mk = ExpertMegakernel(model)
+    mem0 = [(k.clone(), v.clone()) for k, v in st["mem_kv"]]
+    ks0 = cu_kv[:1].clone()
+    R, T = cfg.R_reg, cfg.T_act
+    out = {}
+
+    def call():
+        out["x"], out["k"], out["v"] = mk.run_all(case["noise"], case["mods"], case["dt"], past, cfg.action_dim)
+
+    ring_e = RegisterRing(mem0, ks0, R, kept_delta=-R, new_delta=-(T + R))
+    ring_e.update_past(past)
+    xs = []
+    for _ in range(4):
+        call()
+        xs.append(out["x"].clone())
+        ring_e.append_frame(out["k"], out["v"])
+        ring_e.update_past(past)
+    mk.check()
+    torch.cuda.synchronize()
+    assert not torch.equal(xs[0], xs[1])
+    ring_g = RegisterRing(mem0, ks0, R, kept_delta=-R, new_delta=-(T + R))
+    ring_g.update_past(past)
+    call()  # warm-up, no append
+    torch.cuda.synchronize()
+    graphs, x_of = [], []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            call()
+            ring_g.append_frame(out["k"], out["v"])
+        ring_g.update_past(past)
+        graphs.append(g)
+        x_of.append(out["x"])
+    torch.cuda.synchronize()
+    for f in range(4):
+        graphs[f % 2].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(x_of[f % 2], xs[f]), f"frame {f} differs from the eager sequence"
+    mk.check()
+    _report("reference-layout past, ring, two graphs (A)", frames=4)
+
+
+def test_ring_copies_its_inputs():
+    # the ring's two kv_start buffers alternate as append outputs: the caller's tensors must not be among them
+    from mkx.ring import RegisterRing
+    mem = [(torch.zeros(8, 2, 64, dtype=torch.bfloat16, device="cuda"),
+            torch.zeros(8, 2, 64, dtype=torch.bfloat16, device="cuda"))]
+    ks = torch.tensor([8], dtype=torch.int32, device="cuda")
+    ring = RegisterRing(mem, ks, 2)
+    ring._ks[0].fill_(0)
+    ring._k[0][0].fill_(1)
+    torch.cuda.synchronize()
+    assert int(ks[0]) == 8 and bool((mem[0][0] == 0).all())
+    assert ring.mem_kv[0][0].shape == (8, 2, 64) and int(ring.kv_start[0]) == 0
+    with pytest.raises(ValueError, match="cur_k is on cpu"):
+        ring.append_frame(torch.zeros(1, 1, 2, 2, 64, dtype=torch.bfloat16), torch.zeros(1, 1, 2, 2, 64, dtype=torch.bfloat16))

@@ -166,13 +166,9 @@ def test_modulations_reject_bad_arguments_before_touching_the_device(over, statu
     assert L.mkx_modulations(None, None) == _lib.EINVAL
 
 
-def test_register_ring_copies_its_inputs():
-    # the ring's two kv_start buffers alternate as append outputs: the caller's tensor must not be one of them
+def test_register_ring_rejects_host_memory():
+    # the ring's buffers are device pointers handed to the library: host memory is refused at construction
     from mkx.ring import RegisterRing
     mem = [(torch.zeros(8, 2, 64, dtype=torch.bfloat16), torch.zeros(8, 2, 64, dtype=torch.bfloat16))]
-    ks = torch.tensor([8], dtype=torch.int32)
-    ring = RegisterRing(mem, ks, 2)
-    ring._ks[0].fill_(0)
-    ring._k[0][0].fill_(1)
-    assert int(ks[0]) == 8 and (mem[0][0] == 0).all()
-    assert ring.mem_kv[0][0].shape == (8, 2, 64) and int(ring.kv_start[0]) == 0
+    with pytest.raises(ValueError, match="GPU"):
+        RegisterRing(mem, torch.tensor([8], dtype=torch.int32), 2)
