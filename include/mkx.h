@@ -234,6 +234,15 @@ typedef struct {
 int mkx_source_create(const mkx_source_dims* dims, const void* wk, const void* wv, const void* k_norm, void* stream,
                       mkx_source** out);
 int mkx_source_run(mkx_source* h, const mkx_source_args* args, void* stream);
+
+/* mkx_source_run for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc); no counterpart in the reference. Same arguments, kernels and
+ * results as mkx_source_run, but the call's packed context is staged in a static device array of the
+ * library (16 MiB per GPU, held until the process ends) instead of the handle's buffer, and the call
+ * allocates nothing. A context whose packed form (B * SP rows rounded up to 64, times C * 2 bytes) exceeds
+ * 16 MiB is refused with MKX_EINVAL. Every call on one GPU shares that array: calls that overlap on one GPU
+ * (concurrent streams, other threads) race and must be serialised by the caller. */
+int mkx_source_run_noalloc(mkx_source* h, const mkx_source_args* args, void* stream);
 int mkx_source_destroy(mkx_source* h);
 
 /* Modulation projection: out[r][n] = sum_k silu(c[r][k]) w[n][k] + bias[n], every AdaRMS scale, shift and

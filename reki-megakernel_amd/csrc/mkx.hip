@@ -4,7 +4,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
+#include <atomic>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -529,6 +531,82 @@ int mkx_ring_append(const mkx_ring_args* a, void* stream_) {
   return MKX_OK;
 }
 
+}  // extern "C"
+
+// Static staging for mkx_source_run_noalloc: the call's context in fragment order (rows padded to 64) lives
+// in this file-scope device array instead of the handle's allocation. Each GPU holds its own copy until the
+// process ends; calls on one GPU share it (the last call's contents stay, and calls that overlap race).
+constexpr long long SOURCE_SCRATCH_BYTES = 16LL << 20;
+static __device__ __align__(256) char scratch[SOURCE_SCRATCH_BYTES];
+
+namespace {
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::atomic<void*> g_scratch_ptr[SCRATCH_MAX_DEVICES];
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device (the host-side name is only a stand-in): looked up
+// once per device with that device current, then cached.
+int source_scratch(void** out) {
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return fail(MKX_EUNSUPPORTED, "device index beyond the static scratch table");
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+      if (!p) return fail(MKX_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return MKX_OK;
+}
+
+// Validation shared by mkx_source_run and mkx_source_run_noalloc.
+int source_args_check(const mkx_source* h, const mkx_source_args* a, const char* who) {
+  const std::string w(who);
+  if (!h || !a) return fail(MKX_EINVAL, w + ": handle or args is NULL");
+  const mkx_source_dims& d = h->dims;
+  if (a->B < 1 || a->SP < 1 || (int64_t)a->B * a->SP > d.max_rows)
+    return fail(MKX_EINVAL, w + ": need B, SP >= 1 and B * SP <= max_rows");
+  const int64_t row_elems = (int64_t)d.NH * 64;
+  if (a->B > 1 && a->src_stride_b < a->SP * row_elems)
+    return fail(MKX_EINVAL, w + ": src_stride_b smaller than one sample's cache");
+  if (a->src_stride_b & 3) return fail(MKX_EINVAL, w + ": src_stride_b must be a multiple of 4");
+  auto bad = [](const void* p, uintptr_t align) { return p == nullptr || ((uintptr_t)p & (align - 1)) != 0; };
+  if (bad(a->ctx, 16) || bad(a->ca_len, 4) || bad(a->cos, 4) || bad(a->sin, 4))
+    return fail(MKX_EINVAL, w + ": ctx, ca_len, cos, sin: NULL or misaligned");
+  for (int l = 0; l < d.L; ++l)
+    if (bad(a->kca[l], 8) || bad(a->vca[l], 8)) return fail(MKX_EINVAL, w + ": kca / vca NULL or not 8-byte aligned");
+  return MKX_OK;
+}
+
+// The two launches of a source preparation, the packed context staged at ctxp.
+int source_launch(const mkx_source* h, const mkx_source_args* a, bf16_t* ctxp, hipStream_t stream) {
+  const mkx_source_dims& d = h->dims;
+  const int nrows = a->B * a->SP;
+  const int tiles = (nrows + 63) / 64;
+  const long long n_x = (long long)tiles * 64 * d.C / 8;  // packed pieces, rows padded to 64 with zeros
+  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((n_x + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)a->ctx,
+                     ctxp, nrows, d.C, 1, n_x);
+  SourceParams p{};
+  p.L = d.L; p.NH = d.NH; p.C = d.C; p.B = a->B; p.SP = a->SP;
+  p.ctxp = ctxp; p.wkp = h->wkp; p.wvp = h->wvp; p.k_norm = h->kn;
+  p.ca_len = a->ca_len; p.cos = a->cos; p.sin = a->sin;
+  for (int l = 0; l < d.L; ++l) { p.kca[l] = a->kca[l]; p.vca[l] = a->vca[l]; }
+  p.src_sb = a->src_stride_b;
+  p.eps = d.eps;
+  hipLaunchKernelGGL(prepare_source_kernel, dim3((unsigned)tiles, (unsigned)(d.L * 2 * d.NH)), dim3(PREP_BLOCK), 0,
+                     stream, p);
+  HIPCHK(hipGetLastError());
+  return MKX_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int mkx_source_create(const mkx_source_dims* d, const void* wk, const void* wv, const void* k_norm, void* stream_,
                       mkx_source** out) {
   if (!out) return fail(MKX_EINVAL, "mkx_source_create: out is NULL");
@@ -566,42 +644,36 @@ int mkx_source_create(const mkx_source_dims* d, const void* wk, const void* wv, 
       hipMemcpyAsync(h->kn, k_norm, (size_t)d->L * 64 * 2, hipMemcpyDeviceToDevice, stream) != hipSuccess ||
       hipStreamSynchronize(stream) != hipSuccess)
     return cleanup(MKX_EHIP, "mkx_source_create: weight packing failed");
+  {
+    // the static scratch of mkx_source_run_noalloc on this device, looked up now (set-up time)
+    void* sp = nullptr;
+    const int rs = source_scratch(&sp);
+    if (rs != MKX_OK) {
+      const std::string msg = g_err;
+      return cleanup(rs, msg);
+    }
+  }
   *out = h;
   return MKX_OK;
 }
 
 int mkx_source_run(mkx_source* h, const mkx_source_args* a, void* stream_) {
-  if (!h || !a) return fail(MKX_EINVAL, "mkx_source_run: handle or args is NULL");
-  const mkx_source_dims& d = h->dims;
-  if (a->B < 1 || a->SP < 1 || (int64_t)a->B * a->SP > d.max_rows)
-    return fail(MKX_EINVAL, "mkx_source_run: need B, SP >= 1 and B * SP <= max_rows");
-  const int64_t row_elems = (int64_t)d.NH * 64;
-  if (a->B > 1 && a->src_stride_b < a->SP * row_elems)
-    return fail(MKX_EINVAL, "mkx_source_run: src_stride_b smaller than one sample's cache");
-  if (a->src_stride_b & 3) return fail(MKX_EINVAL, "mkx_source_run: src_stride_b must be a multiple of 4");
-  auto bad = [](const void* p, uintptr_t align) { return p == nullptr || ((uintptr_t)p & (align - 1)) != 0; };
-  if (bad(a->ctx, 16) || bad(a->ca_len, 4) || bad(a->cos, 4) || bad(a->sin, 4))
-    return fail(MKX_EINVAL, "mkx_source_run: ctx, ca_len, cos, sin: NULL or misaligned");
-  for (int l = 0; l < d.L; ++l)
-    if (bad(a->kca[l], 8) || bad(a->vca[l], 8))
-      return fail(MKX_EINVAL, "mkx_source_run: kca / vca NULL or not 8-byte aligned");
-  hipStream_t stream = (hipStream_t)stream_;
-  const int nrows = a->B * a->SP;
-  const int tiles = (nrows + 63) / 64;
-  const long long n_x = (long long)tiles * 64 * d.C / 8;  // packed pieces, rows padded to 64 with zeros
-  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((n_x + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)a->ctx,
-                     h->ctxp, nrows, d.C, 1, n_x);
-  SourceParams p{};
-  p.L = d.L; p.NH = d.NH; p.C = d.C; p.B = a->B; p.SP = a->SP;
-  p.ctxp = h->ctxp; p.wkp = h->wkp; p.wvp = h->wvp; p.k_norm = h->kn;
-  p.ca_len = a->ca_len; p.cos = a->cos; p.sin = a->sin;
-  for (int l = 0; l < d.L; ++l) { p.kca[l] = a->kca[l]; p.vca[l] = a->vca[l]; }
-  p.src_sb = a->src_stride_b;
-  p.eps = d.eps;
-  hipLaunchKernelGGL(prepare_source_kernel, dim3((unsigned)tiles, (unsigned)(d.L * 2 * d.NH)), dim3(PREP_BLOCK), 0,
-                     stream, p);
-  HIPCHK(hipGetLastError());
-  return MKX_OK;
+  const int rc = source_args_check(h, a, "mkx_source_run");
+  if (rc != MKX_OK) return rc;
+  return source_launch(h, a, h->ctxp, (hipStream_t)stream_);
+}
+
+int mkx_source_run_noalloc(mkx_source* h, const mkx_source_args* a, void* stream_) {
+  const int rc = source_args_check(h, a, "mkx_source_run_noalloc");
+  if (rc != MKX_OK) return rc;
+  const long long need = (long long)((a->B * a->SP + 63) / 64) * 64 * h->dims.C * 2;
+  if (need > SOURCE_SCRATCH_BYTES)
+    return fail(MKX_EINVAL, "mkx_source_run_noalloc: the packed context (" + std::to_string(need) +
+                                " bytes) exceeds the static scratch of " + std::to_string(SOURCE_SCRATCH_BYTES) + " bytes");
+  void* sp = nullptr;
+  const int rs = source_scratch(&sp);
+  if (rs != MKX_OK) return rs;
+  return source_launch(h, a, (bf16_t*)sp, (hipStream_t)stream_);
 }
 
 int mkx_source_destroy(mkx_source* h) {

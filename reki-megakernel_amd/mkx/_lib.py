@@ -15,7 +15,7 @@ Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WE
 
 EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
            "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append", "mkx_source_create", "mkx_source_run", "mkx_source_destroy",
-           "mkx_modulations", "mkx_set_spin_limit")
+           "mkx_modulations", "mkx_set_spin_limit", "mkx_source_run_noalloc")
 
 _vp = ctypes.c_void_p
 
@@ -99,6 +99,7 @@ def lib() -> ctypes.CDLL:
         L.mkx_ring_append.argtypes = [ctypes.POINTER(MkxRingArgs), _vp]
         L.mkx_source_create.argtypes = [ctypes.POINTER(MkxSourceDims), _vp, _vp, _vp, _vp, ctypes.POINTER(_vp)]
         L.mkx_source_run.argtypes = [_vp, ctypes.POINTER(MkxSourceArgs), _vp]
+        L.mkx_source_run_noalloc.argtypes = [_vp, ctypes.POINTER(MkxSourceArgs), _vp]
         L.mkx_source_destroy.argtypes = [_vp]
         L.mkx_modulations.argtypes = [ctypes.POINTER(MkxModprojArgs), _vp]
         L.mkx_set_spin_limit.argtypes = [_vp, ctypes.c_uint32]

@@ -74,7 +74,9 @@ class SourcePrepare:
         except Exception:  # interpreter shutdown
             pass
 
-    def __call__(self, ctx: torch.Tensor, ca_len, cos=None, sin=None):
+    def __call__(self, ctx: torch.Tensor, ca_len, cos=None, sin=None, static_scratch: bool = False):
+        """static_scratch: run ``mkx_source_run_noalloc`` (the context staged in the library's static device
+        array; for callers that cannot allocate) instead of ``mkx_source_run``."""
         require_device(self.device, ctx=ctx, ca_len=ca_len if torch.is_tensor(ca_len) else None,
                        cos=cos, sin=sin)
         batched = ctx.dim() == 3
@@ -102,8 +104,9 @@ class SourcePrepare:
         for l in range(self.L):
             a.kca[l], a.vca[l] = ks[l].data_ptr(), vs[l].data_ptr()
         a.src_stride_b = SP * self.NH * 64
-        check(lib().mkx_source_run(self._h, ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
-              "mkx_source_run")
+        fn = lib().mkx_source_run_noalloc if static_scratch else lib().mkx_source_run
+        check(fn(self._h, ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+              "mkx_source_run_noalloc" if static_scratch else "mkx_source_run")
         self._keep = (x, cal, cos, sin)  # inputs outlive the asynchronous launch
         if batched:
             return list(zip(ks, vs))
