@@ -33,6 +33,10 @@ in fp64; ``norm_rope`` against a complex-number rotation; ``attend`` against
 (zero gates => identity layers, zero out-projection => x unchanged, scale = -1 => AdaRMS = shift,
 one valid key => output = V, memory-row permutation invariance, padded/invalid rows have no
 effect, dims >= action_dim never feed back) and fp64 vs fp32 vs mirror consistency.
+``layer_forward``'s wiring (tests/test_oracle_wiring.py): an independent fp64 restatement of one layer with
+torch.nn.functional.linear / rms_norm / scaled_dot_product_attention and boolean key masks, on random
+non-symmetric weights and open gates; planted mutants (a transposed square projection, h instead of h2 or
+h3 into an AdaRMS) must differ from it; a cyclic-shift out-projection must move each column by one.
 """
 from __future__ import annotations
 
