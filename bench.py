@@ -22,6 +22,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "reki-megakernel_amd")]
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFS = 2500.0
+KERNEL_SOURCES = ("mkx_kernel.h", "mkx_device.h", "mkx.hip")
+
+
+def kernel_source_hash() -> str:
+    """sha256 of the megakernel's sources: ties a stored counter profile to the kernel it measured."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, "reki-megakernel_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 METRIC = "expert Euler-loop ms (steps 2–10, batch 1) + achieved HBM GB/s vs peak"
 
 
@@ -220,6 +234,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--stage-profile", action="store_true", help="also print per-stage barrier timestamps (stderr)")
+    ap.add_argument("--stage-profile-out", default="", metavar="FILE", help="write the stage profile as JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (reference kernel for the HBM traffic counters)")
     ap.add_argument("--ring-append", type=int, default=0, metavar="N",
@@ -291,13 +306,18 @@ def main() -> int:
     n_euler = cfg.num_steps - 1
     bytes_launch = SY.algorithmic_bytes_per_step(cfg) * n_euler
     achieved = bytes_launch / (kern_ms * 1e-3) / 1e9
+    # HBM bytes per launch from the PMC runs (profiles/pmc_traffic_<workload>.json), used only when they were
+    # measured on the kernel sources of this tree
     traffic = None
     tf = os.path.join(ROOT, "profiles", f"pmc_traffic_{args.workload}.json")
     if os.path.exists(tf):
         try:
-            traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+            rec = json.load(open(tf))
+            if rec.get("kernel_source_sha256") == kernel_source_hash():
+                traffic = rec.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
+    flops_launch = SY.flops_per_step(cfg) * n_euler
 
     if args.stage_profile:
         mk.set_profile(n_euler)
@@ -311,15 +331,21 @@ def main() -> int:
         for i, v in enumerate(d):
             j = i % per_step
             buckets["tail" if j == per_step - 1 else names[j % 7]].append(v)
-        print(json.dumps({"stage_us_median": {k: round(statistics.median(v), 3) for k, v in buckets.items() if v},
-                          "stage_us_sum_ms": {k: round(sum(v) / 1e3, 4) for k, v in buckets.items() if v},
-                          "first_tail_us": round((ts[1] - ts[0]) / 1e3, 3)}), file=sys.stderr)
+        prof = {"workload": args.workload, "kernel_source_sha256": kernel_source_hash(),
+                "launch_us": round((ts[-1] - ts[0]) / 1e3, 2), "boundaries": len(ts) - 1,
+                "stage_us_median": {k: round(statistics.median(v), 3) for k, v in buckets.items() if v},
+                "stage_us_p90": {k: round(sorted(v)[int(0.9 * (len(v) - 1))], 3) for k, v in buckets.items() if v},
+                "stage_us_sum_ms": {k: round(sum(v) / 1e3, 4) for k, v in buckets.items() if v},
+                "first_tail_us": round((ts[1] - ts[0]) / 1e3, 3)}
+        print(json.dumps(prof), file=sys.stderr)
+        if args.stage_profile_out:
+            with open(args.stage_profile_out, "w") as f:
+                json.dump(prof, f, indent=1)
         mk.set_profile(None)
 
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import expert_ref as ER
-        sys.path.insert(0, os.path.join(ROOT, "tests"))
         cores = host_cores()
         torch.set_num_threads(cores)
         d = ER.ExpertDims(L=cfg.L, H=cfg.H, NH=cfg.NH, I=cfg.I, ctx_dim=cfg.ctx_dim, tdim=cfg.tdim, act=cfg.act)
@@ -351,7 +377,9 @@ def main() -> int:
     out = {
         "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init N(0,0.02) bf16 weights, seeded inputs)",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) " + ("fp8 e4m3 weights with per-channel scales" if cfg.weight_dtype == "fp8_e4m3"
+                                                      else "bf16 weights") + ", seeded inputs)",
         "config": {"workload": f"{args.workload}: batch {cfg.B}, L{cfg.L} H{cfg.H} NH{cfg.NH}x{cfg.HD} I{cfg.I}, "
                                f"{cfg.T_act} action + {cfg.m_q - cfg.T_act} register rows, memory {cfg.PM} rows, "
                                f"source {cfg.S} rows, Euler steps 2-{cfg.num_steps} in one launch",
@@ -361,6 +389,13 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": bytes_launch},
+        # MFMA side of the balance (the batched workloads sit near it): algorithmic flops of the launch
+        # (2 M (6 H^2 + 3 H I) L + attention, per step) over the same time, against the dense bf16 peak, the
+        # type every MFMA of this kernel computes in (fp8 weights are converted to bf16 operands)
+        "roofline_mfma": {"bound": "mfma", "achieved": round(flops_launch / (kern_ms * 1e-3) / 1e12, 2),
+                          "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
+                          "frac": round(flops_launch / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS, 4),
+                          "algorithmic_flops_per_launch": flops_launch},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
