@@ -97,6 +97,108 @@ int lds_of(int H, int I) {
   return 0;
 }
 
+// the shape constants the host's task layout depends on
+struct ShapeK {
+  int HT, IT, SK, NH, NIN, NRED, NTW, W_NARROW, RED_NARROW, W_WIDE, RED_WIDE, SMALL;
+};
+template <class S>
+ShapeK shape_k() {
+  return {S::HT, S::IT, S::SK, S::NH, S::NIN, S::NRED, S::NTW, S::W_NARROW, S::RED_NARROW, S::W_WIDE, S::RED_WIDE, S::SMALL};
+}
+ShapeK shape_k(int H, int I, bool w8) {
+  if (H == 768 && I == 3072) return w8 ? shape_k<Shape<768, 3072, true>>() : shape_k<Shape<768, 3072, false>>();
+  if (H == 1024 && I == 4096) return w8 ? shape_k<Shape<1024, 4096, true>>() : shape_k<Shape<1024, 4096, false>>();
+  return w8 ? shape_k<Shape<256, 512, true>>() : shape_k<Shape<256, 512, false>>();
+}
+
+// Task layout of one launch: row groups, wide tiles, LDS offsets and the workgroup range of every stage's
+// tasks (Params::pl). Where the gate/up tasks and the down-projection tasks fit the grid together, each
+// stage's range is chosen to share as few workgroups as possible with the stages whose last task directly
+// gates it (the out-projections and the down projection then take NTW column tiles per task, so that they
+// need few workgroups): a workgroup is then idle in the stage before each of its tasks, so its weight DMA
+// and the transition run off the critical path, and its ready-epoch poll is not queued behind its own DMA.
+// Cross-attention, whose prefetch is the largest, gets workgroups idle in the two stages before it. The QKV
+// tasks may share workgroups with the down projection's split tasks: they wait for the reducers, a stage
+// later. Other shapes keep one task per workgroup from the bottom of the grid and the attention, reducer
+// and step-tail tasks at the top.
+struct Layout {
+  int pl[PL_KINDS];
+  int rgs_qkv, rgs_o, rgs_cao, nt_o, nt_cao, nt_down, lds_red, lds_mods;
+  bool disjoint;
+};
+Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A) {
+  Layout L{};
+  const int nattn = B * k.NH * nqt, nout = (A + TAIL_AC - 1) / TAIL_AC, mods = B * 2 * H * 4;
+  const bool wide = k.NTW > 1 && k.W_WIDE + std::max(k.RED_WIDE, k.RED_NARROW) + mods <= k.SMALL;
+  const int nt = wide ? k.NTW : 1;
+  auto clampi = [](int v, int lo, int hi) { return std::max(lo, std::min(hi, v)); };
+  const int ndown_d = (k.HT / nt) * k.SK;
+  L.disjoint = k.IT + ndown_d <= G && 6 * k.NH + std::max(k.NRED, nattn) <= G;
+  int cnt[PL_KINDS] = {};
+  if (L.disjoint) {
+    L.nt_o = L.nt_cao = L.nt_down = nt;
+    L.rgs_cao = clampi(ndown_d / (k.HT / nt), 1, RT);
+    // QKV leaves room for the self-attention tasks and the reducers; the out-projection sits inside the QKV
+    // range and leaves room for both attention stages and the CA out-projection
+    L.rgs_qkv = clampi((G - std::max(k.NRED, nattn)) / (6 * k.NH), 1, RT);
+    const int ncao = (k.HT / nt) * L.rgs_cao;
+    L.rgs_o = clampi(std::min(6 * k.NH * L.rgs_qkv, G - 2 * nattn - ncao) / (k.HT / nt), 1, RT);
+  } else {
+    L.nt_o = L.nt_cao = L.nt_down = 1;
+    L.rgs_qkv = clampi(G / (6 * k.NH), 1, RT);
+    L.rgs_o = L.rgs_cao = clampi(G / k.HT, 1, RT);
+  }
+  cnt[PL_QKV] = 6 * k.NH * L.rgs_qkv;
+  cnt[PL_SA] = cnt[PL_CA] = nattn;
+  cnt[PL_O] = (k.HT / L.nt_o) * L.rgs_o;
+  cnt[PL_CAO] = (k.HT / L.nt_cao) * L.rgs_cao;
+  cnt[PL_GU] = k.IT;
+  cnt[PL_DOWN] = (k.HT / L.nt_down) * k.SK;
+  cnt[PL_RED] = k.NRED;
+  cnt[PL_TIN] = k.NIN;
+  cnt[PL_TOUT] = nout;
+  const bool any_wide = L.nt_o > 1 || L.nt_cao > 1 || L.nt_down > 1;
+  L.lds_red = any_wide ? std::max(k.W_WIDE, k.W_NARROW) : k.W_NARROW;
+  L.lds_mods = L.lds_red + (any_wide ? std::max(k.RED_WIDE, k.RED_NARROW) : k.RED_NARROW);
+  auto md = [&](int v) { return ((v % G) + G) % G; };
+  if (L.disjoint) {
+    // base of a range that shares the fewest workgroups with the ranges of `avoid` (lowest base on ties)
+    auto place = [&](int kind, std::initializer_list<int> avoid) {
+      std::vector<char> used(G, 0);
+      for (int a : avoid)
+        for (int i = 0; i < std::min(cnt[a], G); ++i) used[(L.pl[a] + i) % G] = 1;
+      const int n = std::min(cnt[kind], G);
+      int best = 0, best_ov = G + 1;
+      for (int b = 0; b < G; ++b) {
+        int ov = 0;
+        for (int i = 0; i < n; ++i) ov += used[(b + i) % G];
+        if (ov < best_ov) { best_ov = ov; best = b; }
+      }
+      L.pl[kind] = best;
+    };
+    // stage order within a layer: QKV, SA, O, CA, CAO, GU, DOWN (+ reducers); the step tail between the
+    // last layer's reducers and the first layer's QKV. The step tail's output tasks (read a step later)
+    // share the reducers' workgroups.
+    L.pl[PL_GU] = 0;
+    place(PL_DOWN, {PL_GU});
+    place(PL_CAO, {PL_GU});
+    place(PL_RED, {PL_DOWN});
+    place(PL_QKV, {PL_RED});
+    place(PL_O, {PL_RED});
+    place(PL_SA, {PL_QKV, PL_O});
+    place(PL_CA, {PL_O, PL_SA, PL_CAO});
+    place(PL_TIN, {PL_RED, PL_QKV});
+    place(PL_TOUT, {PL_QKV, PL_TIN, PL_DOWN});
+  } else {
+    L.pl[PL_QKV] = L.pl[PL_O] = L.pl[PL_CAO] = L.pl[PL_GU] = L.pl[PL_DOWN] = 0;
+    L.pl[PL_SA] = md(G - nattn);
+    L.pl[PL_CA] = md(G - 2 * nattn);
+    L.pl[PL_TIN] = md(G - k.NIN);
+    L.pl[PL_RED] = L.pl[PL_TOUT] = md(G - k.NIN - k.NRED);
+  }
+  return L;
+}
+
 inline int ceil16(int a) { return (a + 15) / 16 * 16; }
 inline int ceil32(int a) { return (a + 31) / 32 * 32; }
 
@@ -374,18 +476,22 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   const int NRP = ceil16(NR);
   if (NRP > MAX_ROWS_PADDED) return fail(MKX_EUNSUPPORTED, "B * (T_act + R_reg) too large for this library");
   if ((long long)a->B * (H / 64) * (Mqp / 16) > FLAG_MAX) return fail(MKX_EUNSUPPORTED, "too many attention tasks for the ready-epoch table");
-  {
-    // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes)
-    const int RTn = NRP / 16, HT = H / 16, NH = H / 64;
-    auto rgs = [&](int tiles) { return std::max(1, std::min(RTn, h->G / tiles)); };
-    const int rg_o = rgs(HT);
-    if (HT * rg_o > 256 || ((RTn + rg_o - 1) / rg_o) * NH > 256 || 6 * rgs(6 * NH) > 256)
-      return fail(MKX_EUNSUPPORTED, "row grouping needs more than 256 ready epochs per wait");
-  }
   // LDS working sets (layout in mkx_kernel.h): self-attention keeps one query tile, the own rows' K and
   // V^T (hi + lo, 32-key blocks, at most 128 rows) and the wave-merge area in the 88 KB activation region;
   // the GEMM stages stage every sample's modulation slices (2 H floats) in 56 KB.
   if ((long long)a->B * 2 * H * 4 > 56 * 1024) return fail(MKX_EUNSUPPORTED, "batch too large to stage its modulation slices in LDS");
+  const ShapeK sk = shape_k(H, I, h->w8 != 0);
+  const Layout lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A);
+  {
+    // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes): gate/up on every CA out-projection
+    // task, an out-projection task on every head of its rows, cross-attention on every out-projection tile
+    // of a row group, self-attention on the QKV tasks of its head
+    const int RTn = NRP / 16, NH = H / 64;
+    if ((sk.HT / lay.nt_cao) * lay.rgs_cao > 256 || ((RTn + lay.rgs_o - 1) / lay.rgs_o) * NH > 256 ||
+        ((RTn + lay.rgs_cao - 1) / lay.rgs_cao) * NH > 256 || sk.HT > 256 || 6 * lay.rgs_qkv > 256)
+      return fail(MKX_EUNSUPPORTED, "row grouping needs more than 256 ready epochs per wait");
+    if (lay.lds_mods + a->B * 2 * H * 4 > sk.SMALL) return fail(MKX_EUNSUPPORTED, "GEMM LDS map does not fit");
+  }
   if (h->profile && mkx_barriers(h, a->n_steps) + 1 > h->prof_len) return fail(MKX_EINVAL, "profile buffer shorter than barriers + 1");
 #ifdef MKX_TRACE
   if (h->profile && mkx::TRACE_BASE + (1 + mkx_barriers(h, a->n_steps)) * h->G * mkx::TRACE_SLOTS > h->prof_len)
@@ -474,6 +580,10 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.xmask = h->xmask;
   p.prof = h->prof; p.profile = h->profile;
   p.spin_limit = h->spin_limit;
+  for (int k = 0; k < PL_KINDS; ++k) p.pl[k] = lay.pl[k];
+  p.rgs_qkv = lay.rgs_qkv; p.rgs_o = lay.rgs_o; p.rgs_cao = lay.rgs_cao;
+  p.nt_o = lay.nt_o; p.nt_cao = lay.nt_cao; p.nt_down = lay.nt_down;
+  p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
   void* args[] = {&p};
   if (capturing) h->captured = 1;
   if (capturing || h->plain_launch) {

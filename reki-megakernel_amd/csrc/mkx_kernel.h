@@ -12,9 +12,11 @@
 // cross-attention, tail) is a single inlined body driven by a runtime descriptor. The whole loop stays
 // resident in the instruction cache; a stage never waits on instruction fetch.
 //
-// Work decomposition for 256 CUs: every linear layer is cut into 16-column output tiles (one task per
-// workgroup, K = H per task; the down projection is split over K into I/H tasks per tile whose fp32
-// partials are summed in a fixed order by reducer workgroups that have no QKV task). Between finishing its
+// Work decomposition for 256 CUs: every linear layer is cut into tasks of 16-column output tiles (or NTW of
+// them, for the out-projections and the down projection) over a group of row tiles, K = H per task (the down
+// projection is split over K into I/H tasks per tile group whose fp32 partials are summed in a fixed order
+// by reducer tasks). The host places each stage's tasks on a range of workgroups (Params::pl), where the
+// grid allows on workgroups idle in the stage before. Between finishing its
 // work in one stage and waiting for the producers of its next task, a workgroup DMAs into LDS everything
 // constant that task needs: the packed weight tile (or, for attention, the cached K/V). After the wait only
 // the activations are loaded, straight into VGPRs.
@@ -80,7 +82,17 @@ struct Params {
   unsigned long long* flags;             // [FLAG_KINDS][FLAG_MAX][FLAG_STRIDE] ready epochs
   long long* prof; int profile;
   unsigned spin_limit;
+  // Task placement (computed on the host for the launch's shape): task t of placement kind k runs on
+  // workgroup (pl[k] + t) % G, then t + G, ...; the host places consecutive stages on disjoint workgroups
+  // where the grid allows, so a workgroup is idle in the stage before each of its tasks.
+  int pl[10];
+  int rgs_qkv, rgs_o, rgs_cao;  // row groups of the QKV, out-projection and CA out-projection stages
+  int nt_o, nt_cao, nt_down;    // 16-column tiles per out-projection / CA out-projection / down task (1 or NTW)
+  int lds_red, lds_mods;        // GEMM stages' LDS map: cross-wave reduction buffer, staged modulation slices
 };
+
+// placement kinds (Params::pl)
+enum { PL_QKV = 0, PL_SA, PL_O, PL_CA, PL_CAO, PL_GU, PL_DOWN, PL_RED, PL_TIN, PL_TOUT, PL_KINDS };
 
 // the kernel reads its parameters in place from the kernarg segment (constant address space), so the
 // per-layer pointer tables are indexed with scalar loads and never copied to scratch
@@ -103,13 +115,21 @@ struct Shape {
   static constexpr int SMALL = ABUF + ABUF_BYTES, SMALL_BYTES = 4 * 1024;
   static constexpr int LDS = SMALL + SMALL_BYTES;
   static constexpr int RB_FIT = 144 / (KPW * 8);  // row tiles per GEMM pass held in VGPRs (hi + lo)
-  // Workgroups of the top of the grid with fixed roles at the end of a layer and of a step: the step tail's
-  // in-projection tasks (two 16-column tiles each) on the NIN highest workgroups, below them NRED reducers,
-  // each of which sums the down projection's split-K partials of TPR output tiles (and, at the end of a step,
-  // runs the tail's output-dim tasks). None of them has a QKV task, so the next layer's QKV tasks never wait
-  // behind a reduction or a step tail on their own workgroup.
+  // Fixed-role tasks at the end of a layer and of a step: NIN step-tail in-projection tasks (two 16-column
+  // tiles each) and NRED reducers, each of which sums the down projection's split-K partials of TPR output
+  // tiles. The host places them (Params::pl) on workgroups without a QKV task, so the next layer's QKV tasks
+  // never wait behind a reduction or a step tail on their own workgroup.
   static constexpr int NIN = HT / 2, NRED = 16, TPR = HT / NRED;
   static constexpr int RBMAX = RB_FIT > 3 ? 3 : RB_FIT;
+  // Wide tasks of the gated-residual and down-projection GEMMs: NTW 16-column tiles (a reducer's TPR tiles)
+  // per task where their weights fit 72 KB of LDS, else single tiles. A wide pass holds one row tile
+  // (residual stages) or up to RBMAX (down-projection splits); its accumulators are not split into hi / lo
+  // products (NTW x row tiles independent accumulators already keep consecutive MFMAs apart).
+  static constexpr int NTW = (TPR > 1 && TPR <= 4 && TPR * NKB * CH <= 72 * 1024) ? TPR : 1;
+  // GEMM-stage LDS map, narrow (nt <= 2) and wide tasks: weight tiles from 0, then the cross-wave reduction
+  // buffer ([wave][row tile][tile][64 lanes] x 16 bytes), then the staged modulation slices
+  static constexpr int W_NARROW = 2 * NKB * CH, RED_NARROW = NWAVES * (RBMAX + 1) * 2 * 1024;
+  static constexpr int W_WIDE = NTW * NKB * CH, RED_WIDE = NWAVES * RBMAX * NTW * 1024;
   static_assert(H % 256 == 0 && I % H == 0, "H must be a multiple of 256 and I a multiple of H");
   static_assert(HT % NRED == 0 && TPR * SK <= 256, "each reducer waits on at most 256 partial tasks");
   static_assert(KPW >= 1 && RBMAX >= 1, "tile does not fit registers");
@@ -320,30 +340,26 @@ __device__ __forceinline__ float act_fn(float x, int gelu) {
   return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
-// staged per-sample modulation slice: AdaRMS stages hold [scale | shift] (2H), gated-residual stages hold gate (H)
+// staged per-sample modulation slices: gated-residual tasks hold [gate | next AdaRMS scale] (2H) at the GEMM
+// map's offset, the step tail the final [scale | shift] (2H) at its own
 template <class S>
 __device__ __forceinline__ const float* mods_lds(Ctx<S>& c, int b, int width) {
-  return (const float*)(c.smem + S::MODS) + (long long)b * width;
+  return (const float*)(c.smem + c.p.lds_mods) + (long long)b * width;
+}
+template <class S>
+__device__ __forceinline__ const float* tail_mods_lds(Ctx<S>& c, int b) {
+  return (const float*)(c.smem + S::MODS) + (long long)b * 2 * S::H;
 }
 
-// row groups of a single-pass GEMM stage with `tiles` column tiles: as many as idle workgroups allow (the
-// operand rows are the stage's critical-path load; the weight tile is prefetched)
-__device__ __forceinline__ int rgs_of(int RT, int G, int tiles) { return max(1, min(RT, G / tiles)); }
+// this workgroup's first task (then every G-th) of placement kind k
+template <class S>
+__device__ __forceinline__ int task_first(Ctx<S>& c, int k) {
+  const int t = c.wg - c.p.pl[k];
+  return t < 0 ? t + c.G : t;
+}
+
 // row group (of rgs over RT row tiles, group g covering [g RT / rgs, (g + 1) RT / rgs)) holding row tile rt
 __device__ __forceinline__ int row_group_of(int rt, int RT, int rgs) { return ((rt + 1) * rgs - 1) / RT; }
-// the step tail's in-projection task of workgroup wg (or >= NIN: none) and its reducer index (or outside
-// [0, NRED): none)
-template <class S>
-__device__ __forceinline__ int tail_in_task(int G, int wg) { return G - 1 - wg; }
-template <class S>
-__device__ __forceinline__ int reducer_of(int G, int wg) { return G - 1 - S::NIN - wg; }
-// the step tail's output task of workgroup wg (valid when below the task count): on the lowest reducers,
-// which host no self-attention task of the next step
-template <class S>
-__device__ __forceinline__ int tail_out_task(int G, int wg) {
-  const int r = reducer_of<S>(G, wg);
-  return r >= 0 && r < S::NRED ? S::NRED - 1 - r : 1 << 30;
-}
 
 // ------------------------------------------------------------------------------------------------
 // Stage descriptor: what one stage computes, where its operands live, and what to prefetch for it.
@@ -358,8 +374,9 @@ struct Desc {
   float* out; const float* res; float* part;
   float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
   const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][NRP]
-  int ntask, tiles, kind, nt;
+  int ntask, tiles, kind, nt;          // nt: 16-column tiles per task (QKV, gate/up: a pair; wide tasks: NTW)
   int rgs;                             // row groups: task t = tile t % tiles over row-tile group t / tiles
+  int pk;                              // placement kind (Params::pl)
   const char* shs;                     // AdaRMS stages: the split shift fragments of this step and layer
   // staged modulation slices (H floats each, per sample): AdaRMS stages: shift; residual stages: gate, then
   // the scale of the next AdaRMS
@@ -375,7 +392,7 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
   d.w = nullptr; d.wstride = 0; d.a = nullptr; d.out = nullptr; d.res = nullptr; d.part = nullptr;
   d.sc = nullptr; d.sc2 = nullptr;
   d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr; d.shs = nullptr;
-  d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.mod_off = 0; d.mod_off2 = 0; d.rgs = 1;
+  d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.mod_off = 0; d.mod_off2 = 0; d.rgs = 1; d.pk = PL_TIN;
   if (g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
   const int per_step = STAGES_PER_LAYER * p.L + 1;
   const int h = g - 1;
@@ -399,48 +416,63 @@ __device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
       d.w = p.wqkv + l * p.s_qkv; d.wstride = 2LL * S::NKB * S::CH; d.a = c.y_in(d.s, l); d.ssin = c.ss_in(d.s, l);
       if (S::W8) d.sc = p.sc_qkv + (long long)l * 3 * S::H;
       d.out = (float*)(fr + S::qs_off(NRP)); d.yout = (float*)(fr + S::ks_off(NRP)); d.part = (float*)(fr + S::vtb_off(NRP));
-      d.ssout = (float*)(fr + S::ssqk_off(NRP)); d.ntask = d.tiles = 6 * S::NH; d.nt = 2; d.shs = shs;
+      d.ssout = (float*)(fr + S::ssqk_off(NRP)); d.tiles = 6 * S::NH; d.nt = 2; d.shs = shs;
+      d.rgs = p.rgs_qkv; d.pk = PL_QKV;
       break;
     case ST_O:
       d.w = p.wo + l * p.s_o; d.a = (const float*)(fr + S::ysa_off(NRP)); d.out = (float*)(fr + S::h2_off(NRP));
       if (S::W8) d.sc = p.sc_o + (long long)l * S::H;
       d.yout = (float*)(fr + S::y2_off(NRP)); d.ssout = (float*)(fr + S::ss2_off(NRP));
-      d.res = c.h_in(d.s, l); d.ntask = d.tiles = S::HT; d.kind = K_RES; d.mod_off = m_sa + 2 * S::H; d.mod_off2 = m_ca;
+      d.res = c.h_in(d.s, l); d.kind = K_RES; d.mod_off = m_sa + 2 * S::H; d.mod_off2 = m_ca;
+      d.nt = p.nt_o; d.tiles = S::HT / d.nt; d.wstride = (long long)d.nt * S::NKB * S::CH; d.rgs = p.rgs_o; d.pk = PL_O;
       break;
     case ST_CAO:
       d.w = p.woca + l * p.s_o; d.a = (const float*)(fr + S::yca_off(NRP)); d.out = (float*)(fr + S::h3_off(NRP));
       if (S::W8) d.sc = p.sc_oca + (long long)l * S::H;
       d.yout = (float*)(fr + S::y3_off(NRP)); d.ssout = (float*)(fr + S::ss3_off(NRP));
-      d.res = (const float*)(fr + S::h2_off(NRP)); d.ntask = d.tiles = S::HT; d.kind = K_RES;
+      d.res = (const float*)(fr + S::h2_off(NRP)); d.kind = K_RES;
       d.mod_off = m_ca + 2 * S::H; d.mod_off2 = m_mlp;
+      d.nt = p.nt_cao; d.tiles = S::HT / d.nt; d.wstride = (long long)d.nt * S::NKB * S::CH; d.rgs = p.rgs_cao; d.pk = PL_CAO;
       break;
     case ST_GU:
       d.w = p.wgu + l * p.s_gu; d.wstride = 2LL * S::NKB * S::CH; d.a = (const float*)(fr + S::y3_off(NRP));
       if (S::W8) { d.sc = p.sc_g + (long long)l * S::I; d.sc2 = p.sc_u + (long long)l * S::I; }
       d.ssin = (const float*)(fr + S::ss3_off(NRP)); d.out = (float*)(fr + S::g_off(NRP));
-      d.ntask = d.tiles = S::IT; d.kind = K_GU; d.nt = 2; d.shs = shs + 2 * p.B * S::H * 4;
+      d.tiles = S::IT; d.kind = K_GU; d.nt = 2; d.shs = shs + 2 * p.B * S::H * 4; d.pk = PL_GU;
       break;
     case ST_DOWN:
       d.w = p.wd + l * p.s_d; d.a = (const float*)(fr + S::g_off(NRP)); d.out = (float*)(fr + S::hl_off(NRP));
       if (S::W8) d.sc = p.sc_d + (long long)l * S::H;
       d.yout = (float*)(fr + S::yl_off(NRP)); d.ssout = (float*)(fr + S::ssl_off(NRP));
       d.res = (const float*)(fr + S::h3_off(NRP)); d.part = (float*)(fr + S::part_off(NRP));
-      d.tiles = S::HT; d.ntask = S::HT * S::SK; d.kind = K_SPLIT; d.mod_off = m_mlp + 2 * S::H; d.mod_off2 = m_next;
+      d.nt = p.nt_down; d.tiles = S::HT / d.nt; d.rgs = S::SK; d.kind = K_SPLIT; d.pk = PL_DOWN;
+      d.mod_off = m_mlp + 2 * S::H; d.mod_off2 = m_next;
+      break;
+    case ST_SA:
+      d.pk = PL_SA;
+      break;
+    case ST_CA:
+      d.pk = PL_CA;
       break;
     default:
       break;
   }
-  if (d.st == ST_QKV || d.st == ST_O || d.st == ST_CAO) {
-    d.rgs = rgs_of(c.RT, c.G, d.tiles);
-    d.ntask = d.tiles * d.rgs;
-  }
+  d.ntask = d.tiles * d.rgs;  // K_SPLIT: the K splits take the place of row groups
   return d;
 }
 
+// DMA of task t's weight tiles into LDS at dst: nt consecutive 16-column tiles ([tile][k-block] chunks; the
+// down projection's splits are packed [tile][split][k-block], so its tiles are nt runs)
 template <class S>
-__device__ __forceinline__ const char* wtile(const Desc& d, int t) {
-  if (d.kind == K_SPLIT) return d.w + ((long long)(t % d.tiles) * S::SK + t / d.tiles) * S::NKB * S::CH;
-  return d.w + (long long)(t % d.tiles) * d.wstride;
+__device__ __forceinline__ void dma_task_w(Ctx<S>& c, const Desc& d, int t, char* dst) {
+  const int tile = t % d.tiles, split = t / d.tiles;
+  if (d.kind == K_SPLIT) {
+    for (int j = 0; j < d.nt; ++j)
+      dma_w(c, dst + j * S::NKB * S::CH, d.w + ((long long)(tile * d.nt + j) * S::SK + split) * S::NKB * S::CH,
+            S::NKB * S::CH);
+  } else {
+    dma_w(c, dst, d.w + (long long)tile * d.wstride, d.nt * S::NKB * S::CH);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -554,11 +586,12 @@ __device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int
   st_split4(buf, spiece(row, hd * HD + d0 + 32, c.RT), ub);
 }
 
-// MFMAs of one pass: acc[rt][nt][hi/lo] over this wave's k-blocks; the hi and lo products accumulate
-// separately and consecutive MFMAs target different accumulators, so none waits on its predecessor.
-// SWAP (V tasks): D = A W^T; otherwise D^T = W A^T. ADA adds the shift row tile acc[NRT] (always D^T).
-template <class S, int NRT, int NT, bool SWAP, bool ADA>
-__device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][2][2], const bf16x8 (&ah)[NRT][S::KPW],
+// MFMAs of one pass: acc[rt][nt][hi/lo] over this wave's k-blocks (NA = 2: the hi and lo products accumulate
+// separately, so that consecutive MFMAs target different accumulators and none waits on its predecessor;
+// NA = 1 where the row tiles and column tiles alone give that). SWAP (V tasks): D = A W^T; otherwise
+// D^T = W A^T. ADA adds the shift row tile acc[NRT] (always D^T).
+template <class S, int NRT, int NT, int NTA, int NA, bool SWAP, bool ADA>
+__device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][NTA][NA], const bf16x8 (&ah)[NRT][S::KPW],
                                          const bf16x8 (&al)[NRT][S::KPW], const bf16x8 (&sh_h)[S::KPW],
                                          const bf16x8 (&sh_l)[S::KPW], const char* wl, int wave, int lane) {
 #pragma unroll
@@ -574,13 +607,14 @@ __device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][2][2], const bf16
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
           const bf16x8 a = h ? al[rt][i] : ah[rt][i];
-          acc[rt][nt][h] = SWAP ? mfma16(a, wf[nt], acc[rt][nt][h]) : mfma16(wf[nt], a, acc[rt][nt][h]);
+          f32x4& r = acc[rt][nt][h % NA];
+          r = SWAP ? mfma16(a, wf[nt], r) : mfma16(wf[nt], a, r);
         }
     if (ADA) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         acc[NRT][nt][0] = mfma16(wf[nt], sh_h[i], acc[NRT][nt][0]);
-        acc[NRT][nt][1] = mfma16(wf[nt], sh_l[i], acc[NRT][nt][1]);
+        acc[NRT][nt][1 % NA] = mfma16(wf[nt], sh_l[i], acc[NRT][nt][1 % NA]);
       }
     }
   }
@@ -599,7 +633,7 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
   const uint32_t vlane = (uint32_t)c.lane * 16;
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
-  char* red = c.smem + S::RED;                // [wave][RB + 1][2][64 lanes] x 16 bytes
+  char* red = c.smem + p.lds_red;             // [wave][RB + 1][2][64 lanes] x 16 bytes
   // k-block major, in the order the MFMAs use them: the MFMAs of the first k-blocks start while the later
   // blocks are still arriving
   bf16x8 ah[NRT][KPW], al[NRT][KPW];
@@ -633,7 +667,7 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   if (ada) {
     // the split shift fragments, staged in LDS by the prefetch: lane l reads sample l % 16 (zeros for the
     // samples >= B)
-    const char* shl = c.smem + S::MODS;
+    const char* shl = c.smem + p.lds_mods;
     const bool has = (c.lane & 15) < p.B;
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
@@ -649,9 +683,9 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[rt][nt][0] = acc[rt][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   const char* wl = c.smem + S::WBUF;
-  if (vtask) gemm_mma<S, NRT, 2, true, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
-  else if (d.nt == 2) gemm_mma<S, NRT, 2, false, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
-  else gemm_mma<S, NRT, 1, false, false>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
+  if (vtask) gemm_mma<S, NRT, 2, 2, 2, true, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
+  else if (d.nt == 2) gemm_mma<S, NRT, 2, 2, 2, false, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
+  else gemm_mma<S, NRT, 1, 2, 2, false, false>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
   if (ada) {
     float ssp = 0.f;
 #pragma unroll
@@ -671,6 +705,57 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
               as_u4(acc[rt][nt][0] + acc[rt][nt][1]));
 }
 
+// One pass of a wide task (NTW column tiles; gated-residual stages over one row tile, down-projection splits
+// over up to RBMAX): operand loads, the residual piece (and fp8 scales) of this thread's epilogue item
+// (row tile rt0, column tile etile), the MFMAs, and the per-wave partial tiles at [wave][rt][nt] of the
+// reduction buffer.
+template <class S, int NRT>
+__device__ __forceinline__ void gemm_pass_wide(Ctx<S>& c, const Desc& d, int rt0, int kb0, int etile, EpiPre& epre) {
+  constexpr int KPW = S::KPW, NT = S::NTW, NA = NRT == 1 ? 2 : 1;
+  CP& p = c.p;
+  const int RT = c.RT;
+  const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
+  const uint32_t vlane = (uint32_t)c.lane * 16;
+  char* red = c.smem + p.lds_red;
+  bf16x8 ah[NRT][KPW], al[NRT][KPW];
+#pragma unroll
+  for (int i = 0; i < KPW; ++i)
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      const uint32_t blk = (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048);
+      ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
+      al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
+    }
+  bf16x8 sh0[KPW];
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) sh0[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  if (d.kind == K_RES) {
+    const int erow = rt0 * 16 + (c.tid & 15), eL = c.tid & 63;
+    epre = epi_const(c, d, 0, 0, etile, erow, eL);
+    epre.c0 = as_f4(ld16((const char*)d.res + fpiece(erow, etile * 16 + 4 * (eL >> 4), RT)));
+  }
+  // the staged weight tiles (issued before every load above) have landed
+  wait_vm_le<2 * NRT * KPW>();
+  exec_barrier();
+  MKX_TR(c, 1);
+  f32x4 acc[NRT + 1][NT][NA];
+#pragma unroll
+  for (int rt = 0; rt <= NRT; ++rt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int h = 0; h < NA; ++h) acc[rt][nt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+  gemm_mma<S, NRT, NT, NT, NA, false, false>(acc, ah, al, sh0, sh0, c.smem + S::WBUF, c.wave, c.lane);
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      f32x4 v = acc[rt][nt][0];
+      if (NA == 2) v += acc[rt][nt][NA - 1];
+      sts16(red + (((c.wave * NRT + rt) * NT + nt) * 64 + c.lane) * 16, as_u4(v));
+    }
+}
+
 // Waits until the producer tasks of stage g - 1 whose output lines this task reads have published: QKV reads
 // every column of its rows (the down projection's reducers or the step tail's in-projection tasks), the
 // out-projections read every head of their row tiles (attention tasks), gate/up every row of every column
@@ -687,19 +772,21 @@ __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, 
       return ((rt / NQT) * S::NH + hd) * NQT + rt % NQT;
     }, (unsigned long long)g);
   } else if (d.st == ST_GU) {
-    flag_wait(bc, F_CAO, S::HT * rgs_of(c.RT, c.G, S::HT), [](int i) { return i; }, (unsigned long long)g);
+    flag_wait(bc, F_CAO, (S::HT / c.p.nt_cao) * c.p.rgs_cao, [](int i) { return i; }, (unsigned long long)g);
   } else {
     flag_wait(bc, F_GU, S::HT, [&](int i) { return split * S::HT + i; }, (unsigned long long)g);
   }
 }
 
-// Down-projection reducer r: once the SK split tasks of its output tiles t0 .. t0 + TPR - 1 have published
-// their partial sums, it adds them in split order and applies the gated residual (hl = h3 + gate * sum, with
-// yl and the sums of squares for the next AdaRMS), then publishes one ready epoch for the TPR tiles.
+// Down-projection reducer r: once the split tasks of its output tiles t0 .. t0 + TPR - 1 have published
+// their partial sums (SK per tile group of nt tiles: split task (split, group) is task split * tiles + group),
+// it adds them in split order and applies the gated residual (hl = h3 + gate * sum, with yl and the sums of
+// squares for the next AdaRMS), then publishes one ready epoch for the TPR tiles.
 template <class S>
 __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc, int g, int r) {
   const int RT = c.RT, t0 = r * S::TPR;
-  flag_wait(bc, F_DPART, S::TPR * S::SK, [&](int i) { return (i % S::SK) * S::HT + t0 + i / S::SK; }, (unsigned long long)g);
+  const int gpr = S::TPR / d.nt, g0 = t0 / d.nt;  // tile groups (split tasks per split) of this reducer
+  flag_wait(bc, F_DPART, S::SK * gpr, [&](int i) { return (i % S::SK) * d.tiles + g0 + i / S::SK; }, (unsigned long long)g);
   wait_vm0();  // the staged gate and next AdaRMS scale (the prefetch's DMA) have landed
   __syncthreads();
   // one (tile, row tile) block of 64 items per wave and round (lanes L, L^16, L^32, L^48 hold one row);
@@ -743,17 +830,22 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
   const uint32_t vlane = (uint32_t)c.lane * 16;
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
-  char* red = c.smem + S::RED;                // [wave][RB + 1][2][64 lanes] x 16 bytes
-  for (int t = c.wg; t < d.ntask; t += c.G) {
+  char* red = c.smem + p.lds_red;             // [wave][RB + 1][2][64 lanes] x 16 bytes (wide: [wave][rt][nt])
+  // wide tasks (gated-residual or down-projection tasks of NTW column tiles); a wide gated-residual pass
+  // covers one row tile, so that each wave's epilogue item is one column tile of it
+  const bool wide = (d.kind == K_RES || d.kind == K_SPLIT) && d.nt > 1;
+  const int RBS = wide && d.kind == K_RES ? 1 : RB;
+  const int t0 = task_first(c, d.pk);
+  for (int t = t0; t < d.ntask; t += c.G) {
     const int tile = t % d.tiles, split = t / d.tiles;  // split: K quarter (K_SPLIT) or row group
     // QKV tiles: kind (q, k, v), head, quarter pair j; v is computed untransposed (D = A W^T) so that each
     // lane holds 4 consecutive keys of one d: 8 bytes of the V^T layout
     const int qkind = d.kind == K_QKV ? tile / (2 * S::NH) : 0, qhd = (tile >> 1) % S::NH, qj = tile & 1;
     const bool vtask = qkind == 2;
-    if (t != c.wg) {  // later tasks of this workgroup: load their weights now (the first was prefetched)
+    if (t != t0) {  // later tasks of this workgroup: load their weights now (the first was prefetched)
       wait_vm0();
       __syncthreads();
-      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB * S::CH);
+      dma_task_w(c, d, t, c.smem + S::WBUF);
     }
     const int kb0 = d.kind == K_SPLIT ? split * S::NKB : 0;
     const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
@@ -764,13 +856,40 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     MKX_TR(c, 14);
     gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
     MKX_TR(c, 0);
-    for (int rt0 = rt_lo; rt0 < rt_hi; rt0 += RB) {
-      const int nrt = min(RB, rt_hi - rt0);
-      if (nrt == 1) gemm_pass<S, 1>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
-      else if (nrt == 2 || RB == 2) gemm_pass<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
-      else gemm_pass<S, RB>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+    for (int rt0 = rt_lo; rt0 < rt_hi; rt0 += RBS) {
+      const int nrt = min(RBS, rt_hi - rt0);
+      if (wide) {
+        const int etile = tile * d.nt + min(c.wave, d.nt - 1);
+        if (nrt == 1) gemm_pass_wide<S, 1>(c, d, rt0, kb0, etile, epre);
+        else if (nrt == 2 || RB == 2) gemm_pass_wide<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, etile, epre);
+        else gemm_pass_wide<S, RB>(c, d, rt0, kb0, etile, epre);
+      } else {
+        if (nrt == 1) gemm_pass<S, 1>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+        else if (nrt == 2 || RB == 2) gemm_pass<S, (RB < 2 ? 1 : 2)>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+        else gemm_pass<S, RB>(c, d, rt0, kb0, vtask, qkind, qj, tile, epre);
+      }
       __syncthreads();
       MKX_TR(c, 2);
+      if (wide) {
+        // one (row tile, column tile) block of 64 items per wave and round: row (rt0 + rt) * 16 + L % 16,
+        // columns of 16-column tile tile * nt + j, 4 (L / 16) + 0..3; gated-residual passes have one row
+        // tile, so wave j's block is the one its preloaded residual piece belongs to
+        for (int blk = c.wave; blk < nrt * d.nt; blk += NWAVES) {
+          const int rt = blk / d.nt, j = blk - rt * d.nt, L = c.lane;
+          f32x4 pw[NWAVES];
+#pragma unroll
+          for (int w = 0; w < NWAVES; ++w) pw[w] = ldf4((const float*)(red + (((w * nrt + rt) * d.nt + j) * 64 + L) * 16));
+          lds_batch(pw);
+          const f32x4 v = ((pw[0] + pw[1]) + pw[2]) + pw[3];
+          const int t16 = tile * d.nt + j;
+          if (d.kind == K_SPLIT) {
+            st_sc1(d.part, (uint32_t)((((split * S::HT + t16) * RT + rt0 + rt) * 64 + L) * 16), as_u4(v));
+          } else {
+            const int row = (rt0 + rt) * 16 + (L & 15), col = t16 * 16 + 4 * (L >> 4);
+            res_piece(c, d, t16, row, col, L, S::W8 ? v * epre.sa : v, epre.c0);
+          }
+        }
+      } else
       // epilogue: one (row tile, lane) item per thread: row (rt0 + rt) * 16 + L % 16, columns tile*16 + 4 (L / 16) + 0..3
       {
         const int rt = c.tid >> 6, L = c.tid & 63;
@@ -867,15 +986,15 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
           }
         }
       }
-      if (rt0 + RB < rt_hi) __syncthreads();  // red and ssw are reused by the next pass
+      if (rt0 + RBS < rt_hi) __syncthreads();  // red and ssw are reused by the next pass
       MKX_TR(c, 3);
     }
     flag_publish(bc, d.st == ST_QKV ? F_QKV : d.st == ST_O ? F_O : d.st == ST_CAO ? F_CAO : d.st == ST_GU ? F_GU : F_DPART, t,
                  (unsigned long long)g + 1);
   }
   if (d.kind == K_SPLIT) {
-    const int r = reducer_of<S>(c.G, c.wg);
-    if (r >= 0 && r < S::NRED) down_reduce(c, d, bc, g, r);
+    const int r = task_first(c, PL_RED);
+    if (r < S::NRED) down_reduce(c, d, bc, g, r);
   }
 }
 
@@ -1095,11 +1214,11 @@ __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float*
   st_split4(y, spiece(b * c.p.Mqp + q, hd * HD + c.wave * 16 + 4 * (c.lane >> 4), c.RT), out);
 }
 
-// Attention tasks: task u -> (sample-head hh, query tile qt), u in [0, nqt * nhb), placed by attn_first on
+// Attention tasks: task u -> (sample-head hh, query tile qt), u in [0, nqt * nhb), placed (Params::pl) on
 // workgroups that the stages before leave idle, so their prefetch of the attention operands overlaps those
-// stages. Heads in complete
-// groups of 8 are arranged so that the query tiles of one head run on one XCD (u % 8 is the XCD class) and
-// share its L2; the remaining heads follow compactly.
+// stages. Heads in complete groups of 8 are arranged so that the query tiles of one head run on one XCD
+// (consecutive workgroups are on consecutive XCDs, so u % 8 is the XCD class) and share its L2; the
+// remaining heads follow compactly.
 struct AttnTask {
   int hh, qt;
   bool ok;
@@ -1120,12 +1239,6 @@ __device__ __forceinline__ AttnTask attn_task(int u, int nqt, int nhb) {
   return a;
 }
 __device__ __forceinline__ int attn_count(int nqt, int nhb) { return nqt * nhb; }
-// first task of workgroup wg (then every G-th): self-attention tasks occupy the top of the grid (idle in
-// QKV), cross-attention tasks the workgroups just below them (idle in self-attention and the
-// out-projection, so their constant operands load during both)
-__device__ __forceinline__ int attn_first(bool cross, int G, int wg, int cnt) {
-  return ((G - 1 - (cross ? cnt : 0) - wg) % G + G) % G;
-}
 
 template <class S>
 __device__ __forceinline__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd, int kvs) {
@@ -1259,7 +1372,7 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* mrg = rk + 128;
   const int NHB = p.B * S::NH;
   const bool want_kv = (d.s == 0 && p.cur_k != nullptr && p.R > 0);
-  const int u0 = attn_first(false, c.G, c.wg, attn_count(NQT, NHB));
+  const int u0 = task_first(c, PL_SA);
   for (int v = u0; v < attn_count(NQT, NHB); v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
@@ -1273,7 +1386,7 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
     // the QKV tasks of this head (q, k, v x two column pairs, every row group): the rows' sums of squares
     // and V^T blocks of one head interleave row groups within cache lines
     {
-      const int rgq = rgs_of(RT, c.G, 6 * S::NH);
+      const int rgq = p.rgs_qkv;
       flag_wait(bc, F_QKV, 6 * rgq, [&](int i) {
         const int k = i % 6, rg = i / 6;
         return rg * 6 * S::NH + (k >> 1) * 2 * S::NH + 2 * hd + (k & 1);
@@ -1434,7 +1547,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
   const int NHB = p.B * S::NH;
   const uint32_t vlane = (uint32_t)c.lane * 16;
-  const int cnt = attn_count(NQT, NHB), u0 = attn_first(true, c.G, c.wg, cnt);
+  const int cnt = attn_count(NQT, NHB), u0 = task_first(c, PL_CA);
   // The operands that do not depend on the stage before, the Wq fragments of the task's head and the shift
   // fragments (an MFMA row tile whose rows are the samples), are loaded before the barrier completes: the
   // workgroups running this stage are idle in the stage before. (Loads only: the waves that do not poll the
@@ -1458,7 +1571,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   // (wave 0 too, although its poll then completes only after these loads: the workgroups of this stage
   // enter it two stages before their operands are ready, which leaves the loads several microseconds)
   if (u0 < cnt) pre(attn_task(u0, NQT, NHB).hh % S::NH);
-  const int rgo = rgs_of(RT, c.G, S::HT);
+  const int rgo = p.rgs_o;
   for (int v = u0; v < cnt; v += c.G) {
     const AttnTask at = attn_task(v, NQT, NHB);
     if (!at.ok) continue;
@@ -1494,7 +1607,8 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     // every out-projection tile of the row group holding the query rows (their sums of squares share lines)
     {
       const int rg = row_group_of(rq, RT, rgo);
-      flag_wait(bc, F_O, S::HT, [&](int i) { return rg * S::HT + i; }, (unsigned long long)g);
+      const int to = S::HT / p.nt_o;  // out-projection tasks per row group
+      flag_wait(bc, F_O, to, [&](int i) { return rg * to + i; }, (unsigned long long)g);
     }
     MKX_TR(c, 0);
     // 1a. operands: y2 fragments of the query rows, sums of squares
@@ -1642,9 +1756,9 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 // Step tail (src/mk_expert.py:254-299): o = AdaRMS_final(h_L); v = o Wout^T + bout; x' = x + dt v;
 // h0' = x'_real Win + bin (action rows), register tokens (register rows), all fp32; with h0' its layer-0
 // AdaRMS operand y0' = h0' (1 + scale) (split) and sums of squares. Tasks [0, NIN): in-projection tasks of
-// two 16-column tiles (each recomputes the velocity of the real action dims), on the NIN highest workgroups;
+// two 16-column tiles (each recomputes the velocity of the real action dims);
 // then A / TAIL_AC output tasks of TAIL_AC dims each (x after the step, which only the next step tail
-// reads), on reducers of the down projection. Wave w takes the action rows w + 4 k, TAIL_RPW of them per
+// reads), placed by the host (Params::pl). Wave w takes the action rows w + 4 k, TAIL_RPW of them per
 // batch with their loads issued together; lane owns the 4-column pieces 4 (lane + 64 q). The final
 // modulation rows and the task's Wout rows were staged in LDS by the prefetch; the in-projection's constant
 // operands (Win columns, bias, register tokens, layer-0 scale) are loaded with the first batch.
@@ -1673,7 +1787,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   float* win_t = (float*)(c.smem + S::SMALL);            // Win columns of the task [adim][32]
   const int sn = d.first ? 0 : d.s + 1;
   // this workgroup's tasks: its in-projection task (k = 0), then its output task
-  const int tin = tail_in_task<S>(c.G, c.wg), tout = tail_out_task<S>(c.G, c.wg);
+  const int tin = task_first(c, PL_TIN), tout = task_first(c, PL_TOUT);
   bool first_task = true;
   for (int k = 0; k < 2; ++k) {
     int t = -1;
@@ -1741,7 +1855,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
         for (int k = 0; k < R; ++k) {
           const int ri = min(r0 + NWAVES * k, nrows - 1);
           const float rs = rsqrtf(ss[k] * (1.0f / (float)S::H) + p.eps);
-          const float* ml = mods_lds(c, ri / p.T, 2 * S::H);
+          const float* ml = tail_mods_lds(c, ri / p.T);
 #pragma unroll
           for (int q = 0; q < NP; ++q) {
             const int col = 4 * (c.lane + 64 * q);
@@ -1843,12 +1957,10 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
 template <class S>
 __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
-  const int t = c.wg;
-  char* mb = c.smem + S::MODS;
   MKX_TRW(c, 8);
   if (d.st == ST_SA || d.st == ST_CA) {
-    const int nqt = p.Mqp / 16, cnt = attn_count(nqt, p.B * S::NH);
-    const AttnTask at = attn_task(attn_first(d.st == ST_CA, c.G, t, cnt), nqt, p.B * S::NH);
+    const int nqt = p.Mqp / 16;
+    const AttnTask at = attn_task(task_first(c, d.pk), nqt, p.B * S::NH);
     if (at.ok) {
       const int b = at.hh / S::NH, hd = at.hh % S::NH;
       if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
@@ -1857,22 +1969,24 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   } else if (d.st == ST_TAIL) {
     // workgroups with a tail task: the final modulation rows, and the Wout rows of the task's dims (the real
     // dims for an in-projection task)
-    const int tout = tail_out_task<S>(c.G, t);
-    const bool tin = tail_in_task<S>(c.G, t) < (d.last ? 0 : S::NIN);
+    char* mb = c.smem + S::MODS;
+    const int tout = task_first(c, PL_TOUT);
+    const bool tin = task_first(c, PL_TIN) < (d.last ? 0 : S::NIN);
     if (!d.first && (tin || tout < (p.A + TAIL_AC - 1) / TAIL_AC)) {
       for (int b = 0; b < p.B; ++b) dma_f32(c, mb + b * 2 * S::H * 4, c.modrow(b, d.s) + 9 * p.L * S::H, 2 * S::H);
       if (tin) dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
       else dma_f32(c, c.smem + S::WBUF, p.wout + (long long)tout * TAIL_AC * S::H, min(TAIL_AC, p.A - tout * TAIL_AC) * S::H);
     }
   } else {
+    const int t = task_first(c, d.pk);
+    char* mb = c.smem + p.lds_mods;
     if (t < d.ntask) {
-      dma_w(c, c.smem + S::WBUF, wtile<S>(d, t), d.nt * S::NKB * S::CH);
+      dma_task_w(c, d, t, c.smem + S::WBUF);
       MKX_TRW(c, 9);
     }
     // gate and the next AdaRMS scale: the residual stages' tasks, and the down projection's reducers (its
     // split tasks only store partial sums)
-    const int red = reducer_of<S>(c.G, t);
-    if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && red >= 0 && red < S::NRED)) {
+    if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && task_first(c, PL_RED) < S::NRED)) {
       for (int b = 0; b < p.B; ++b) {
         const float* mr = c.modrow(b, d.s);
         dma_f32(c, mb + b * 2 * S::H * 4, mr + d.mod_off, S::H);
@@ -1898,10 +2012,12 @@ __device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_
 // into LDS, by waves 1-3
 template <class S>
 __device__ __forceinline__ void prefetch_shifts(Ctx<S>& c, const Desc& d) {
-  if (c.wave == 0 || !(d.kind == K_QKV || d.kind == K_GU) || c.wg >= d.ntask || d.st == ST_TAIL || d.st == ST_SA || d.st == ST_CA) return;
+  if (c.wave == 0 || !(d.kind == K_QKV || d.kind == K_GU) || d.st == ST_TAIL || d.st == ST_SA || d.st == ST_CA ||
+      task_first(c, d.pk) >= d.ntask)
+    return;
   c.dw = c.wave - 1;
   c.dn = NWAVES - 1;
-  dma_f32(c, c.smem + S::MODS, (const float*)d.shs, c.p.B * S::H);
+  dma_f32(c, c.smem + c.p.lds_mods, (const float*)d.shs, c.p.B * S::H);
   c.dw = c.wave;
   c.dn = NWAVES;
 }
