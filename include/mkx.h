@@ -44,7 +44,9 @@ typedef enum {
   MKX_EHIP = 3,          /* a HIP runtime call failed; mkx_last_error() names it */
   MKX_ETIMEOUT = 4,      /* a barrier or ready-epoch wait exceeded its spin bound; results are invalid */
   MKX_ENOMEM = 5,
-  MKX_EUNSUPPORTED = 6   /* a shape the library has no kernel instantiation for */
+  MKX_EUNSUPPORTED = 6,  /* a shape the library has no kernel instantiation for */
+  MKX_ERANGE = 7         /* a weight (at creation) or a GEMM operand (at run time) exceeds the fp16 range 65504
+                            of the GEMM operands; a launch with such an operand returns NaN */
 } mkx_status;
 
 typedef enum { MKX_WEIGHTS_BF16 = 0, MKX_WEIGHTS_FP8_E4M3 = 1 } mkx_weight_dtype;
@@ -149,8 +151,9 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* weights, void* stream, m
  * other work) until mkx_check resets the synchronisation state. */
 int mkx_run(mkx_handle* h, const mkx_step_args* args, void* stream);
 
-/* Reads the device error flag of the last launch (synchronises `stream`): MKX_OK or MKX_ETIMEOUT (and then
- * resets the handle's synchronisation state, so the next launch runs normally). */
+/* Reads the device error flag of the last launch (synchronises `stream`): MKX_OK, MKX_ETIMEOUT, or MKX_ERANGE
+ * (a GEMM operand beyond the fp16 range; that launch returned NaN), and then resets the handle's
+ * synchronisation state, so the next launch runs normally. */
 int mkx_check(mkx_handle* h, void* stream);
 
 /* Spin bound of every grid-barrier and ready-epoch wait of later launches, in polls (0 = the default,

@@ -18,8 +18,16 @@ Modes.
   ``mirror`` rounds to bf16 at every point the reference kernel rounds (marked ``bf16(.)`` in the
              citations), including the residual stream.
   ``mixed``  rounds where a bf16 MFMA kernel must (GEMM inputs and outputs, attention operands) but keeps
-             the residual stream (h0, h2, h3, h_l and the gated branch added to it) in fp32 — the
-             numerics of this library's HIP kernel, used for tight GPU checks.
+             the residual stream (h0, h2, h3, h_l and the gated branch added to it) in fp32: the numerics
+             of a bf16-activation kernel, reported beside the GPU results for comparison.
+  ``f16``    the numerics of this library's HIP kernel: every GEMM operand is rounded to fp16 (round to
+             nearest even) where the kernel stores it — the AdaRMS operand h (1 + scale) and the shift
+             (the GEMM computes rstd(h) * (Q(h (1 + scale)) W^T) + Q(shift) W^T), the attention outputs
+             before the out-projections, and the gated MLP product before the down projection — and
+             everything else stays fp32. Not a reference mode: it models the kernel's rounding points.
+             Over tens of layers these rounding decisions are chaotic (a 1e-7 relative change of the input
+             moves the result as much as the rounding itself), so this mode gives the error level the kernel
+             should show against ``fp32``, not a per-element reference.
   ``fp64``   like ``fp32`` but in float64; used by the oracle's own pin tests.
 
 Parts REKI would have supplied (its code is not available offline): the timestep embedding and
@@ -47,7 +55,7 @@ import torch
 import torch.nn.functional as F
 
 __all__ = [
-    "ExpertDims", "rounder", "rstd", "adarms", "norm_rope", "attend", "act_fn", "layer_forward",
+    "ExpertDims", "rounder", "operand_rounder", "rstd", "adarms", "norm_rope", "attend", "act_fn", "layer_forward",
     "step_tail", "in_proj", "run_steps", "timestep_embedding", "step_modulations", "rope_cos_sin",
     "register_prepare", "mods_offsets",
 ]
@@ -86,6 +94,14 @@ def rounder(mode: str):
     """The rounding hook R: bf16 round trip in ``mirror`` and ``mixed`` modes, identity otherwise."""
     if mode in ("mirror", "mixed"):
         return lambda t: t.to(torch.bfloat16).to(torch.float32)
+    return lambda t: t
+
+
+def operand_rounder(mode: str):
+    """Rounding of the GEMM operands: fp16 round trip (round to nearest even) in ``f16`` mode, identity
+    otherwise."""
+    if mode == "f16":
+        return lambda t: t.to(torch.float16).to(t.dtype)
     return lambda t: t
 
 
@@ -154,10 +170,19 @@ def layer_forward(h: torch.Tensor, l: int, W: dict, mrow: torch.Tensor, cache: d
     appended as (k, v) [R, NH, HD] (what REKI's step 1 returns as cur_k / cur_v)."""
     R = rounder(mode)
     Rr = res_rounder(mode)
+    Q = operand_rounder(mode)
     mirror = mode in ("mirror", "mixed")
     H, NH, HD = d.H, d.NH, d.HD
     M = h.shape[0]
     lw = W["layers"][l]
+
+    def ada(x, sc, sh):
+        # AdaRMS as a GEMM operand: mode f16 rounds the unnormalised operand and the shift where the kernel
+        # stores them (rstd(x) is applied to the product; AdaRMS is linear in both)
+        if mode == "f16":
+            return rstd(x, d.eps) * Q(x * (1.0 + sc)) + Q(sh)
+        return adarms(x, sc, sh, d.eps, R)
+
     off = mods_offsets(d, l)
     sa_sc, sa_sh, sa_g = (mrow[off["sa"] + i * H: off["sa"] + (i + 1) * H] for i in range(3))
     ca_sc, ca_sh, ca_g = (mrow[off["ca"] + i * H: off["ca"] + (i + 1) * H] for i in range(3))
@@ -165,7 +190,7 @@ def layer_forward(h: torch.Tensor, l: int, W: dict, mrow: torch.Tensor, cache: d
     scale = HD ** -0.5
 
     # 1. qkv = bf16(AdaRMS(h) @ [Wq;Wk;Wv]^T)  (mk_expert.py:343-348, weight packing :446-447)
-    a = adarms(h, sa_sc, sa_sh, d.eps, R)
+    a = ada(h, sa_sc, sa_sh)
     q = R(a @ lw["q"].T).view(M, NH, HD)
     k = R(a @ lw["k"].T).view(M, NH, HD)
     v = R(a @ lw["v"].T).view(M, NH, HD)
@@ -180,23 +205,23 @@ def layer_forward(h: torch.Tensor, l: int, W: dict, mrow: torch.Tensor, cache: d
     mv = cache["memv"][l, b, ks:pm]
     y = attend(qr, torch.cat([mk, kr], 0), torch.cat([mv, v], 0), scale, R, mirror).reshape(M, H)
     # 3. h2 = bf16(h + bf16(y @ Wo^T) * gate_sa)  (mk_expert.py:364-366, 162-172)
-    h2 = Rr(h + Rr(y @ lw["o"].T) * sa_g)
+    h2 = Rr(h + Rr(Q(y) @ lw["o"].T) * sa_g)
     # 4. qca = bf16(AdaRMS_ca(h2) @ Wqca^T)  (mk_expert.py:373-378)
-    a = adarms(h2, ca_sc, ca_sh, d.eps, R)
+    a = ada(h2, ca_sc, ca_sh)
     qca = R(a @ lw["ca_q"].T).view(M, NH, HD)
     # 5. cross-attention over the S valid source rows (mk_expert.py:225-251)
     qr = norm_rope(qca, lw["ca_q_norm"], cache["ca_cos"], cache["ca_sin"], d.qk_eps, R)
     S = int(cache["ca_len"][b])
     y = attend(qr, cache["kca"][l, b, :S], cache["vca"][l, b, :S], scale, R, mirror).reshape(M, H)
     # 6. h3 = bf16(h2 + bf16(y @ Woca^T) * gate_ca)  (mk_expert.py:395-397)
-    h3 = Rr(h2 + Rr(y @ lw["ca_o"].T) * ca_g)
+    h3 = Rr(h2 + Rr(Q(y) @ lw["ca_o"].T) * ca_g)
     # 7. g = bf16(act(bf16(A Wg^T)) * bf16(A Wu^T)), A = AdaRMS_mlp(h3)  (mk_expert.py:404-413)
-    a = adarms(h3, m_sc, m_sh, d.eps, R)
+    a = ada(h3, m_sc, m_sh)
     gf = R(a @ lw["gate"].T)
     uf = R(a @ lw["up"].T)
     g = R(act_fn(gf, d.act) * uf)
     # 8. h = bf16(h3 + bf16(g @ Wd^T) * gate_mlp)  (mk_expert.py:417-419)
-    return Rr(h3 + Rr(g @ lw["down"].T) * m_g)
+    return Rr(h3 + Rr(Q(g) @ lw["down"].T) * m_g)
 
 
 def in_proj(x: torch.Tensor, W: dict, action_dim: int, R) -> torch.Tensor:

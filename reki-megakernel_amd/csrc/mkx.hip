@@ -36,11 +36,13 @@ int fail(int code, const std::string& msg) {
 constexpr unsigned SPIN_LIMIT = 1u << 20;  // default spin bound of a wait (polls), about 0.5 s
 constexpr int MAX_ROWS_PADDED = 512;
 
-// W [L][N][K] row-major -> chunks (l, t, kb): dst[l*dls + (t'*tstride + toff + kb)*512 + lane*8 + j] =
-// W[l][t*16 + lane%16][kb*32 + 8(lane/16) + j] (the MFMA 16x16x32 operand layout). t' = t, or with `pairs`
-// the 16-column tiles of each 64-column head reordered 0, 2, 1, 3 (a task's d and d + 32 tiles adjacent).
+// W [L][N][K] row-major bf16 -> fp16 chunks (l, t, kb): dst[l*dls + (t'*tstride + toff + kb)*512 + lane*8 + j]
+// = W[l][t*16 + lane%16][kb*32 + 8(lane/16) + j] (the MFMA 16x16x32 operand layout). t' = t, or with
+// `pairs` the 16-column tiles of each 64-column head reordered 0, 2, 1, 3 (a task's d and d + 32 tiles
+// adjacent). bf16 -> fp16 is exact within the fp16 range (8 significant bits of 11; values below 2^-14
+// become fp16 subnormals, at most 2^-25 away); a weight beyond it sets *range.
 __global__ void pack_tiles(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst, int L, int N, int K,
-                           long long dls, int tstride, int toff, int pairs) {
+                           long long dls, int tstride, int toff, int pairs, int* range) {
   const long long total = (long long)L * (N / 16) * (K / 32) * 64;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
@@ -53,7 +55,16 @@ __global__ void pack_tiles(const bf16_t* __restrict__ src, bf16_t* __restrict__ 
   const bf16_t* s = src + ((long long)l * N + t * 16 + lane % 16) * K + kb * 32 + 8 * (lane / 16);
   const int tp = pairs ? ((t & ~3) | ((t & 1) << 1) | ((t >> 1) & 1)) : t;
   bf16_t* d = dst + (long long)l * dls + ((long long)tp * tstride + toff + kb) * 512 + lane * 8;
-  *reinterpret_cast<u32x4*>(d) = *reinterpret_cast<const u32x4*>(s);
+  const u32x4 w = *reinterpret_cast<const u32x4*>(s);
+  u32x4 o;
+  bool big = false;
+  for (int j = 0; j < 4; ++j) {
+    const float a = __uint_as_float(w[j] << 16), b = __uint_as_float(w[j] & 0xffff0000u);
+    big = big || fabsf(a) > F16_MAX || fabsf(b) > F16_MAX;
+    o[j] = cvt_pk_h(a, b);
+  }
+  *reinterpret_cast<u32x4*>(d) = o;
+  if (big) atomicOr(range, 1);
 }
 
 // The same chunk layout for e4m3 bytes: 8 bytes per lane, 512-byte chunks (dls, tstride in chunks).
@@ -288,6 +299,7 @@ const char* mkx_status_string(int status) {
     case MKX_ETIMEOUT: return "grid barrier wait exceeded its spin bound";
     case MKX_ENOMEM: return "out of device memory";
     case MKX_EUNSUPPORTED: return "unsupported shape";
+    case MKX_ERANGE: return "value beyond the fp16 range of the GEMM operands";
     default: return "unknown status";
   }
 }
@@ -372,13 +384,17 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   HCHK(alloc((void**)&h->wgu, sgu * wb));
   HCHK(alloc((void**)&h->wd, sd * wb));
   // dls, tstride, toff in chunks (16 x 32 weights)
+  // bf16 weights are packed as fp16, the GEMMs' MFMA operand type; a weight beyond the fp16 range is refused
+  int* range = nullptr;
+  HCHK(hipMalloc(&range, sizeof(int)));
+  HCHK(hipMemsetAsync(range, 0, sizeof(int), stream));
   auto pack = [&](const void* src, char* dst, int N, int K, long long dls, int tstride, int toff, int pairs) {
     const long long total = (long long)L * (N / 16) * (K / 32) * 64;
     const dim3 grid((unsigned)((total + 255) / 256));
     if (w8)
       hipLaunchKernelGGL(pack_tiles8, grid, dim3(256), 0, stream, (const uint8_t*)src, (uint8_t*)dst, L, N, K, dls, tstride, toff, pairs);
     else
-      hipLaunchKernelGGL(pack_tiles, grid, dim3(256), 0, stream, (const bf16_t*)src, (bf16_t*)dst, L, N, K, dls * 512, tstride, toff, pairs);
+      hipLaunchKernelGGL(pack_tiles, grid, dim3(256), 0, stream, (const bf16_t*)src, (bf16_t*)dst, L, N, K, dls * 512, tstride, toff, pairs, range);
   };
   const int kbh = H / 32, kbi = I / 32;
   pack(w->wqkv, h->wqkv, 3 * H, H, 3LL * (H / 16) * kbh, kbh, 0, 1);
@@ -389,6 +405,13 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   pack(w->wu, h->wgu, I, H, 2LL * (I / 16) * kbh, 2 * kbh, kbh, 0);
   pack(w->wd, h->wd, H, I, (long long)(H / 16) * kbi, kbi, 0, 0);
   HCHK(hipGetLastError());
+  {
+    int big = 0;
+    HCHK(hipMemcpyAsync(&big, range, sizeof(int), hipMemcpyDeviceToHost, stream));
+    HCHK(hipStreamSynchronize(stream));
+    (void)hipFree(range);
+    if (big) return bail(fail(MKX_ERANGE, "a bf16 weight exceeds the fp16 range (65504) of the GEMM operands"));
+  }
   if (w8) {
     const size_t n = (size_t)L * (3 * H + 3 * H + 2 * I + H);
     HCHK(alloc((void**)&h->scales, n * 4));
@@ -823,7 +846,8 @@ int mkx_check(mkx_handle* h, void* stream_) {
     HIPCHK(hipMemset(h->bar, 0, sizeof(BarState)));
     HIPCHK(hipMemset(h->flags, 0, sizeof(unsigned long long) * FLAG_KINDS * FLAG_MAX * FLAG_STRIDE));
     h->gen_before = 0;
-    return fail(MKX_ETIMEOUT, "a stage wait exceeded its spin bound; the synchronisation state was reset");
+    if (err & 1) return fail(MKX_ETIMEOUT, "a stage wait exceeded its spin bound; the synchronisation state was reset");
+    return fail(MKX_ERANGE, "a GEMM operand exceeded the fp16 range (65504); the launch returned NaN");
   }
   return MKX_OK;
 }

@@ -105,6 +105,10 @@ __device__ __forceinline__ long long clock100() { return (long long)__builtin_am
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma16h(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 
 // Cross-lane sums and maxima in registers (no LDS round trip): DPP within a 16-lane row, the gfx950
 // permlane swaps across rows. Each step adds a lane's value and its partner's, so both partners (and, at the

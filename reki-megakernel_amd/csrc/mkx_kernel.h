@@ -28,21 +28,22 @@
 // first 1 KB and the 8 bf16 residuals in the second. A wave loads one split operand fragment (16 rows x 32
 // columns, hi and lo) with two contiguous 1 KB loads and feeds it to the MFMA unchanged.
 //
-// Numerics ("split-bf16"): weights are bf16; every activation operand of an MFMA is split into a bf16 high
-// part and a bf16 residual (a = hi + lo, |lo| <= ulp(hi)/2), and both are multiplied, so the products are
-// those of the fp32 activation to ~2^-17 relative. Activations, softmax probabilities and the residual
-// stream stay fp32 between stages. The split is done once, by the producer of an operand: attention writes
-// its output split; the residual stages write h (fp32, for the next residual add), y = h * (1 + scale) of
-// the next AdaRMS (split) and per-tile partial sums of squares of h; the AdaRMS GEMM then computes
+// Numerics: the linear layers run on fp16 MFMAs with fp32 accumulation. Weights are fp16 (bf16 weights are
+// packed as fp16 at handle creation, exactly within the fp16 range; fp8 e4m3 weights are decoded to fp16, also
+// exactly). Every GEMM operand is stored once, by its producer, as fp16 (round to nearest even): attention
+// writes its output in fp16; the residual stages write h (fp32, for the next residual add), y = h * (1 + scale)
+// of the next AdaRMS (fp16) and per-tile partial sums of squares of h; the AdaRMS GEMM then computes
 // rstd(h) * (y W^T) + shift W^T (src/mk_expert.py:93-122 rearranged), with shift W^T taken by the MFMA as
-// one extra row tile of per-sample shift rows. The QKV projection is computed per (head, d-quarter pair)
-// so its epilogue holds d and d + 32 of a row: it applies the q/k norm weight and RoPE and writes the
-// attention operands split (V directly in the transposed P V layout), leaving only the per-row RMS factor,
-// which attention folds into the scores. The cross-attention query is projected inside the cross-attention
-// stage, where a workgroup holds whole head rows. The kernel therefore reproduces the fp32 eager expert
-// (not the bf16 rounding points of the reference's Triton kernel, src/mk_expert.py:119, 169-172, 220): a
-// bf16-activation kernel sits at the bf16 rounding-noise floor of the model (~1.5e-3 mean |delta| at full
-// depth), which is most of the 2e-3 parity budget.
+// one extra row tile of per-sample fp16 shift rows. The residual stream, softmax and everything between
+// stages stay fp32, and attention multiplies its operands as split bf16 (hi + lo, ~2^-17 relative). The QKV
+// projection is computed per (head, d-quarter pair) so its epilogue holds d and d + 32 of a row: it applies
+// the q/k norm weight and RoPE and writes the attention operands split (V directly in the transposed P V
+// layout), leaving only the per-row RMS factor, which attention folds into the scores. The cross-attention
+// query is projected inside the cross-attention stage, where a workgroup holds whole head rows. fp16 carries
+// 3 more significant bits than bf16: the kernel tracks the fp32 eager expert about ten times closer than a
+// bf16-activation kernel (which sits at ~1.5e-3 mean |delta| at full depth, most of the 2e-3 parity budget),
+// and loads half the operand bytes of the split-bf16 operands it replaces. An operand beyond the fp16 range
+// (65504) sets the launch's range error: the launch returns NaN and mkx_check reports it.
 #pragma once
 #include "mkx_device.h"
 
@@ -276,29 +277,33 @@ __device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);
 }
-// 8 e4m3 values (OCP fp8, as the weights are quantised) -> 8 bf16, exactly (v_cvt_pk_f32_fp8 decodes OCP
-// e4m3 on gfx950; every e4m3 value is a bf16 value)
-__device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint2 v) {
-  const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.x, true);
-  const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8((int)v.y, true);
-  u32x4 r;
-  r[0] = cvt_pk(a[0], a[1]);
-  r[1] = cvt_pk(b[0], b[1]);
-  r[2] = cvt_pk(c[0], c[1]);
-  r[3] = cvt_pk(d[0], d[1]);
-  return __builtin_bit_cast(bf16x8, r);
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+// two fp32 -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32)
+__device__ __forceinline__ uint32_t cvt_pk_h(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
 }
-// this lane's weight operand fragment of a packed chunk in LDS (chunk = its first byte)
+// 8 e4m3 values (OCP fp8, as the weights are quantised) -> 8 fp16, exactly (v_cvt_scalef32_pk_f16_fp8 with
+// scale 1 decodes OCP e4m3 on gfx950; every e4m3 value is an fp16 value)
+__device__ __forceinline__ f16x8 fp8x8_to_f16(uint2 v) {
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)v.x, 1.0f, false));
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)v.x, 1.0f, true));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)v.y, 1.0f, false));
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)v.y, 1.0f, true));
+  return __builtin_bit_cast(f16x8, r);
+}
+// this lane's fp16 weight operand fragment of a packed chunk in LDS (chunk = its first byte): bf16 weights are
+// packed as fp16 at handle creation, fp8 weights are decoded here
 template <class S>
-__device__ __forceinline__ bf16x8 wfrag_lds(const char* chunk, int lane) {
-  if constexpr (S::W8) return fp8x8_to_bf16(*reinterpret_cast<const uint2*>(chunk + lane * 8));
-  else return *reinterpret_cast<const bf16x8*>(chunk + lane * 16);
+__device__ __forceinline__ f16x8 wfrag_lds(const char* chunk, int lane) {
+  if constexpr (S::W8) return fp8x8_to_f16(*reinterpret_cast<const uint2*>(chunk + lane * 8));
+  else return *reinterpret_cast<const f16x8*>(chunk + lane * 16);
 }
 // the same from global memory
 template <class S>
-__device__ __forceinline__ bf16x8 wfrag_glb(const char* chunk, int lane) {
-  if constexpr (S::W8) return fp8x8_to_bf16(*reinterpret_cast<const uint2*>(chunk + lane * 8));
-  else return __builtin_bit_cast(bf16x8, ld16(chunk + lane * 16));
+__device__ __forceinline__ f16x8 wfrag_glb(const char* chunk, int lane) {
+  if constexpr (S::W8) return fp8x8_to_f16(*reinterpret_cast<const uint2*>(chunk + lane * 8));
+  else return __builtin_bit_cast(f16x8, ld16(chunk + lane * 16));
 }
 __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
 #pragma unroll
@@ -317,6 +322,22 @@ __device__ __forceinline__ void st_split4(void* base, uint32_t off, f32x4 v) {
   st_sc1_b64(base, off, h);
   st_sc1_b64(base, off + 1024, l);
 }
+// Largest finite fp16 value. GEMM operands are stored as fp16; a value beyond it cannot be represented.
+constexpr float F16_MAX = 65504.0f;
+// 4 fp32 values -> 4 fp16 (round to nearest even) at off of a GEMM operand buffer (the first 1 KB of each
+// 2 KB block holds an MFMA fragment), written through; returns whether a value exceeds the fp16 range
+__device__ __forceinline__ bool st_h4(void* base, uint32_t off, f32x4 v) {
+  u32x2 h;
+  h[0] = cvt_pk_h(v[0], v[1]);
+  h[1] = cvt_pk_h(v[2], v[3]);
+  st_sc1_b64(base, off, h);
+  return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) > F16_MAX;
+}
+// records that a GEMM operand of this launch exceeded the fp16 range (error bit 2): the launch returns NaN and
+// mkx_check reports MKX_ERANGE
+__device__ __forceinline__ void range_error(BarState* bs) {
+  __hip_atomic_fetch_or(&bs->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ u32x4 lds16(const char* p) { return *reinterpret_cast<const u32x4*>(p); }
 // Marks LDS values as needed together: the reads that produced them are issued back to back and waited for
 // once, instead of the compiler reusing one register and waiting after every read.
@@ -327,6 +348,7 @@ __device__ __forceinline__ void lds_batch(T (&v)[N]) {
 }
 __device__ __forceinline__ void sts16(char* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ bf16x8 ldsfrag(const char* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ f16x8 ldsfrag_h(const char* p) { return *reinterpret_cast<const f16x8*>(p); }
 __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
 // SiLU, or GELU with the tanh approximation (tanh u = 1 - 2 / (exp(2u) + 1)); hardware exp and reciprocal
@@ -502,7 +524,7 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
   const float* ml = mods_lds(c, c.sample_of(row), 2 * S::H);
   const f32x4 h = res + v * ldf4(ml + col);
   st_sc1(d.out, off, as_u4(h));
-  st_split4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)));
+  if (st_h4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)))) range_error(c.p.bar);
   float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
   ss = xor32_sum(xor16_sum(ss));
   if (L < 16) st_sc1_b32(d.ssout, ss_slot(row, tile, S::HT), __float_as_uint(ss));
@@ -586,36 +608,29 @@ __device__ __forceinline__ void qk_piece(Ctx<S>& c, const Desc& d, int kind, int
   st_split4(buf, spiece(row, hd * HD + d0 + 32, c.RT), ub);
 }
 
-// MFMAs of one pass: acc[rt][nt][hi/lo] over this wave's k-blocks (NA = 2: the hi and lo products accumulate
-// separately, so that consecutive MFMAs target different accumulators and none waits on its predecessor;
-// NA = 1 where the row tiles and column tiles alone give that). SWAP (V tasks): D = A W^T; otherwise
-// D^T = W A^T. ADA adds the shift row tile acc[NRT] (always D^T).
+// MFMAs of one pass (fp16 operands, fp16 weight fragments, fp32 accumulation) over this wave's k-blocks:
+// acc[rt][nt][i % NA] (NA = 2: consecutive k-blocks alternate between two accumulators of each tile, so that no
+// MFMA waits for its predecessor where the tiles alone are too few). SWAP (V tasks): D = A W^T; otherwise
+// D^T = W A^T. ADA adds the shift row tile (always D^T) into accs[nt][i % 2].
 template <class S, int NRT, int NT, int NTA, int NA, bool SWAP, bool ADA>
-__device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT + 1][NTA][NA], const bf16x8 (&ah)[NRT][S::KPW],
-                                         const bf16x8 (&al)[NRT][S::KPW], const bf16x8 (&sh_h)[S::KPW],
-                                         const bf16x8 (&sh_l)[S::KPW], const char* wl, int wave, int lane) {
+__device__ __forceinline__ void gemm_mma(f32x4 (&acc)[NRT][NTA][NA], f32x4 (&accs)[NTA][2], const f16x8 (&a)[NRT][S::KPW],
+                                         const f16x8 (&sh)[S::KPW], const char* wl, int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < S::KPW; ++i) {
     const int kb = wave + NWAVES * i;
-    bf16x8 wf[NT];
+    f16x8 wf[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) wf[nt] = wfrag_lds<S>(wl + (nt * S::NKB + kb) * S::CH, lane);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-          const bf16x8 a = h ? al[rt][i] : ah[rt][i];
-          f32x4& r = acc[rt][nt][h % NA];
-          r = SWAP ? mfma16(a, wf[nt], r) : mfma16(wf[nt], a, r);
-        }
+      for (int rt = 0; rt < NRT; ++rt) {
+        f32x4& r = acc[rt][nt][i % NA];
+        r = SWAP ? mfma16h(a[rt][i], wf[nt], r) : mfma16h(wf[nt], a[rt][i], r);
+      }
     if (ADA) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        acc[NRT][nt][0] = mfma16(wf[nt], sh_h[i], acc[NRT][nt][0]);
-        acc[NRT][nt][1 % NA] = mfma16(wf[nt], sh_l[i], acc[NRT][nt][1 % NA]);
-      }
+      for (int nt = 0; nt < NT; ++nt) accs[nt][i & 1] = mfma16h(wf[nt], sh[i], accs[nt][i & 1]);
     }
   }
 }
@@ -634,18 +649,15 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   const uint32_t vlane = (uint32_t)c.lane * 16;
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
   char* red = c.smem + p.lds_red;             // [wave][RB + 1][2][64 lanes] x 16 bytes
-  // k-block major, in the order the MFMAs use them: the MFMAs of the first k-blocks start while the later
-  // blocks are still arriving
-  bf16x8 ah[NRT][KPW], al[NRT][KPW];
+  // fp16 operand fragments (the first 1 KB of each 2 KB block), k-block major, in the order the MFMAs use
+  // them: the MFMAs of the first k-blocks start while the later blocks are still arriving
+  f16x8 a[NRT][KPW];
 #pragma unroll
   for (int i = 0; i < KPW; ++i)
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-      const uint32_t blk = (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048);
-      ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
-      al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
-    }
-  bf16x8 sh_h[KPW], sh_l[KPW];  // the split shift fragments of this wave's k-blocks (rows = samples)
+    for (int rt = 0; rt < NRT; ++rt)
+      a[rt][i] = __builtin_bit_cast(f16x8, bload(ra, vlane, (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048)));
+  f16x8 sh[KPW];  // the fp16 shift fragments of this wave's k-blocks (rows = samples)
   u32x4 ssv[S::HT / 16];  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
   if (ada) {
     const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
@@ -654,7 +666,7 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
     for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
   } else {
 #pragma unroll
-    for (int i = 0; i < KPW; ++i) sh_h[i] = sh_l[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < KPW; ++i) sh[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
   const int erow = epi_row(rt0, NRT, c.tid), eL = c.tid & 63;
   epre = epi_const(c, d, qkind, qj, tile, erow, eL);
@@ -662,30 +674,31 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   // The staged weights and modulation slices (the prefetch's LDS DMAs, issued before every load above) have
   // landed once no more than the activation loads are outstanding; the activations are waited for where the
   // MFMAs use them.
-  wait_vm_le<2 * NRT * KPW>();
+  wait_vm_le<NRT * KPW>();
   exec_barrier();
   if (ada) {
-    // the split shift fragments, staged in LDS by the prefetch: lane l reads sample l % 16 (zeros for the
-    // samples >= B)
+    // the shift fragments, staged in LDS by the prefetch: lane l reads sample l % 16 (zeros for the samples
+    // >= B)
     const char* shl = c.smem + p.lds_mods;
     const bool has = (c.lane & 15) < p.B;
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       const int o = (((c.lane & 15) * S::NKB + c.wave + NWAVES * i) * 4 + (c.lane >> 4)) * 32;
-      sh_h[i] = has ? ldsfrag(shl + o) : bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      sh_l[i] = has ? ldsfrag(shl + o + 16) : bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      sh[i] = has ? ldsfrag_h(shl + o) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
   MKX_TR(c, 1);
-  f32x4 acc[NRT + 1][2][2];
+  f32x4 acc[NRT][2][2], accs[2][2];
 #pragma unroll
-  for (int rt = 0; rt <= NRT; ++rt)
+  for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) acc[rt][nt][0] = acc[rt][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < NRT; ++rt) acc[rt][nt][0] = acc[rt][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accs[nt][0] = accs[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   const char* wl = c.smem + S::WBUF;
-  if (vtask) gemm_mma<S, NRT, 2, 2, 2, true, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
-  else if (d.nt == 2) gemm_mma<S, NRT, 2, 2, 2, false, true>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
-  else gemm_mma<S, NRT, 1, 2, 2, false, false>(acc, ah, al, sh_h, sh_l, wl, c.wave, c.lane);
+  if (vtask) gemm_mma<S, NRT, 2, 2, 2, true, true>(acc, accs, a, sh, wl, c.wave, c.lane);
+  else if (d.nt == 2) gemm_mma<S, NRT, 2, 2, 2, false, true>(acc, accs, a, sh, wl, c.wave, c.lane);
+  else gemm_mma<S, NRT, 1, 2, 2, false, false>(acc, accs, a, sh, wl, c.wave, c.lane);
   if (ada) {
     float ssp = 0.f;
 #pragma unroll
@@ -702,7 +715,7 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
     for (int nt = 0; nt < 2; ++nt)
       if (nt < d.nt && (rt < NRT || ada))
         sts16(red + (((c.wave * (RB + 1) + (rt < NRT ? rt : RB)) * 2 + nt) * 64 + c.lane) * 16,
-              as_u4(acc[rt][nt][0] + acc[rt][nt][1]));
+              as_u4(rt < NRT ? acc[rt][nt][0] + acc[rt][nt][1] : accs[nt][0] + accs[nt][1]));
 }
 
 // One pass of a wide task (NTW column tiles; gated-residual stages over one row tile, down-projection splits
@@ -717,35 +730,34 @@ __device__ __forceinline__ void gemm_pass_wide(Ctx<S>& c, const Desc& d, int rt0
   const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
   const uint32_t vlane = (uint32_t)c.lane * 16;
   char* red = c.smem + p.lds_red;
-  bf16x8 ah[NRT][KPW], al[NRT][KPW];
+  f16x8 a[NRT][KPW];
 #pragma unroll
   for (int i = 0; i < KPW; ++i)
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-      const uint32_t blk = (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048);
-      ah[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk));
-      al[rt][i] = __builtin_bit_cast(bf16x8, bload(ra, vlane, blk + 1024));
-    }
-  bf16x8 sh0[KPW];
+    for (int rt = 0; rt < NRT; ++rt)
+      a[rt][i] = __builtin_bit_cast(f16x8, bload(ra, vlane, (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048)));
+  f16x8 sh0[KPW];
 #pragma unroll
-  for (int i = 0; i < KPW; ++i) sh0[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < KPW; ++i) sh0[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   if (d.kind == K_RES) {
     const int erow = rt0 * 16 + (c.tid & 15), eL = c.tid & 63;
     epre = epi_const(c, d, 0, 0, etile, erow, eL);
     epre.c0 = as_f4(ld16((const char*)d.res + fpiece(erow, etile * 16 + 4 * (eL >> 4), RT)));
   }
   // the staged weight tiles (issued before every load above) have landed
-  wait_vm_le<2 * NRT * KPW>();
+  wait_vm_le<NRT * KPW>();
   exec_barrier();
   MKX_TR(c, 1);
-  f32x4 acc[NRT + 1][NT][NA];
+  f32x4 acc[NRT][NT][NA], accs[NT][2];
 #pragma unroll
-  for (int rt = 0; rt <= NRT; ++rt)
+  for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
       for (int h = 0; h < NA; ++h) acc[rt][nt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
-  gemm_mma<S, NRT, NT, NT, NA, false, false>(acc, ah, al, sh0, sh0, c.smem + S::WBUF, c.wave, c.lane);
+    accs[nt][0] = accs[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  gemm_mma<S, NRT, NT, NT, NA, false, false>(acc, accs, a, sh0, c.smem + S::WBUF, c.wave, c.lane);
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
@@ -979,7 +991,7 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
             if (d.kind == K_GU) {
 #pragma unroll
               for (int j = 0; j < 4; ++j) v[j] = act_fn(v[j], p.act) * u[j];
-              st_split4(d.out, spiece(row, col, RT), v);
+              if (st_h4(d.out, spiece(row, col, RT), v)) range_error(p.bar);
             } else {
               qk_piece(c, d, qkind, qhd, qj, row, L, v, u, epre);
             }
@@ -1211,7 +1223,7 @@ __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float*
   den = xor32_sum(xor16_sum(den));
   const int q = qt * 16 + (c.lane & 15);
   const f32x4 out = (den > 0.f && q < c.p.Mq) ? acc * (1.0f / den) : f32x4{0.f, 0.f, 0.f, 0.f};
-  st_split4(y, spiece(b * c.p.Mqp + q, hd * HD + c.wave * 16 + 4 * (c.lane >> 4), c.RT), out);
+  if (st_h4(y, spiece(b * c.p.Mqp + q, hd * HD + c.wave * 16 + 4 * (c.lane >> 4), c.RT), out)) range_error(c.p.bar);
 }
 
 // Attention tasks: task u -> (sample-head hh, query tile qt), u in [0, nqt * nhb), placed (Params::pl) on
@@ -1261,8 +1273,9 @@ __device__ __forceinline__ void sa_prefetch(Ctx<S>& c, int l, int b, int hd, int
   }
 }
 
-// Per-launch split of every AdaRMS shift slice (step s, layer l, attention / cross-attention / MLP) into
-// bf16 hi / lo: one lane per (sample, 8-column group).
+// Per-launch fp16 copy of every AdaRMS shift slice (step s, layer l, attention / cross-attention / MLP),
+// the shift row tile of the fp16 GEMMs (rounded to nearest even, like the GEMM operands): one lane per
+// (sample, 8-column group), 16 bytes in the first half of the group's 32-byte slot.
 template <class S>
 __device__ __forceinline__ void split_shifts(Ctx<S>& c) {
   CP& p = c.p;
@@ -1283,10 +1296,10 @@ __device__ __forceinline__ void split_shifts(Ctx<S>& c) {
     for (int u = 0; u < 4; ++u) {
       const int k = k0 + u * c.G * NTHREADS;
       if (k < ngrp) {
-        bf16x8 hi, lo;
-        split8(v[u], hi, lo);
-        st_sc1(p.shs, (uint32_t)(k * 32), __builtin_bit_cast(u32x4, hi));
-        st_sc1(p.shs, (uint32_t)(k * 32 + 16), __builtin_bit_cast(u32x4, lo));
+        u32x4 h;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = cvt_pk_h(v[u][2 * j], v[u][2 * j + 1]);
+        st_sc1(p.shs, (uint32_t)(k * 32), h);
       }
     }
   }
@@ -1552,7 +1565,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   // fragments (an MFMA row tile whose rows are the samples), are loaded before the barrier completes: the
   // workgroups running this stage are idle in the stage before. (Loads only: the waves that do not poll the
   // barrier reach it without waiting for them.)
-  bf16x8 wf[4][KPW], sh_h[KPW], sh_l[KPW];
+  f16x8 wf[4][KPW], sh[KPW];
   auto pre = [&](int hd) {
     const __amdgpu_buffer_rsrc_t rsh =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(shs), (short)0, p.B * S::H * 4, 0x00020000);
@@ -1561,8 +1574,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       const int kb = c.wave + NWAVES * i;
       // lane l reads sample l % 16; samples >= B fall outside the buffer and read zeros
       const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + kb) * 4 + (c.lane >> 4)) * 32);
-      sh_h[i] = __builtin_bit_cast(bf16x8, bload(rsh, o, 0));
-      sh_l[i] = __builtin_bit_cast(bf16x8, bload(rsh, o + 16, 0));
+      sh[i] = __builtin_bit_cast(f16x8, bload(rsh, o, 0));
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
         wf[nt][i] = wfrag_glb<S>(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * S::CH, c.lane);
@@ -1600,9 +1612,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 #pragma unroll
     for (int i = 0; i < KPW; ++i)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) accb[nt][h] = mfma16(wf[nt][i], h ? sh_l[i] : sh_h[i], accb[nt][h]);
+      for (int nt = 0; nt < 4; ++nt) accb[nt][i & 1] = mfma16h(wf[nt][i], sh[i], accb[nt][i & 1]);
     MKX_TR(c, 14);
     // every out-projection tile of the row group holding the query rows (their sums of squares share lines)
     {
@@ -1611,17 +1621,15 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       flag_wait(bc, F_O, to, [&](int i) { return rg * to + i; }, (unsigned long long)g);
     }
     MKX_TR(c, 0);
-    // 1a. operands: y2 fragments of the query rows, sums of squares
-    bf16x8 yh[KPW], ylo[KPW];
+    // 1a. operands: y2 fragments (fp16) of the query rows, sums of squares
+    f16x8 yh[KPW];
     u32x4 ssv[S::HT / 16];
     {
       const __amdgpu_buffer_rsrc_t ry = rsrc(y2);
 #pragma unroll
       for (int i = 0; i < KPW; ++i) {
         const int kb = c.wave + NWAVES * i;
-        const uint32_t blk = (uint32_t)((kb * RT + rq) * 2048);
-        yh[i] = __builtin_bit_cast(bf16x8, bload(ry, vlane, blk));
-        ylo[i] = __builtin_bit_cast(bf16x8, bload(ry, vlane, blk + 1024));
+        yh[i] = __builtin_bit_cast(f16x8, bload(ry, vlane, (uint32_t)((kb * RT + rq) * 2048)));
       }
       const __amdgpu_buffer_rsrc_t rs_ = rsrc(ss2);
       const uint32_t so = (uint32_t)(((rq * 16 + (c.lane & 15)) * S::HT + c.wave * (S::HT / 4)) * 4);
@@ -1630,20 +1638,18 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     }
     // Everything but the query rows and their sums of squares has landed (the prefetched K/V chunks were
     // issued before them); the query rows are waited for where the MFMAs use them.
-    wait_vm_le<2 * KPW + S::HT / 16>();
+    wait_vm_le<KPW + S::HT / 16>();
     __builtin_amdgcn_sched_barrier(0);  // every query-row load is issued before the first MFMA
     MKX_TR(c, 3);
     {
-      // [column tile][hi, lo]: 8 independent accumulation chains
+      // [column tile][k-block parity]: 8 independent accumulation chains
       f32x4 acc[4][2];
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) acc[nt][0] = acc[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < KPW; ++i)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int nt = 0; nt < 4; ++nt) acc[nt][h] = mfma16(wf[nt][i], h ? ylo[i] : yh[i], acc[nt][h]);
+        for (int nt = 0; nt < 4; ++nt) acc[nt][i & 1] = mfma16h(wf[nt][i], yh[i], acc[nt][i & 1]);
       float ssp = 0.f;
 #pragma unroll
       for (int i = 0; i < S::HT / 16; ++i) {
@@ -1941,7 +1947,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
                     __uint_as_float(rg.y & 0xffff0000u)};
         }
         st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
-        st_split4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc));
+        if (st_h4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc))) range_error(p.bar);
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
         ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
         if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, 2 * t + (q >> 2), S::HT), __float_as_uint(ss));

@@ -8,7 +8,7 @@ import os
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmkx.so")
 MAX_LAYERS = 32
 
-OK, EINVAL, ENORESIDENT, EHIP, ETIMEOUT, ENOMEM, EUNSUPPORTED = range(7)
+OK, EINVAL, ENORESIDENT, EHIP, ETIMEOUT, ENOMEM, EUNSUPPORTED, ERANGE = range(8)
 WEIGHTS_BF16, WEIGHTS_FP8_E4M3 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
 Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WEIGHT_BYTES, Q_LDS_BYTES = range(8)

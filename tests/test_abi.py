@@ -29,9 +29,10 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_status_strings():
     L = _lib.lib()
     assert L.mkx_abi_version() == 1
-    for s in range(7):
-        assert L.mkx_status_string(s).decode()
+    for s in range(8):
+        assert L.mkx_status_string(s).decode() != "unknown status"
     assert L.mkx_status_string(_lib.ETIMEOUT).decode().startswith("grid barrier")
+    assert "fp16" in L.mkx_status_string(_lib.ERANGE).decode()
 
 
 def _dims(**over):

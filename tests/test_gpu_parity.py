@@ -1,8 +1,11 @@
 """GPU parity of the HIP megakernel against the CPU oracle, through the C ABI (via mkx.ExpertMegakernel).
 
 Tolerances: the parity metric is max |delta| <= 1e-2 and mean |delta| <= 2e-3 over the real action dims
-against the fp32 oracle (the eager fp32 expert). Against the ``mixed`` oracle, which rounds where this
-kernel rounds, the bound is tighter (accumulation order and exp/rsqrt approximations remain).
+against the fp32 oracle (the eager fp32 expert). The kernel's own error level is that of the ``f16`` oracle,
+which rounds the GEMM operands to fp16 where this kernel stores them: over tens of layers the rounding
+decisions are chaotic (a 1e-7 relative change of the input re-rolls them and moves the result as much as the
+rounding itself), so the ``f16`` oracle fixes the size of the error the kernel should show against fp32, not
+its per-element value.
 """
 import json
 import math
@@ -20,9 +23,13 @@ torch.set_grad_enabled(False)
 
 # Parity bound (against the fp32 oracle, real action dims): max |delta| <= 1e-2, mean <= 2e-3.
 FP32_MAX, FP32_MEAN = 1e-2, 2e-3
-# The kernel multiplies fp32 activations as split bf16 (hi + lo) against bf16 weights, so it tracks the
-# fp32 oracle far inside the parity bound; this tighter bound is the kernel's own precision claim.
-TIGHT_MAX, TIGHT_MEAN = 1e-3, 2e-4
+# The kernel multiplies fp16 GEMM operands (activations rounded to nearest even where they are stored) with
+# fp16 or fp8 weights into fp32 accumulators and keeps everything else fp32, so it tracks the fp32 oracle
+# five times inside the parity bound (a bf16-activation kernel, the ``mixed`` oracle, uses most of it) ...
+TIGHT_MAX, TIGHT_MEAN = 2e-3, 4e-4
+# ... and its error against fp32 is at most this factor above that of the ``f16`` oracle (same rounding
+# points, different accumulation order and exp / rsqrt approximations)
+F16_FACTOR_MAX, F16_FACTOR_MEAN = 3.0, 2.0
 
 
 def _report(name, **kv):
@@ -49,10 +56,14 @@ def _check_loop(name, case, tight=(TIGHT_MAX, TIGHT_MEAN)):
     mall, _ = diff(x, r32, cfg.A)
     rmx = oracle_steps(case, x1, 1, n, "mixed")  # bf16-activation numerics, reported for comparison
     mmx, amx = diff(rmx, r32, cfg.action_dim)
-    _report(name, vs_fp32_max=m32, vs_fp32_mean=a32, all_dims_max=mall, bf16_activation_oracle_vs_fp32_max=mmx,
-            bf16_activation_oracle_vs_fp32_mean=amx, max_abs_x=float(r32[..., : cfg.action_dim].abs().max()))
+    r16 = oracle_steps(case, x1, 1, n, "f16")  # the kernel's own rounding points: its expected error level
+    m16, a16 = diff(r16, r32, cfg.action_dim)
+    _report(name, vs_fp32_max=m32, vs_fp32_mean=a32, all_dims_max=mall, f16_oracle_vs_fp32_max=m16, f16_oracle_vs_fp32_mean=a16,
+            bf16_activation_oracle_vs_fp32_max=mmx, bf16_activation_oracle_vs_fp32_mean=amx,
+            max_abs_x=float(r32[..., : cfg.action_dim].abs().max()))
     assert m32 <= FP32_MAX and a32 <= FP32_MEAN, (m32, a32)
     assert m32 <= tight[0] and a32 <= tight[1], (m32, a32)
+    assert m32 <= F16_FACTOR_MAX * m16 + 1e-5 and a32 <= F16_FACTOR_MEAN * a16 + 1e-6, (m32, a32, m16, a16)
     assert mall <= FP32_MAX
     return mk, x1, x
 

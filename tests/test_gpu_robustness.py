@@ -1,5 +1,6 @@
 """GPU tests of the boundary's failure handling and instrumentation, through the C ABI: bounded waits that
-give up (forced from the host with a tiny spin bound, so every kernel still exits normally), per-boundary
+give up (forced from the host with a tiny spin bound, so every kernel still exits normally), GEMM operands
+beyond the fp16 range (forced with huge inputs; the launch completes and reports it), per-boundary
 timestamps, scratch growth under and after graph capture, and a reference-layout past captured with the
 register ring. The reference has none of these paths: its grid barrier spins without bound
 (README.md:262-263) and its timestamps are only binned by tune_mk.py (:82-95)."""
@@ -55,6 +56,33 @@ def test_timeout_drains_returns_nan_and_recovers():
     m, a = diff(x, ref, cfg.action_dim)
     _report("timeout then recovery (tiny)", vs_fp32_max=m, vs_fp32_mean=a)
     assert m <= 1e-3 and a <= 2e-4
+
+
+def test_operands_beyond_the_fp16_range_are_reported():
+    """GEMM operands are stored as fp16: a launch whose activations exceed 65504 (inputs scaled by 1e9) still
+    completes, returns NaN, and mkx_check reports MKX_ERANGE and resets; the next launch with the ordinary
+    inputs matches the oracle. A bf16 weight beyond the fp16 range is refused when the handle is created."""
+    case = make_case(TINY)
+    cfg = case["cfg"]
+    x1 = _first_step(case)
+    mk = ExpertMegakernel(case["model"])
+    x_bad = mk.run(x1 * 1e9, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    torch.cuda.synchronize()
+    assert torch.isnan(x_bad).all(), "a launch with an operand beyond the fp16 range must return NaN"
+    with pytest.raises(MkxError) as ei:
+        mk.check()
+    assert ei.value.status == _lib.ERANGE
+    x = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    mk.check()
+    ref = oracle_steps(case, x1, 1, cfg.num_steps - 1, "fp32")
+    m, a = diff(x, ref, cfg.action_dim)
+    _report("fp16 range error then recovery (tiny)", vs_fp32_max=m, vs_fp32_mean=a)
+    assert m <= 1e-3 and a <= 2e-4
+    W = SY.make_weights(TINY, 0)
+    W["layers"][1]["down"][3, 5] = 1.0e5  # bf16 1e5 > 65504
+    with pytest.raises(MkxError) as ei:
+        ExpertMegakernel(SY.SyntheticReki(TINY, W, device="cuda"))
+    assert ei.value.status == _lib.ERANGE
 
 
 def test_boundary_timestamps_are_monotonic_and_inside_the_launch():

@@ -159,6 +159,41 @@ def test_mirror_rounds_to_bf16():
     assert got[2] == 3.140625
 
 
+def test_f16_mode_rounds_gemm_operands_to_nearest_even_fp16():
+    Q = ER.operand_rounder("f16")
+    x = torch.tensor([1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 3.14159265, 70000.0], dtype=torch.float64)
+    got = Q(x)
+    assert got[0] == 1.0  # ties to even (fp16 keeps 10 fraction bits)
+    assert got[1] == 1.0 + 2 ** -9
+    assert got[2] == 3.140625
+    assert math.isinf(got[3])  # beyond the fp16 range: the kernel reports this launch as a range error
+    for mode in ("fp32", "fp64", "mirror", "mixed"):
+        assert torch.equal(ER.operand_rounder(mode)(x), x)
+
+
+def test_f16_mode_error_sits_between_fp32_and_bf16():
+    """fp16 operands: rounding is active, and with 3 more fraction bits than bf16 the f16 mode stays several
+    times closer to fp64 than the bf16-activation (mixed) mode; with the operand rounding made the identity,
+    the f16 mode's AdaRMS-as-operand form (rstd(h) Q(h (1 + scale)) + Q(shift)) equals the fp32 mode."""
+    d = TINY
+    W, cache, mods, x = tiny_weights(d), tiny_cache(d), tiny_mods(d, n=3), tiny_x()
+    r64 = _run(x, mods, W, cache, d, mode="fp64")
+    r32 = _run(x, mods, W, cache, d, mode="fp32")
+    r16 = _run(x, mods, W, cache, d, mode="f16")
+    rmx = _run(x, mods, W, cache, d, mode="mixed")
+    e16 = (r16 - r64).abs().max()
+    emx = (rmx - r64).abs().max()
+    assert e16 > 10 * (r32 - r64).abs().max()
+    assert e16 * 4 < emx
+    orig = ER.operand_rounder
+    try:
+        ER.operand_rounder = lambda mode: (lambda t: t)
+        r16_id = _run(x, mods, W, cache, d, mode="f16")
+    finally:
+        ER.operand_rounder = orig
+    assert (r16_id - r32).abs().max() < 1e-6
+
+
 def test_timestep_embedding_closed_form():
     e = ER.timestep_embedding(torch.tensor([0.0, 0.5]), 8)
     assert torch.all(e[0, :4] == 1) and torch.all(e[0, 4:] == 0)

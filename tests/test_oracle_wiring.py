@@ -107,12 +107,12 @@ def _mutant(old: str, new: str):
 
 
 @pytest.mark.parametrize("old,new", [
-    ('Rr(y @ lw["o"].T)', 'Rr(y @ lw["o"])'),          # transposed self-attention out-projection
-    ('Rr(y @ lw["ca_o"].T)', 'Rr(y @ lw["ca_o"])'),    # transposed cross-attention out-projection
+    ('Rr(Q(y) @ lw["o"].T)', 'Rr(Q(y) @ lw["o"])'),          # transposed self-attention out-projection
+    ('Rr(Q(y) @ lw["ca_o"].T)', 'Rr(Q(y) @ lw["ca_o"])'),    # transposed cross-attention out-projection
     ('R(a @ lw["ca_q"].T)', 'R(a @ lw["ca_q"])'),      # transposed cross-attention query projection
     ('R(a @ lw["q"].T)', 'R(a @ lw["q"])'),            # transposed q projection
-    ("a = adarms(h2, ca_sc", "a = adarms(h, ca_sc"),    # CA query from h instead of h2
-    ("a = adarms(h3, m_sc", "a = adarms(h2, m_sc"),     # MLP from h2 instead of h3
+    ("a = ada(h2, ca_sc", "a = ada(h, ca_sc"),          # CA query from h instead of h2
+    ("a = ada(h3, m_sc", "a = ada(h2, m_sc"),           # MLP from h2 instead of h3
     ("h3 = Rr(h2 +", "h3 = Rr(h +"),                   # CA residual onto h instead of h2
 ])
 def test_planted_wiring_mistakes_are_detected(old, new):
