@@ -140,9 +140,10 @@ struct Shape {
   // frame layout (bytes), buffers of NRP rows; HB = NRP * H * 4:
   //   qs, ks: split q / k (roped, not normed) | vt: split V^T blocks per (sample, head) (2 HB) | ysa split |
   //   h2 fp32 | y2 split | yca split | h3 fp32 | y3 split | g split (I columns) | hl fp32 | yl split |
-  //   part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ss2, ss3, ssl [NRP][HT]
-  // (sums of squares of h per 16-column tile t, at row * HT + (t % 4) * HT / 4 + t / 4: wave w of a consumer
-  // reads its tiles w + 4 i as one contiguous run)
+  //   part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ss2, ss3, ssl [HT][RT][32]
+  // (sums of squares of h per 16-column tile t and row: one 128-byte line per (tile, 16-row tile), its first
+  // 16 floats used, so that each line has exactly one writer: several producers writing 4-byte pieces of one
+  // line at once take twice as long to be acknowledged)
   __host__ __device__ static long long hb(int nrp) { return (long long)nrp * H * 4; }
   __host__ __device__ static long long qs_off(int) { return 0; }
   __host__ __device__ static long long ks_off(int nrp) { return hb(nrp); }
@@ -159,11 +160,12 @@ struct Shape {
   __host__ __device__ static long long part_off(int nrp) { return (12 + SK) * hb(nrp); }
   __host__ __device__ static long long ssqk_off(int nrp) { return (12 + 2 * SK) * hb(nrp); }
   __host__ __device__ static long long ss2_off(int nrp) { return ssqk_off(nrp) + 4LL * NH * nrp * 4; }
-  __host__ __device__ static long long ss3_off(int nrp) { return ss2_off(nrp) + (long long)HT * nrp * 4; }
-  __host__ __device__ static long long ssl_off(int nrp) { return ss3_off(nrp) + (long long)HT * nrp * 4; }
-  __host__ __device__ static long long frame_bytes(int nrp) { return ssl_off(nrp) + (long long)HT * nrp * 4; }
-  // step area: h0 fp32 | y0 split | ss0 [NRP][HT] | x [B*T][A] fp32
-  __host__ __device__ static long long step_x_off(int nrp) { return 2 * hb(nrp) + (long long)HT * nrp * 4; }
+  __host__ __device__ static long long ss_bytes(int nrp) { return (long long)HT * (nrp / 16) * 128; }
+  __host__ __device__ static long long ss3_off(int nrp) { return ss2_off(nrp) + ss_bytes(nrp); }
+  __host__ __device__ static long long ssl_off(int nrp) { return ss3_off(nrp) + ss_bytes(nrp); }
+  __host__ __device__ static long long frame_bytes(int nrp) { return ssl_off(nrp) + ss_bytes(nrp); }
+  // step area: h0 fp32 | y0 split | ss0 [HT][RT][32] | x [B*T][A] fp32
+  __host__ __device__ static long long step_x_off(int nrp) { return 2 * hb(nrp) + ss_bytes(nrp); }
 };
 
 // byte offset of the 4-float piece (row r, columns c .. c+3; c % 4 == 0) of a fragment-major fp32 buffer
@@ -245,6 +247,9 @@ struct Ctx {
 
 __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ float bload32f(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 __device__ __forceinline__ f32x4 as_f4(u32x4 v) { return __builtin_bit_cast(f32x4, v); }
 __device__ __forceinline__ u32x4 as_u4(f32x4 v) { return __builtin_bit_cast(u32x4, v); }
@@ -395,7 +400,7 @@ struct Desc {
   const float* a;                      // split operand frame
   float* out; const float* res; float* part;
   float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
-  const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][NRP]
+  const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][RT][32]
   int ntask, tiles, kind, nt;          // nt: 16-column tiles per task (QKV, gate/up: a pair; wide tasks: NTW)
   int rgs;                             // row groups: task t = tile t % tiles over row-tile group t / tiles
   int pk;                              // placement kind (Params::pl)
@@ -405,27 +410,41 @@ struct Desc {
   int mod_off, mod_off2;
 };
 
+// Position of stage g of a launch: step s, layer l and kind k (ST_QKV .. ST_DOWN), or l == L for the step
+// tail; the launch's first stage (g = 0) is the tail of step -1. Stepped forward by increments only.
+struct StagePos {
+  int g, s, l, k;
+};
+__device__ __forceinline__ void advance(StagePos& q, int L) {
+  ++q.g;
+  if (q.l == L) {
+    q.l = 0;
+    q.k = 0;
+    ++q.s;
+  } else if (++q.k == STAGES_PER_LAYER) {
+    q.k = 0;
+    ++q.l;
+  }
+}
+
 template <class S>
-__device__ __forceinline__ Desc describe(Ctx<S>& c, int g) {
+__device__ __forceinline__ Desc describe(Ctx<S>& c, const StagePos& q) {
   CP& p = c.p;
   Desc d;
-  d.first = g == 0;
+  d.first = q.g == 0;
   d.last = false;
   d.w = nullptr; d.wstride = 0; d.a = nullptr; d.out = nullptr; d.res = nullptr; d.part = nullptr;
   d.sc = nullptr; d.sc2 = nullptr;
   d.yout = nullptr; d.ssout = nullptr; d.ssin = nullptr; d.shs = nullptr;
   d.ntask = 0; d.tiles = 1; d.kind = K_QKV; d.nt = 1; d.mod_off = 0; d.mod_off2 = 0; d.rgs = 1; d.pk = PL_TIN;
-  if (g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
-  const int per_step = STAGES_PER_LAYER * p.L + 1;
-  const int h = g - 1;
-  d.s = h / per_step;
-  const int j = h - d.s * per_step;
-  if (j == STAGES_PER_LAYER * p.L) {
+  if (q.g == 0) { d.st = ST_TAIL; d.s = 0; d.l = 0; return d; }
+  d.s = q.s;
+  if (q.l == p.L) {
     d.st = ST_TAIL; d.l = p.L - 1; d.last = d.s + 1 == p.n_steps;
     return d;
   }
-  d.l = j / STAGES_PER_LAYER;
-  d.st = j - d.l * STAGES_PER_LAYER;
+  d.l = q.l;
+  d.st = q.k;
   const int NRP = p.NRP, l = d.l;
   char* fr = c.frame(d.s, l);
   // AdaRMS slices of a layer's mods row (src/mk_expert.py:302-426): [scale | shift | gate] for self-attention,
@@ -511,10 +530,13 @@ __device__ __forceinline__ void dma_task_w(Ctx<S>& c, const Desc& d, int t, char
 //     in split order and applies K_RES (down_reduce).
 // K (= H per task) is split over the 4 waves; the wave partials are summed through LDS.
 
-// byte offset of the sum of squares of (row, 16-column tile t) in an [NRP][HT] array
-__device__ __forceinline__ uint32_t ss_slot(int row, int t, int HT) {
-  return (uint32_t)((row * HT + (t & 3) * (HT / 4) + (t >> 2)) * 4);
+// byte offset of the sum of squares of (row, 16-column tile t) in a [HT][RT][32] array (one 128-byte line
+// per (tile, row tile), written by the one task that computes that tile of those rows)
+__device__ __forceinline__ uint32_t ss_slot(int row, int t, int RT) {
+  return (uint32_t)(((t * RT + (row >> 4)) * 32 + (row & 15)) * 4);
 }
+// distance in bytes between the sums of squares of tiles t and t + 4 (the tiles one wave of a consumer sums)
+__device__ __forceinline__ uint32_t ss_tile4(int RT) { return (uint32_t)(4 * RT * 128); }
 
 // residual epilogue of one 4-column piece: h = res + v * gate; stores h, y = h (1 + next scale) and the
 // piece's share of the row's sum of squares (lanes L, L^16, L^32, L^48 hold one row's 16 columns)
@@ -527,7 +549,7 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
   if (st_h4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)))) range_error(c.p.bar);
   float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
   ss = xor32_sum(xor16_sum(ss));
-  if (L < 16) st_sc1_b32(d.ssout, ss_slot(row, tile, S::HT), __float_as_uint(ss));
+  if (L < 16) st_sc1_b32(d.ssout, ss_slot(row, tile, c.RT), __float_as_uint(ss));
 }
 
 // q/k epilogue of one row: xa, xb = columns d0 .. d0+3 and d0+32 .. d0+35 of head hd (kind 0 = q, 1 = k).
@@ -649,6 +671,15 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   const uint32_t vlane = (uint32_t)c.lane * 16;
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
   char* red = c.smem + p.lds_red;             // [wave][RB + 1][2][64 lanes] x 16 bytes
+  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`: loaded first, so that
+  // waiting for them never waits for the operand loads
+  float ssv[S::HT / 4];
+  if (ada) {
+    const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
+    const uint32_t so = ss_slot(min(rt0 * 16 + c.lane, NRP - 1), c.wave, RT);
+#pragma unroll
+    for (int i = 0; i < S::HT / 4; ++i) ssv[i] = bload32f(rs_, so, (uint32_t)i * ss_tile4(RT));
+  }
   // fp16 operand fragments (the first 1 KB of each 2 KB block), k-block major, in the order the MFMAs use
   // them: the MFMAs of the first k-blocks start while the later blocks are still arriving
   f16x8 a[NRT][KPW];
@@ -658,22 +689,16 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
     for (int rt = 0; rt < NRT; ++rt)
       a[rt][i] = __builtin_bit_cast(f16x8, bload(ra, vlane, (uint32_t)(((kb0 + c.wave + NWAVES * i) * RT + rt0 + rt) * 2048)));
   f16x8 sh[KPW];  // the fp16 shift fragments of this wave's k-blocks (rows = samples)
-  u32x4 ssv[S::HT / 16];  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`
-  if (ada) {
-    const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
-    const uint32_t so = (uint32_t)((min(rt0 * 16 + c.lane, NRP - 1) * S::HT + c.wave * (S::HT / 4)) * 4);
-#pragma unroll
-    for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
-  } else {
+  if (!ada) {
 #pragma unroll
     for (int i = 0; i < KPW; ++i) sh[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
   const int erow = epi_row(rt0, NRT, c.tid), eL = c.tid & 63;
   epre = epi_const(c, d, qkind, qj, tile, erow, eL);
   if (d.kind == K_RES) epre.c0 = as_f4(ld16((const char*)d.res + fpiece(erow, tile * 16 + 4 * (eL >> 4), c.RT)));
-  // The staged weights and modulation slices (the prefetch's LDS DMAs, issued before every load above) have
-  // landed once no more than the activation loads are outstanding; the activations are waited for where the
-  // MFMAs use them.
+  // The staged weights and modulation slices (the prefetch's LDS DMAs, issued before every load above) and
+  // the sums of squares have landed once no more than the activation loads are outstanding; the activations
+  // are waited for where the MFMAs use them.
   wait_vm_le<NRT * KPW>();
   exec_barrier();
   if (ada) {
@@ -702,10 +727,7 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   if (ada) {
     float ssp = 0.f;
 #pragma unroll
-    for (int i = 0; i < S::HT / 16; ++i) {
-      const f32x4 x = as_f4(ssv[i]);
-      ssp += (x[0] + x[1]) + (x[2] + x[3]);
-    }
+    for (int i = 0; i < S::HT / 16; ++i) ssp += (ssv[4 * i] + ssv[4 * i + 1]) + (ssv[4 * i + 2] + ssv[4 * i + 3]);
     ssw[c.wave * 64 + c.lane] = ssp;
   }
   // cross-wave reduction through LDS (the shift tile at slot RB)
@@ -1614,31 +1636,32 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) accb[nt][i & 1] = mfma16h(wf[nt][i], sh[i], accb[nt][i & 1]);
     MKX_TR(c, 14);
-    // every out-projection tile of the row group holding the query rows (their sums of squares share lines)
+    // every out-projection task of the row group holding the query rows
     {
       const int rg = row_group_of(rq, RT, rgo);
       const int to = S::HT / p.nt_o;  // out-projection tasks per row group
       flag_wait(bc, F_O, to, [&](int i) { return rg * to + i; }, (unsigned long long)g);
     }
     MKX_TR(c, 0);
-    // 1a. operands: y2 fragments (fp16) of the query rows, sums of squares
+    // 1a. operands: sums of squares (first, so that waiting for them never waits for the query rows), then
+    // the y2 fragments (fp16) of the query rows
     f16x8 yh[KPW];
-    u32x4 ssv[S::HT / 16];
+    float ssv[S::HT / 4];
     {
+      const __amdgpu_buffer_rsrc_t rs_ = rsrc(ss2);
+      const uint32_t so = ss_slot(rq * 16 + (c.lane & 15), c.wave, RT);
+#pragma unroll
+      for (int i = 0; i < S::HT / 4; ++i) ssv[i] = bload32f(rs_, so, (uint32_t)i * ss_tile4(RT));
       const __amdgpu_buffer_rsrc_t ry = rsrc(y2);
 #pragma unroll
       for (int i = 0; i < KPW; ++i) {
         const int kb = c.wave + NWAVES * i;
         yh[i] = __builtin_bit_cast(f16x8, bload(ry, vlane, (uint32_t)((kb * RT + rq) * 2048)));
       }
-      const __amdgpu_buffer_rsrc_t rs_ = rsrc(ss2);
-      const uint32_t so = (uint32_t)(((rq * 16 + (c.lane & 15)) * S::HT + c.wave * (S::HT / 4)) * 4);
-#pragma unroll
-      for (int i = 0; i < S::HT / 16; ++i) ssv[i] = bload(rs_, so, (uint32_t)(i * 16));
     }
-    // Everything but the query rows and their sums of squares has landed (the prefetched K/V chunks were
-    // issued before them); the query rows are waited for where the MFMAs use them.
-    wait_vm_le<KPW + S::HT / 16>();
+    // Everything but the query rows has landed (the prefetched K/V chunks were issued before them); the
+    // query rows are waited for where the MFMAs use them.
+    wait_vm_le<KPW>();
     __builtin_amdgcn_sched_barrier(0);  // every query-row load is issued before the first MFMA
     MKX_TR(c, 3);
     {
@@ -1652,10 +1675,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
         for (int nt = 0; nt < 4; ++nt) acc[nt][i & 1] = mfma16h(wf[nt][i], yh[i], acc[nt][i & 1]);
       float ssp = 0.f;
 #pragma unroll
-      for (int i = 0; i < S::HT / 16; ++i) {
-        const f32x4 x = as_f4(ssv[i]);
-        ssp += (x[0] + x[1]) + (x[2] + x[3]);
-      }
+      for (int i = 0; i < S::HT / 16; ++i) ssp += (ssv[4 * i] + ssv[4 * i + 1]) + (ssv[4 * i + 2] + ssv[4 * i + 3]);
       if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
@@ -1950,7 +1970,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
         if (st_h4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc))) range_error(p.bar);
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
         ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
-        if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, 2 * t + (q >> 2), S::HT), __float_as_uint(ss));
+        if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, 2 * t + (q >> 2), c.RT), __float_as_uint(ss));
       }
     }
     flag_publish(bc, inproj ? F_TAIL_IN : F_TAIL_OUT, inproj ? t : a_out, (unsigned long long)g + 1);
@@ -2028,6 +2048,41 @@ __device__ __forceinline__ void prefetch_shifts(Ctx<S>& c, const Desc& d) {
   c.dn = NWAVES;
 }
 
+// Stage kinds in which this workgroup has a task: bit st (ST_QKV .. ST_DOWN, the down projection's
+// reducers included; ST_TAIL: a step tail with an in-projection or output task), bit TAIL_LAST_BIT: the
+// launch's last step tail (output tasks only). Workgroup 0 takes part in every stage, so that its stage
+// boundary timestamps cover all of them.
+constexpr int TAIL_LAST_BIT = 8;
+template <class S>
+__device__ __forceinline__ unsigned task_mask(Ctx<S>& c) {
+  CP& p = c.p;
+  if (c.wg == 0) return ~0u;
+  const int nattn = attn_count(p.Mqp / 16, p.B * S::NH), nout = (p.A + TAIL_AC - 1) / TAIL_AC;
+  unsigned m = 0;
+  if (task_first(c, PL_QKV) < 6 * S::NH * p.rgs_qkv) m |= 1u << ST_QKV;
+  if (task_first(c, PL_SA) < nattn) m |= 1u << ST_SA;
+  if (task_first(c, PL_O) < (S::HT / p.nt_o) * p.rgs_o) m |= 1u << ST_O;
+  if (task_first(c, PL_CA) < nattn) m |= 1u << ST_CA;
+  if (task_first(c, PL_CAO) < (S::HT / p.nt_cao) * p.rgs_cao) m |= 1u << ST_CAO;
+  if (task_first(c, PL_GU) < S::IT) m |= 1u << ST_GU;
+  if (task_first(c, PL_DOWN) < (S::HT / p.nt_down) * S::SK || task_first(c, PL_RED) < S::NRED) m |= 1u << ST_DOWN;
+  const bool tout = task_first(c, PL_TOUT) < nout;
+  if (tout || task_first(c, PL_TIN) < S::NIN) m |= 1u << ST_TAIL;
+  if (tout) m |= 1u << TAIL_LAST_BIT;
+  return m;
+}
+
+// the first stage after q in which this workgroup has a task (g = total if none)
+__device__ __forceinline__ StagePos next_stage(unsigned mask, StagePos q, int total, int L) {
+  while (true) {
+    advance(q, L);
+    if (q.g >= total) break;
+    const int bit = q.l == L ? (q.g == total - 1 ? TAIL_LAST_BIT : ST_TAIL) : q.k;
+    if ((mask >> bit) & 1u) break;
+  }
+  return q;
+}
+
 // ------------------------------------------------------------------------------------------------
 template <int H, int I, bool W8>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
@@ -2064,8 +2119,12 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   if (p.profile && c.wg == 0 && c.tid == 0) p.prof[0] = clock100() * 10;
 
   const int total = 1 + p.n_steps * (STAGES_PER_LAYER * p.L + 1);
-  Desc cur = describe(c, 0);
-  for (int g = 0; g < total; ++g) {
+  // a workgroup goes from each of its stages straight to the next stage in which it has a task (its weight
+  // or K/V prefetch for that task is issued right away), passing over the stages between
+  const unsigned mask = task_mask(c);
+  StagePos pos{0, -1, p.L, 0};
+  Desc cur = describe(c, pos);
+  for (int g = 0; g < total;) {
     {
       // parameters are re-read from the kernarg segment in every stage instead of being kept live (and
       // spilled) across the whole loop
@@ -2085,33 +2144,33 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
     }
     c.ep = (unsigned)g;
     MKX_TR(c, 4);
+    pos = next_stage(mask, pos, total, p.L);
+    const int gn = pos.g;
     if (g == 0) {
-      // the per-launch copies (V^T of the caches, split shifts) are read by every later stage: the launch's
-      // one grid barrier; the next stage's constant operands are DMA'd while it completes
+      // the per-launch copies (V^T of the caches, split shifts) are read by every later stage (prefetches
+      // included): the launch's one grid barrier
       wait_vm0();
       bar_arrive(bc, 1);
-      cur = describe(c, 1);
-      if (c.wave != 0) prefetch(c, cur, s_ks);
       bar_wait(bc, 1);
-      // the split shifts were written by every workgroup in this first stage: staged only after the barrier
-      prefetch_shifts(c, cur);
     } else {
       __syncthreads();  // this stage's LDS is no longer read: the next stage's prefetch may overwrite it
-      if (g + 1 < total) {
-        cur = describe(c, g + 1);
-        // waves 1-3 issue the prefetch; wave 0, which polls the ready epochs, keeps no loads in flight
-        if (c.wave != 0) {
-          prefetch(c, cur, s_ks);
-          prefetch_shifts(c, cur);
-        }
+    }
+    if (gn < total) {
+      cur = describe(c, pos);
+      // waves 1-3 issue the prefetch; wave 0, which polls the ready epochs, keeps no loads in flight
+      if (c.wave != 0) {
+        prefetch(c, cur, s_ks);
+        prefetch_shifts(c, cur);
       }
     }
-    c.ep = (unsigned)(g + 1);
+    c.ep = (unsigned)gn;
     MKX_TR(c, 6);
+    // (workgroup 0 has no stage to pass over: gn = g + 1)
     if (p.profile && c.wg == 0 && c.tid == 0) p.prof[g + 1] = clock100() * 10;
+    g = gn;
   }
-  // every workgroup has passed every stage boundary: count them like barrier arrivals (the arrival counters
-  // then read (gen + total) x workgroups, the state the next launch's barrier expects)
+  // every workgroup has passed (or passed over) every stage boundary: count them like barrier arrivals (the
+  // arrival counters then read (gen + total) x workgroups, the state the next launch's barrier expects)
   wait_vm0();
   __syncthreads();
   if (c.tid == 0) __hip_atomic_fetch_add(&p.bar->arrive[bc.x][0], (unsigned long long)(total - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
