@@ -140,10 +140,10 @@ struct Shape {
   // frame layout (bytes), buffers of NRP rows; HB = NRP * H * 4:
   //   qs, ks: split q / k (roped, not normed) | vt: split V^T blocks per (sample, head) (2 HB) | ysa split |
   //   h2 fp32 | y2 split | yca split | h3 fp32 | y3 split | g split (I columns) | hl fp32 | yl split |
-  //   part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ss2, ss3, ssl [HT][RT][32]
-  // (sums of squares of h per 16-column tile t and row: one 128-byte line per (tile, 16-row tile), its first
-  // 16 floats used, so that each line has exactly one writer: several producers writing 4-byte pieces of one
-  // line at once take twice as long to be acknowledged)
+  //   part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ss2, ss3, ssl [RT][HT / 2][16][2]
+  // (sums of squares of h per 16-column tile t and row: one 128-byte line per (16-row tile, tile pair), so
+  // that a line has at most two writers: many producers writing 4-byte pieces of one line at once take
+  // twice as long to be acknowledged)
   __host__ __device__ static long long hb(int nrp) { return (long long)nrp * H * 4; }
   __host__ __device__ static long long qs_off(int) { return 0; }
   __host__ __device__ static long long ks_off(int nrp) { return hb(nrp); }
@@ -160,11 +160,11 @@ struct Shape {
   __host__ __device__ static long long part_off(int nrp) { return (12 + SK) * hb(nrp); }
   __host__ __device__ static long long ssqk_off(int nrp) { return (12 + 2 * SK) * hb(nrp); }
   __host__ __device__ static long long ss2_off(int nrp) { return ssqk_off(nrp) + 4LL * NH * nrp * 4; }
-  __host__ __device__ static long long ss_bytes(int nrp) { return (long long)HT * (nrp / 16) * 128; }
+  __host__ __device__ static long long ss_bytes(int nrp) { return (long long)HT * nrp * 4; }
   __host__ __device__ static long long ss3_off(int nrp) { return ss2_off(nrp) + ss_bytes(nrp); }
   __host__ __device__ static long long ssl_off(int nrp) { return ss3_off(nrp) + ss_bytes(nrp); }
   __host__ __device__ static long long frame_bytes(int nrp) { return ssl_off(nrp) + ss_bytes(nrp); }
-  // step area: h0 fp32 | y0 split | ss0 [HT][RT][32] | x [B*T][A] fp32
+  // step area: h0 fp32 | y0 split | ss0 [RT][HT / 2][16][2] | x [B*T][A] fp32
   __host__ __device__ static long long step_x_off(int nrp) { return 2 * hb(nrp) + ss_bytes(nrp); }
 };
 
@@ -248,8 +248,21 @@ struct Ctx {
 __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
-__device__ __forceinline__ float bload32f(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+}
+// sum of N pairs of floats, pairwise
+template <int N>
+__device__ __forceinline__ float ss_pairs_sum(const u32x2 (&v)[N]) {
+  float p[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = __uint_as_float(v[i][0]) + __uint_as_float(v[i][1]);
+#pragma unroll
+  for (int w = 1; w < N; w *= 2)
+#pragma unroll
+    for (int i = 0; i + w < N; i += 2 * w) p[i] += p[i + w];
+  return p[0];
 }
 __device__ __forceinline__ f32x4 as_f4(u32x4 v) { return __builtin_bit_cast(f32x4, v); }
 __device__ __forceinline__ u32x4 as_u4(f32x4 v) { return __builtin_bit_cast(u32x4, v); }
@@ -400,7 +413,7 @@ struct Desc {
   const float* a;                      // split operand frame
   float* out; const float* res; float* part;
   float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
-  const float* ssin;                   // AdaRMS stages: the operand's sums of squares [HT][RT][32]
+  const float* ssin;                   // AdaRMS stages: the operand's sums of squares [RT][HT / 2][16][2]
   int ntask, tiles, kind, nt;          // nt: 16-column tiles per task (QKV, gate/up: a pair; wide tasks: NTW)
   int rgs;                             // row groups: task t = tile t % tiles over row-tile group t / tiles
   int pk;                              // placement kind (Params::pl)
@@ -530,13 +543,13 @@ __device__ __forceinline__ void dma_task_w(Ctx<S>& c, const Desc& d, int t, char
 //     in split order and applies K_RES (down_reduce).
 // K (= H per task) is split over the 4 waves; the wave partials are summed through LDS.
 
-// byte offset of the sum of squares of (row, 16-column tile t) in a [HT][RT][32] array (one 128-byte line
-// per (tile, row tile), written by the one task that computes that tile of those rows)
-__device__ __forceinline__ uint32_t ss_slot(int row, int t, int RT) {
-  return (uint32_t)(((t * RT + (row >> 4)) * 32 + (row & 15)) * 4);
+// byte offset of the sum of squares of (row, 16-column tile t) in a [RT][HT / 2][16][2] array: one 128-byte
+// line per (row tile, tile pair), written by the tasks that compute those two tiles of those rows; a row's
+// two tiles of a pair are one 8-byte piece
+template <int HT>
+__device__ __forceinline__ uint32_t ss_slot(int row, int t) {
+  return (uint32_t)(((((row >> 4) * (HT / 2) + (t >> 1)) * 16 + (row & 15)) * 2 + (t & 1)) * 4);
 }
-// distance in bytes between the sums of squares of tiles t and t + 4 (the tiles one wave of a consumer sums)
-__device__ __forceinline__ uint32_t ss_tile4(int RT) { return (uint32_t)(4 * RT * 128); }
 
 // residual epilogue of one 4-column piece: h = res + v * gate; stores h, y = h (1 + next scale) and the
 // piece's share of the row's sum of squares (lanes L, L^16, L^32, L^48 hold one row's 16 columns)
@@ -549,7 +562,7 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
   if (st_h4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)))) range_error(c.p.bar);
   float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
   ss = xor32_sum(xor16_sum(ss));
-  if (L < 16) st_sc1_b32(d.ssout, ss_slot(row, tile, c.RT), __float_as_uint(ss));
+  if (L < 16) st_sc1_b32(d.ssout, ss_slot<S::HT>(row, tile), __float_as_uint(ss));
 }
 
 // q/k epilogue of one row: xa, xb = columns d0 .. d0+3 and d0+32 .. d0+35 of head hd (kind 0 = q, 1 = k).
@@ -671,14 +684,16 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   const uint32_t vlane = (uint32_t)c.lane * 16;
   float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][64 pass rows] partial sums of squares
   char* red = c.smem + p.lds_red;             // [wave][RB + 1][2][64 lanes] x 16 bytes
-  // this wave's share (tiles wave + 4i) of the sums of squares of pass row `lane`: loaded first, so that
-  // waiting for them never waits for the operand loads
-  float ssv[S::HT / 4];
+  // this wave's share (tiles wave HT / 4 .. + HT / 4 - 1, as HT / 8 pairs) of the sums of squares of pass row
+  // `lane` (the lanes past the pass rows repeat its first row tile): loaded first, so that waiting for them
+  // never waits for the operand loads
+  u32x2 ssv[S::HT / 8];
   if (ada) {
     const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
-    const uint32_t so = ss_slot(min(rt0 * 16 + c.lane, NRP - 1), c.wave, RT);
+    const int prow = c.lane < NRT * 16 ? c.lane : (c.lane & 15);
+    const uint32_t so = ss_slot<S::HT>(min(rt0 * 16 + prow, NRP - 1), c.wave * (S::HT / 4));
 #pragma unroll
-    for (int i = 0; i < S::HT / 4; ++i) ssv[i] = bload32f(rs_, so, (uint32_t)i * ss_tile4(RT));
+    for (int i = 0; i < S::HT / 8; ++i) ssv[i] = bload8(rs_, so, (uint32_t)i * 128);
   }
   // fp16 operand fragments (the first 1 KB of each 2 KB block), k-block major, in the order the MFMAs use
   // them: the MFMAs of the first k-blocks start while the later blocks are still arriving
@@ -724,12 +739,7 @@ __device__ __forceinline__ void gemm_pass(Ctx<S>& c, const Desc& d, int rt0, int
   if (vtask) gemm_mma<S, NRT, 2, 2, 2, true, true>(acc, accs, a, sh, wl, c.wave, c.lane);
   else if (d.nt == 2) gemm_mma<S, NRT, 2, 2, 2, false, true>(acc, accs, a, sh, wl, c.wave, c.lane);
   else gemm_mma<S, NRT, 1, 2, 2, false, false>(acc, accs, a, sh, wl, c.wave, c.lane);
-  if (ada) {
-    float ssp = 0.f;
-#pragma unroll
-    for (int i = 0; i < S::HT / 16; ++i) ssp += (ssv[4 * i] + ssv[4 * i + 1]) + (ssv[4 * i + 2] + ssv[4 * i + 3]);
-    ssw[c.wave * 64 + c.lane] = ssp;
-  }
+  if (ada) ssw[c.wave * 64 + c.lane] = ss_pairs_sum<S::HT / 8>(ssv);
   // cross-wave reduction through LDS (the shift tile at slot RB)
 #pragma unroll
   for (int rt = 0; rt <= NRT; ++rt)
@@ -1646,12 +1656,12 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     // 1a. operands: sums of squares (first, so that waiting for them never waits for the query rows), then
     // the y2 fragments (fp16) of the query rows
     f16x8 yh[KPW];
-    float ssv[S::HT / 4];
+    u32x2 ssv[S::HT / 8];
     {
       const __amdgpu_buffer_rsrc_t rs_ = rsrc(ss2);
-      const uint32_t so = ss_slot(rq * 16 + (c.lane & 15), c.wave, RT);
+      const uint32_t so = ss_slot<S::HT>(rq * 16 + (c.lane & 15), c.wave * (S::HT / 4));
 #pragma unroll
-      for (int i = 0; i < S::HT / 4; ++i) ssv[i] = bload32f(rs_, so, (uint32_t)i * ss_tile4(RT));
+      for (int i = 0; i < S::HT / 8; ++i) ssv[i] = bload8(rs_, so, (uint32_t)i * 128);
       const __amdgpu_buffer_rsrc_t ry = rsrc(y2);
 #pragma unroll
       for (int i = 0; i < KPW; ++i) {
@@ -1673,9 +1683,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       for (int i = 0; i < KPW; ++i)
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) acc[nt][i & 1] = mfma16h(wf[nt][i], yh[i], acc[nt][i & 1]);
-      float ssp = 0.f;
-#pragma unroll
-      for (int i = 0; i < S::HT / 16; ++i) ssp += (ssv[4 * i] + ssv[4 * i + 1]) + (ssv[4 * i + 2] + ssv[4 * i + 3]);
+      const float ssp = ss_pairs_sum<S::HT / 8>(ssv);
       if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
@@ -1970,7 +1978,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
         if (st_h4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc))) range_error(p.bar);
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
         ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
-        if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot(row, 2 * t + (q >> 2), c.RT), __float_as_uint(ss));
+        if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot<S::HT>(row, 2 * t + (q >> 2)), __float_as_uint(ss));
       }
     }
     flag_publish(bc, inproj ? F_TAIL_IN : F_TAIL_OUT, inproj ? t : a_out, (unsigned long long)g + 1);
