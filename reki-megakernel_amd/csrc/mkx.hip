@@ -110,11 +110,11 @@ int lds_of(int H, int I) {
 
 // the shape constants the host's task layout depends on
 struct ShapeK {
-  int HT, IT, SK, NH, NIN, NRED, NTW, W_NARROW, RED_NARROW, W_WIDE, RED_WIDE, SMALL;
+  int HT, IT, SK, NH, NIN, NTW, W_NARROW, RED_NARROW, W_WIDE, RED_WIDE, SMALL;
 };
 template <class S>
 ShapeK shape_k() {
-  return {S::HT, S::IT, S::SK, S::NH, S::NIN, S::NRED, S::NTW, S::W_NARROW, S::RED_NARROW, S::W_WIDE, S::RED_WIDE, S::SMALL};
+  return {S::HT, S::IT, S::SK, S::NH, S::NIN, S::NTW, S::W_NARROW, S::RED_NARROW, S::W_WIDE, S::RED_WIDE, S::SMALL};
 }
 ShapeK shape_k(int H, int I, bool w8) {
   if (H == 768 && I == 3072) return w8 ? shape_k<Shape<768, 3072, true>>() : shape_k<Shape<768, 3072, false>>();
@@ -134,7 +134,7 @@ ShapeK shape_k(int H, int I, bool w8) {
 // and step-tail tasks at the top.
 struct Layout {
   int pl[PL_KINDS];
-  int rgs_qkv, rgs_o, rgs_cao, nt_o, nt_cao, nt_down, lds_red, lds_mods;
+  int rgs_qkv, rgs_o, rgs_cao, nt_o, nt_cao, nt_down, lds_red, lds_mods, tpr, nred;
   bool disjoint;
 };
 Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A) {
@@ -143,15 +143,15 @@ Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A)
   const bool wide = k.NTW > 1 && k.W_WIDE + std::max(k.RED_WIDE, k.RED_NARROW) + mods <= k.SMALL;
   const int nt = wide ? k.NTW : 1;
   auto clampi = [](int v, int lo, int hi) { return std::max(lo, std::min(hi, v)); };
-  const int ndown_d = (k.HT / nt) * k.SK;
-  L.disjoint = k.IT + ndown_d <= G && 6 * k.NH + std::max(k.NRED, nattn) <= G;
+  const int ndown_d = (k.HT / nt) * k.SK, nred_d = k.HT / nt;
+  L.disjoint = k.IT + ndown_d <= G && 6 * k.NH + std::max(nred_d, nattn) <= G;
   int cnt[PL_KINDS] = {};
   if (L.disjoint) {
     L.nt_o = L.nt_cao = L.nt_down = nt;
     L.rgs_cao = clampi(ndown_d / (k.HT / nt), 1, RT);
     // QKV leaves room for the self-attention tasks and the reducers; the out-projection sits inside the QKV
     // range and leaves room for both attention stages and the CA out-projection
-    L.rgs_qkv = clampi((G - std::max(k.NRED, nattn)) / (6 * k.NH), 1, RT);
+    L.rgs_qkv = clampi((G - std::max(nred_d, nattn)) / (6 * k.NH), 1, RT);
     const int ncao = (k.HT / nt) * L.rgs_cao;
     L.rgs_o = clampi(std::min(6 * k.NH * L.rgs_qkv, G - 2 * nattn - ncao) / (k.HT / nt), 1, RT);
   } else {
@@ -165,7 +165,12 @@ Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A)
   cnt[PL_CAO] = (k.HT / L.nt_cao) * L.rgs_cao;
   cnt[PL_GU] = k.IT;
   cnt[PL_DOWN] = (k.HT / L.nt_down) * k.SK;
-  cnt[PL_RED] = k.NRED;
+  // reducers: with the disjoint layout, one per wide task's tiles (their loads then equal a wide task's
+  // operand share, and they fit beside the QKV tasks); otherwise one per 16-column tile, so that batched
+  // shapes, whose reductions cover many row tiles, spread them over more workgroups
+  L.tpr = L.disjoint ? nt : 1;
+  L.nred = k.HT / L.tpr;
+  cnt[PL_RED] = L.nred;
   cnt[PL_TIN] = k.NIN;
   cnt[PL_TOUT] = nout;
   const bool any_wide = L.nt_o > 1 || L.nt_cao > 1 || L.nt_down > 1;
@@ -205,7 +210,7 @@ Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A)
     L.pl[PL_SA] = md(G - nattn);
     L.pl[PL_CA] = md(G - 2 * nattn);
     L.pl[PL_TIN] = md(G - k.NIN);
-    L.pl[PL_RED] = L.pl[PL_TOUT] = md(G - k.NIN - k.NRED);
+    L.pl[PL_RED] = L.pl[PL_TOUT] = md(G - k.NIN - L.nred);
   }
   return L;
 }
@@ -507,11 +512,12 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   const Layout lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A);
   {
     // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes): gate/up on every CA out-projection
-    // task, an out-projection task on every head of its rows, cross-attention on every out-projection tile
-    // of a row group, self-attention on the QKV tasks of its head
+    // task, an out-projection task on every head of its rows; and on at most 64 (one load per poll) where
+    // it waits on every out-projection task of a row group (cross-attention) or on the QKV tasks of its
+    // head (self-attention)
     const int RTn = NRP / 16, NH = H / 64;
     if ((sk.HT / lay.nt_cao) * lay.rgs_cao > 256 || ((RTn + lay.rgs_o - 1) / lay.rgs_o) * NH > 256 ||
-        ((RTn + lay.rgs_cao - 1) / lay.rgs_cao) * NH > 256 || sk.HT > 256 || 6 * lay.rgs_qkv > 256)
+        ((RTn + lay.rgs_cao - 1) / lay.rgs_cao) * NH > 256 || sk.HT > 64 || 6 * lay.rgs_qkv > 64)
       return fail(MKX_EUNSUPPORTED, "row grouping needs more than 256 ready epochs per wait");
     if (lay.lds_mods + a->B * 2 * H * 4 > sk.SMALL) return fail(MKX_EUNSUPPORTED, "GEMM LDS map does not fit");
   }
@@ -607,6 +613,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.rgs_qkv = lay.rgs_qkv; p.rgs_o = lay.rgs_o; p.rgs_cao = lay.rgs_cao;
   p.nt_o = lay.nt_o; p.nt_cao = lay.nt_cao; p.nt_down = lay.nt_down;
   p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
+  p.tpr = lay.tpr; p.nred = lay.nred;
   void* args[] = {&p};
   if (capturing) h->captured = 1;
   if (capturing || h->plain_launch) {

@@ -232,12 +232,11 @@ __device__ __forceinline__ void flag_publish(BarCtx& c, int kind, int idx, unsig
     __hip_atomic_store(&c.flags[((long long)kind * FLAG_MAX + idx) * FLAG_STRIDE], c.base + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// wait until flags[kind][idx(i)] >= base + e for every i < n (n <= 256): wave 0 polls them all, 64 per
+// wait until flags[kind][idx(i)] >= base + e for every i < n (n <= 64 NCH): wave 0 polls them all, 64 per
 // device-scope load, each poll one round trip; the workgroup proceeds together. Bounded like bar_wait (only
-// wave 0 polls, so only wave 0 tracks whether a wait gave up).
-template <class F>
+// wave 0 polls, so only wave 0 tracks whether a wait gave up). Waits whose n is bounded by 64 use NCH = 1.
+template <int NCH = 4, class F>
 __device__ __forceinline__ void flag_wait(BarCtx& c, int kind, int n, F idx, unsigned long long e) {
-  constexpr int NCH = 4;  // up to 256 flags: every poll reads them all with one load per 64
   if (threadIdx.x < 64 && !c.failed) {
     const unsigned long long t = c.base + e;
     const int lane = (int)threadIdx.x;

@@ -90,6 +90,7 @@ struct Params {
   int rgs_qkv, rgs_o, rgs_cao;  // row groups of the QKV, out-projection and CA out-projection stages
   int nt_o, nt_cao, nt_down;    // 16-column tiles per out-projection / CA out-projection / down task (1 or NTW)
   int lds_red, lds_mods;        // GEMM stages' LDS map: cross-wave reduction buffer, staged modulation slices
+  int tpr, nred;                // down-projection reducers: 16-column tiles per reducer, reducers (HT / tpr)
 };
 
 // placement kinds (Params::pl)
@@ -117,22 +118,25 @@ struct Shape {
   static constexpr int LDS = SMALL + SMALL_BYTES;
   static constexpr int RB_FIT = 144 / (KPW * 8);  // row tiles per GEMM pass held in VGPRs (hi + lo)
   // Fixed-role tasks at the end of a layer and of a step: NIN step-tail in-projection tasks (two 16-column
-  // tiles each) and NRED reducers, each of which sums the down projection's split-K partials of TPR output
-  // tiles. The host places them (Params::pl) on workgroups without a QKV task, so the next layer's QKV tasks
-  // never wait behind a reduction or a step tail on their own workgroup.
-  static constexpr int NIN = HT / 2, NRED = 16, TPR = HT / NRED;
+  // tiles each) and Params::nred reducers, each of which sums the down projection's split-K partials of
+  // Params::tpr output tiles (at most NTW; a reducer's loads, 5 KB per tile and row tile, are its critical
+  // path). The host places them (Params::pl).
+  static constexpr int NIN = HT / 2;
   static constexpr int RBMAX = RB_FIT > 3 ? 3 : RB_FIT;
-  // Wide tasks of the gated-residual and down-projection GEMMs: NTW 16-column tiles (a reducer's TPR tiles)
-  // per task where their weights fit 72 KB of LDS, else single tiles. A wide pass holds one row tile
-  // (residual stages) or up to RBMAX (down-projection splits); its accumulators are not split into hi / lo
-  // products (NTW x row tiles independent accumulators already keep consecutive MFMAs apart).
-  static constexpr int NTW = (TPR > 1 && TPR <= 4 && TPR * NKB * CH <= 72 * 1024) ? TPR : 1;
+  // Wide tasks of the gated-residual and down-projection GEMMs: NTW = HT / 16 16-column tiles per task where
+  // their weights fit 72 KB of LDS, else single tiles. A wide pass holds one row tile (residual stages) or up
+  // to RBMAX (down-projection splits); its accumulators are not split into hi / lo products (NTW x row tiles
+  // independent accumulators already keep consecutive MFMAs apart).
+  static constexpr int WT = HT / 16;
+  static constexpr int NTW = (WT > 1 && WT <= 4 && WT * NKB * CH <= 72 * 1024) ? WT : 1;
   // GEMM-stage LDS map, narrow (nt <= 2) and wide tasks: weight tiles from 0, then the cross-wave reduction
   // buffer ([wave][row tile][tile][64 lanes] x 16 bytes), then the staged modulation slices
   static constexpr int W_NARROW = 2 * NKB * CH, RED_NARROW = NWAVES * (RBMAX + 1) * 2 * 1024;
   static constexpr int W_WIDE = NTW * NKB * CH, RED_WIDE = NWAVES * RBMAX * NTW * 1024;
   static_assert(H % 256 == 0 && I % H == 0, "H must be a multiple of 256 and I a multiple of H");
-  static_assert(HT % NRED == 0 && TPR * SK <= 256, "each reducer waits on at most 256 partial tasks");
+  // waits on at most 64 ready epochs poll with one load (flag_wait<1>): the QKV, down-split, reducer,
+  // self-attention, cross-attention and step-tail waits
+  static_assert(HT <= 64 && 5 * SK <= 64, "waits polled with one load cover at most 64 flags");
   static_assert(KPW >= 1 && RBMAX >= 1, "tile does not fit registers");
   static_assert(NKB * CH * 2 <= WBUF_BYTES, "gate/up weight tile pair must fit the weight buffer");
   static_assert(NWAVES * (RBMAX + 1) * 2 * 1024 <= RED_BYTES, "cross-wave reduction must fit LDS");
@@ -809,7 +813,7 @@ __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, 
   const int NQT = c.p.Mqp / 16;
   if (d.st == ST_QKV) {
     // every column of its rows: the step tail's in-projection tasks, or the down projection's reducers
-    flag_wait(bc, d.l == 0 ? F_TAIL_IN : F_DOWN, d.l == 0 ? S::NIN : S::NRED, [](int i) { return i; }, (unsigned long long)g);
+    flag_wait<1>(bc, d.l == 0 ? F_TAIL_IN : F_DOWN, d.l == 0 ? S::NIN : c.p.nred, [](int i) { return i; }, (unsigned long long)g);
   } else if (d.st == ST_O || d.st == ST_CAO) {
     flag_wait(bc, d.st == ST_O ? F_SA : F_CA, (rt_hi - rt_lo) * S::NH, [&](int i) {
       const int rt = rt_lo + i / S::NH, hd = i % S::NH;
@@ -818,25 +822,28 @@ __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, 
   } else if (d.st == ST_GU) {
     flag_wait(bc, F_CAO, (S::HT / c.p.nt_cao) * c.p.rgs_cao, [](int i) { return i; }, (unsigned long long)g);
   } else {
-    flag_wait(bc, F_GU, S::HT, [&](int i) { return split * S::HT + i; }, (unsigned long long)g);
+    flag_wait<1>(bc, F_GU, S::HT, [&](int i) { return split * S::HT + i; }, (unsigned long long)g);
   }
 }
 
 // Down-projection reducer r: once the split tasks of its output tiles t0 .. t0 + TPR - 1 have published
 // their partial sums (SK per tile group of nt tiles: split task (split, group) is task split * tiles + group),
 // it adds them in split order and applies the gated residual (hl = h3 + gate * sum, with yl and the sums of
-// squares for the next AdaRMS), then publishes one ready epoch for the TPR tiles.
-template <class S>
+// squares for the next AdaRMS), then publishes one ready epoch for the TPR tiles. Instantiated for the two
+// reducer widths the host uses (Params::tpr: the wide tasks' NTW tiles, or one).
+template <class S, int TPR>
 __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc, int g, int r) {
-  const int RT = c.RT, t0 = r * S::TPR;
-  const int gpr = S::TPR / d.nt, g0 = t0 / d.nt;  // tile groups (split tasks per split) of this reducer
-  flag_wait(bc, F_DPART, S::SK * gpr, [&](int i) { return (i % S::SK) * d.tiles + g0 + i / S::SK; }, (unsigned long long)g);
+  constexpr int tpr = TPR;
+  const int RT = c.RT, t0 = r * tpr;
+  // the tile groups (split tasks per split) holding tiles t0 .. t0 + tpr - 1
+  const int g0 = t0 / d.nt, ng = (t0 + tpr - 1) / d.nt - g0 + 1;
+  flag_wait<1>(bc, F_DPART, S::SK * ng, [&](int i) { return (i % S::SK) * d.tiles + g0 + i / S::SK; }, (unsigned long long)g);
   wait_vm0();  // the staged gate and next AdaRMS scale (the prefetch's DMA) have landed
   __syncthreads();
   // one (tile, row tile) block of 64 items per wave and round (lanes L, L^16, L^32, L^48 hold one row);
   // the loads of RR rounds are issued together, so their latencies overlap
   constexpr int RR = 3;
-  const int nblk = S::TPR * RT;
+  const int nblk = tpr * RT;
   for (int b0 = c.wave; b0 < nblk; b0 += NWAVES * RR) {
     u32x4 xp[RR][S::SK];
     f32x4 res[RR];
@@ -1038,7 +1045,10 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   }
   if (d.kind == K_SPLIT) {
     const int r = task_first(c, PL_RED);
-    if (r < S::NRED) down_reduce(c, d, bc, g, r);
+    if (r < p.nred) {
+      if (p.tpr == S::NTW) down_reduce<S, S::NTW>(c, d, bc, g, r);
+      else down_reduce<S, 1>(c, d, bc, g, r);
+    }
   }
 }
 
@@ -1432,7 +1442,7 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
     // and V^T blocks of one head interleave row groups within cache lines
     {
       const int rgq = p.rgs_qkv;
-      flag_wait(bc, F_QKV, 6 * rgq, [&](int i) {
+      flag_wait<1>(bc, F_QKV, 6 * rgq, [&](int i) {
         const int k = i % 6, rg = i / 6;
         return rg * 6 * S::NH + (k >> 1) * 2 * S::NH + 2 * hd + (k & 1);
       }, (unsigned long long)g);
@@ -1650,7 +1660,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     {
       const int rg = row_group_of(rq, RT, rgo);
       const int to = S::HT / p.nt_o;  // out-projection tasks per row group
-      flag_wait(bc, F_O, to, [&](int i) { return rg * to + i; }, (unsigned long long)g);
+      flag_wait<1>(bc, F_O, to, [&](int i) { return rg * to + i; }, (unsigned long long)g);
     }
     MKX_TR(c, 0);
     // 1a. operands: sums of squares (first, so that waiting for them never waits for the query rows), then
@@ -1850,8 +1860,8 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     if (!d.first) {
       // every tile of the last layer's output (its reducers), and x of this step (the previous step tail's
       // output dims)
-      flag_wait(bc, F_DOWN, S::NRED, [](int i) { return i; }, (unsigned long long)g);
-      if (d.s > 0) flag_wait(bc, F_TAIL_OUT, nout, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
+      flag_wait<1>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
+      if (d.s > 0) flag_wait<1>(bc, F_TAIL_OUT, nout, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
     }
     // the staged final modulation rows and Wout rows (DMA'd by the prefetch) have landed
     wait_vm0();
@@ -2020,7 +2030,7 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
     }
     // gate and the next AdaRMS scale: the residual stages' tasks, and the down projection's reducers (its
     // split tasks only store partial sums)
-    if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && task_first(c, PL_RED) < S::NRED)) {
+    if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && task_first(c, PL_RED) < p.nred)) {
       for (int b = 0; b < p.B; ++b) {
         const float* mr = c.modrow(b, d.s);
         dma_f32(c, mb + b * 2 * S::H * 4, mr + d.mod_off, S::H);
@@ -2073,7 +2083,7 @@ __device__ __forceinline__ unsigned task_mask(Ctx<S>& c) {
   if (task_first(c, PL_CA) < nattn) m |= 1u << ST_CA;
   if (task_first(c, PL_CAO) < (S::HT / p.nt_cao) * p.rgs_cao) m |= 1u << ST_CAO;
   if (task_first(c, PL_GU) < S::IT) m |= 1u << ST_GU;
-  if (task_first(c, PL_DOWN) < (S::HT / p.nt_down) * S::SK || task_first(c, PL_RED) < S::NRED) m |= 1u << ST_DOWN;
+  if (task_first(c, PL_DOWN) < (S::HT / p.nt_down) * S::SK || task_first(c, PL_RED) < p.nred) m |= 1u << ST_DOWN;
   const bool tout = task_first(c, PL_TOUT) < nout;
   if (tout || task_first(c, PL_TIN) < S::NIN) m |= 1u << ST_TAIL;
   if (tout) m |= 1u << TAIL_LAST_BIT;
