@@ -23,16 +23,19 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "reki-megakernel_amd")]
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFS = 2500.0  # dense fp16 (and bf16) MFMA peak
-KERNEL_SOURCES = ("mkx_kernel.h", "mkx_device.h", "mkx.hip")
+KERNEL_SOURCES = ("mkx_kernel.h", "mkx_device.h", "mkx.hip", "mkx_mk768.hip", "mkx_mk1024.hip", "mkx_mk256.hip")
 
 
 def kernel_source_hash() -> str:
-    """sha256 of the megakernel's sources: ties a stored counter profile to the kernel it measured."""
+    """sha256 of the megakernel's sources and build options: ties a stored counter profile to the kernel it
+    measured."""
     import hashlib
     h = hashlib.sha256()
     for name in KERNEL_SOURCES:
         with open(os.path.join(ROOT, "reki-megakernel_amd", "csrc", name), "rb") as f:
             h.update(f.read())
+    with open(os.path.join(ROOT, "reki-megakernel_amd", "mkx", "_build.py"), "rb") as f:
+        h.update(f.read())
     return h.hexdigest()
 
 

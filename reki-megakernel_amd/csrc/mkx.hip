@@ -89,6 +89,21 @@ __global__ void xcc_probe(unsigned* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
+}  // namespace
+
+// The megakernel's instantiations live in their own translation units (mkx_mk768.hip, mkx_mk1024.hip,
+// mkx_mk256.hip), each compiled with its shape's code-generation options.
+namespace mkx {
+extern template __global__ void mkx_megakernel<768, 3072, false>(Params);
+extern template __global__ void mkx_megakernel<768, 3072, true>(Params);
+extern template __global__ void mkx_megakernel<1024, 4096, false>(Params);
+extern template __global__ void mkx_megakernel<1024, 4096, true>(Params);
+extern template __global__ void mkx_megakernel<256, 512, false>(Params);
+extern template __global__ void mkx_megakernel<256, 512, true>(Params);
+}  // namespace mkx
+
+namespace {
+
 template <int H, int I>
 const void* kernel_of(bool w8) {
   return w8 ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true>) : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false>);
