@@ -10,7 +10,8 @@
 //
 // Code layout: the kernel is one flat loop over stages, and each kind of stage (GEMM, self-attention,
 // cross-attention, tail) is a single inlined body driven by a runtime descriptor. The whole loop stays
-// resident in the instruction cache; a stage never waits on instruction fetch.
+// resident in the instruction cache; a stage never waits on instruction fetch. A workgroup passes over the
+// stages in which it has no task.
 //
 // Work decomposition for 256 CUs: every linear layer is cut into tasks of 16-column output tiles (or NTW of
 // them, for the out-projections and the down projection) over a group of row tiles, K = H per task (the down
@@ -24,9 +25,10 @@
 // Activation frames are fragment-major: a buffer of C columns and NRP rows is cut into 2 KB blocks
 // (32-column block kb, 16-row tile rt) at ((kb * RT + rt) * 2) KB, lane-major inside (lane = row % 16 +
 // 16 * (8-column group)). "fp32" buffers hold columns 0-3 of each 8-column group in the first 1 KB and 4-7
-// in the second; "split" buffers hold an MFMA operand fragment directly: 8 bf16 high parts per lane in the
-// first 1 KB and the 8 bf16 residuals in the second. A wave loads one split operand fragment (16 rows x 32
-// columns, hi and lo) with two contiguous 1 KB loads and feeds it to the MFMA unchanged.
+// in the second; GEMM operand buffers hold an MFMA operand fragment directly, 8 fp16 values per lane in the
+// first 1 KB, so that a wave loads one fragment (16 rows x 32 columns) with one contiguous 1 KB load and
+// feeds it to the MFMA unchanged; the attention operands (q, k, V^T) are split: 8 bf16 high parts per lane
+// in the first 1 KB and the 8 bf16 residuals in the second.
 //
 // Numerics: the linear layers run on fp16 MFMAs with fp32 accumulation. Weights are fp16 (bf16 weights are
 // packed as fp16 at handle creation, exactly within the fp16 range; fp8 e4m3 weights are decoded to fp16, also
@@ -70,9 +72,9 @@ struct Params {
   // V^T copies of the memory / cross-attention V caches, made once per launch:
   // [L][B][NH][PMP/32 or SPP/32 key blocks][4 d-slices][512 bf16]
   bf16_t* memvt; bf16_t* cavt; int SPP;
-  // AdaRMS shift slices split into bf16 hi / lo, made once per launch: [n_steps][L][3: self-attn,
-  // cross-attn, MLP] blocks of B * H * 4 bytes; sample b's 8-column group (k-block kb, group j) is 16 bytes
-  // of hi then 16 bytes of lo at ((b * H/32 + kb) * 4 + j) * 32
+  // AdaRMS shift slices as fp16, made once per launch: [n_steps][L][3: self-attn, cross-attn, MLP] blocks
+  // of B * H * 4 bytes; sample b's 8-column group (k-block kb, group j) is 16 bytes of fp16 at
+  // ((b * H/32 + kb) * 4 + j) * 32 (the next 16 bytes are unused)
   char* shs;
   int n_steps, action_dim, T, R, B, PM, SP, L, Mq, Mqp, NR, NRP, A, act;
   float eps, qk_eps, sm_scale;
@@ -105,8 +107,8 @@ __host__ __device__ constexpr int ceil_to(int a, int m) { return (a + m - 1) / m
 template <int H_, int I_, bool W8_ = false>
 struct Shape {
   static constexpr int H = H_, I = I_, NH = H / HD, NKB = H / 32, HT = H / 16, IT = I / 16, SK = I / H;
-  // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): bf16, or fp8
-  // e4m3 converted to bf16 fragments when read (weight-only quantisation; the activations stay split bf16)
+  // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): fp16 (packed
+  // from bf16), or fp8 e4m3 decoded to fp16 fragments when read (weight-only quantisation)
   static constexpr bool W8 = W8_;
   static constexpr int CH = W8 ? 512 : 1024;  // bytes per chunk
   static constexpr int KPW = NKB / NWAVES;  // 32-wide k-blocks per wave
@@ -142,8 +144,9 @@ struct Shape {
   static_assert(NWAVES * (RBMAX + 1) * 2 * 1024 <= RED_BYTES, "cross-wave reduction must fit LDS");
   static_assert(LDS <= 160 * 1024 - 256, "LDS budget");
   // frame layout (bytes), buffers of NRP rows; HB = NRP * H * 4:
-  //   qs, ks: split q / k (roped, not normed) | vt: split V^T blocks per (sample, head) (2 HB) | ysa split |
-  //   h2 fp32 | y2 split | yca split | h3 fp32 | y3 split | g split (I columns) | hl fp32 | yl split |
+  //   qs, ks: split q / k (roped, not normed) | vt: split V^T blocks per (sample, head) (2 HB) | ysa f16 |
+  //   h2 fp32 | y2 f16 | yca f16 | h3 fp32 | y3 f16 | g f16 (I columns) | hl fp32 | yl f16 |
+  //   (f16: fp16 GEMM operands in the first 1 KB of each 2 KB block)
   //   part fp32 [SK][H] | ssqk [2][NH][2][NRP] | ss2, ss3, ssl [RT][HT / 2][16][2]
   // (sums of squares of h per 16-column tile t and row: one 128-byte line per (16-row tile, tile pair), so
   // that a line has at most two writers: many producers writing 4-byte pieces of one line at once take
@@ -168,7 +171,7 @@ struct Shape {
   __host__ __device__ static long long ss3_off(int nrp) { return ss2_off(nrp) + ss_bytes(nrp); }
   __host__ __device__ static long long ssl_off(int nrp) { return ss3_off(nrp) + ss_bytes(nrp); }
   __host__ __device__ static long long frame_bytes(int nrp) { return ssl_off(nrp) + ss_bytes(nrp); }
-  // step area: h0 fp32 | y0 split | ss0 [RT][HT / 2][16][2] | x [B*T][A] fp32
+  // step area: h0 fp32 | y0 f16 | ss0 [RT][HT / 2][16][2] | x [B*T][A] fp32
   __host__ __device__ static long long step_x_off(int nrp) { return 2 * hb(nrp) + ss_bytes(nrp); }
 };
 
@@ -176,7 +179,8 @@ struct Shape {
 __host__ __device__ __forceinline__ uint32_t fpiece(int r, int c, int RT) {
   return (uint32_t)((((c >> 5) * RT + (r >> 4)) * 2 + ((c >> 2) & 1)) * 1024 + ((r & 15) + 16 * ((c & 31) >> 3)) * 16);
 }
-// byte offset of the 4 high parts (row r, columns c .. c+3) of a split buffer; the residuals are 1 KB later
+// byte offset of the 4 fp16 values (row r, columns c .. c+3) of a GEMM operand buffer, or of the 4 high parts
+// of a split buffer (the residuals are 1 KB later)
 __host__ __device__ __forceinline__ uint32_t spiece(int r, int c, int RT) {
   return (uint32_t)(((c >> 5) * RT + (r >> 4)) * 2048 + ((r & 15) + 16 * ((c & 31) >> 3)) * 16 + (c & 4) * 2);
 }
@@ -414,14 +418,14 @@ struct Desc {
   // GEMM stages
   const char* w; long long wstride;    // packed weight chunks; tile t at w + t * wstride bytes (not split)
   const float* sc; const float* sc2;   // fp8 weights: the layer's output-channel scales (gate/up: sc2 = up)
-  const float* a;                      // split operand frame
+  const float* a;                      // fp16 operand frame
   float* out; const float* res; float* part;
   float* yout; float* ssout;           // residual stages: y = h * (1 + next scale) (split), sums of squares
   const float* ssin;                   // AdaRMS stages: the operand's sums of squares [RT][HT / 2][16][2]
   int ntask, tiles, kind, nt;          // nt: 16-column tiles per task (QKV, gate/up: a pair; wide tasks: NTW)
   int rgs;                             // row groups: task t = tile t % tiles over row-tile group t / tiles
   int pk;                              // placement kind (Params::pl)
-  const char* shs;                     // AdaRMS stages: the split shift fragments of this step and layer
+  const char* shs;                     // AdaRMS stages: the fp16 shift fragments of this step and layer
   // staged modulation slices (H floats each, per sample): AdaRMS stages: shift; residual stages: gate, then
   // the scale of the next AdaRMS
   int mod_off, mod_off2;
@@ -536,13 +540,13 @@ __device__ __forceinline__ void dma_task_w(Ctx<S>& c, const Desc& d, int t, char
 // ------------------------------------------------------------------------------------------------
 // GEMM stage: out tile (16 columns, all rows) of A @ W^T for each task of this workgroup, computed
 // transposed (D^T = W_tile A^T) so that each lane's accumulator is 4 consecutive output columns of one row:
-// one 16-byte piece of the fragment-major output. A is a split operand frame (hi and lo both multiplied).
+// one 16-byte piece of the fragment-major output. A is an fp16 operand frame.
 //   AdaRMS stages (K_QKV: q/k/v; K_GU): A = y = h * (1 + scale) was written by the
 //     producer of h, so out = rstd(h) * (y W^T) + shift W^T (src/mk_expert.py:93-122); rstd comes from the
 //     producer's per-tile sums of squares, shift W^T from an extra MFMA row tile whose rows are the
-//     samples' shift slices. K_QKV: see qk_piece / the V^T epilogue; K_GU stores act(gate) * up split
+//     samples' shift slices. K_QKV: see qk_piece / the V^T epilogue; K_GU stores act(gate) * up in fp16
 //     (:404-413).
-//   K_RES: h_out = res + acc * gate (:162-172), stored fp32, plus y = h_out * (1 + next scale) split and
+//   K_RES: h_out = res + acc * gate (:162-172), stored fp32, plus y = h_out * (1 + next scale) in fp16 and
 //     the tile's sums of squares of h_out; K_SPLIT: K-split partial; the tile's reducer sums the partials
 //     in split order and applies K_RES (down_reduce).
 // K (= H per task) is split over the 4 waves; the wave partials are summed through LDS.
