@@ -92,27 +92,33 @@ __global__ void xcc_probe(unsigned* out) {
 }  // namespace
 
 // The megakernel's instantiations live in their own translation units (mkx_mk768.hip, mkx_mk1024.hip,
-// mkx_mk256.hip), each compiled with its shape's code-generation options.
+// mkx_mk256.hip with GEMM stages in passes; mkx_mk768r.hip, mkx_mk1024r.hip, mkx_mk256r.hip with row-wise GEMM
+// stages), each compiled with its own code-generation options.
 namespace mkx {
-extern template __global__ void mkx_megakernel<768, 3072, false>(Params);
-extern template __global__ void mkx_megakernel<768, 3072, true>(Params);
-extern template __global__ void mkx_megakernel<1024, 4096, false>(Params);
-extern template __global__ void mkx_megakernel<1024, 4096, true>(Params);
-extern template __global__ void mkx_megakernel<256, 512, false>(Params);
-extern template __global__ void mkx_megakernel<256, 512, true>(Params);
+#define MKX_EXTERN(H, I)                                                          \
+  extern template __global__ void mkx_megakernel<H, I, false, false>(Params); \
+  extern template __global__ void mkx_megakernel<H, I, true, false>(Params);  \
+  extern template __global__ void mkx_megakernel<H, I, false, true>(Params);  \
+  extern template __global__ void mkx_megakernel<H, I, true, true>(Params);
+MKX_EXTERN(768, 3072)
+MKX_EXTERN(1024, 4096)
+MKX_EXTERN(256, 512)
+#undef MKX_EXTERN
 }  // namespace mkx
 
 namespace {
 
-template <int H, int I>
+template <int H, int I, bool ROWWISE>
 const void* kernel_of(bool w8) {
-  return w8 ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true>) : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false>);
+  return w8 ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, ROWWISE>)
+            : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false, ROWWISE>);
 }
 
-const void* pick_kernel(int H, int I, bool w8) {
-  if (H == 768 && I == 3072) return kernel_of<768, 3072>(w8);
-  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>(w8);
-  if (H == 256 && I == 512) return kernel_of<256, 512>(w8);
+// rowwise: the form whose GEMM stages compute whole-K products per wave (launches with many row tiles)
+const void* pick_kernel(int H, int I, bool w8, bool rowwise) {
+  if (H == 768 && I == 3072) return rowwise ? kernel_of<768, 3072, true>(w8) : kernel_of<768, 3072, false>(w8);
+  if (H == 1024 && I == 4096) return rowwise ? kernel_of<1024, 4096, true>(w8) : kernel_of<1024, 4096, false>(w8);
+  if (H == 256 && I == 512) return rowwise ? kernel_of<256, 512, true>(w8) : kernel_of<256, 512, false>(w8);
   return nullptr;
 }
 
@@ -125,11 +131,11 @@ int lds_of(int H, int I) {
 
 // the shape constants the host's task layout depends on
 struct ShapeK {
-  int HT, IT, SK, NH, NIN, NTW, W_NARROW, RED_NARROW, W_WIDE, RED_WIDE, SMALL;
+  int HT, IT, SK, NH, NIN, NTW, W_NARROW, RED_NARROW, W_WIDE, RED_WIDE, SMALL, RBMAX;
 };
 template <class S>
 ShapeK shape_k() {
-  return {S::HT, S::IT, S::SK, S::NH, S::NIN, S::NTW, S::W_NARROW, S::RED_NARROW, S::W_WIDE, S::RED_WIDE, S::SMALL};
+  return {S::HT, S::IT, S::SK, S::NH, S::NIN, S::NTW, S::W_NARROW, S::RED_NARROW, S::W_WIDE, S::RED_WIDE, S::SMALL, S::RBMAX};
 }
 ShapeK shape_k(int H, int I, bool w8) {
   if (H == 768 && I == 3072) return w8 ? shape_k<Shape<768, 3072, true>>() : shape_k<Shape<768, 3072, false>>();
@@ -273,6 +279,8 @@ struct mkx_handle {
   int prof_len = 0;
   int profile = 0;
   int plain_launch = 0;  // MKX_PLAIN_LAUNCH=1 at creation: hipLaunchKernel instead of the cooperative launch
+  const void* kernel_rows = nullptr;  // the instantiation with row-wise GEMM stages
+  int gemm_form = -1;    // MKX_GEMM_FORM at creation: 0 passes, 1 row-wise, -1 chosen per launch
   unsigned spin_limit = SPIN_LIMIT;
   int captured = 0;      // a launch of this handle was captured into a graph: its scratch pointers are frozen
   unsigned long long gen_before = 0;
@@ -338,7 +346,7 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   if (d.max_batch < 1 || d.max_batch > MAX_BATCH) return fail(MKX_EINVAL, "max_batch must be in [1, 16]");
   if (d.max_rows < 1 || d.max_rows > 128) return fail(MKX_EINVAL, "max_rows (own rows per sample) must be in [1, 128]");
   if (d.max_mem_rows < 0 || d.max_mem_rows > 256) return fail(MKX_EINVAL, "max_mem_rows must be in [0, 256]");
-  const void* kern = pick_kernel(d.H, d.I, w8);
+  const void* kern = pick_kernel(d.H, d.I, w8, false);
   if (!kern) return fail(MKX_EUNSUPPORTED, "no kernel instantiation for (H, I) = (" + std::to_string(d.H) + ", " + std::to_string(d.I) + ")");
   if (!w->wqkv || !w->wo || !w->wqca || !w->woca || !w->wg || !w->wu || !w->wd || !w->qn || !w->kn || !w->qcan ||
       !w->win || !w->bin || !w->wout || !w->bout)
@@ -350,6 +358,7 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   h->d = d;
   h->w8 = w8 ? 1 : 0;
   h->kernel = kern;
+  h->kernel_rows = pick_kernel(d.H, d.I, w8, true);
   auto bail = [&](int code) { free_handle(h); return code; };
 #define HCHK(x)                                                                                       \
   do {                                                                                                \
@@ -365,10 +374,15 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   int per_cu = 0;
   HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NTHREADS, 0));
   if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel does not fit one workgroup per CU"));
+  HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, h->kernel_rows, NTHREADS, 0));
+  if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel (row-wise GEMM form) does not fit one workgroup per CU"));
   h->G = prop.multiProcessorCount;
   {
     const char* pl = std::getenv("MKX_PLAIN_LAUNCH");
     h->plain_launch = (pl && pl[0] == '1') ? 1 : 0;
+    const char* gf = std::getenv("MKX_GEMM_FORM");
+    if (gf && std::strcmp(gf, "passes") == 0) h->gemm_form = 0;
+    else if (gf && std::strcmp(gf, "rows") == 0) h->gemm_form = 1;
   }
   // XCD of each workgroup of a G-workgroup launch; the barrier's per-XCD counts come from it
   unsigned* dx = nullptr;
@@ -630,12 +644,17 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
   p.tpr = lay.tpr; p.nred = lay.nred;
   void* args[] = {&p};
+  // Row-wise GEMM stages where a gate/up task would need more than one pass of row tiles (the form takes
+  // gated-residual and down-projection tasks of one column tile)
+  const bool one_tile = lay.nt_o == 1 && lay.nt_cao == 1 && lay.nt_down == 1;
+  const bool rows = one_tile && (h->gemm_form == 1 || (h->gemm_form < 0 && NRP / 16 > sk.RBMAX));
+  const void* kern = rows ? h->kernel_rows : h->kernel;
   if (capturing) h->captured = 1;
   if (capturing || h->plain_launch) {
     // co-residency was established at creation (one workgroup per CU fits); capture a plain launch
-    HIPCHK(hipLaunchKernel(h->kernel, dim3(h->G), dim3(NTHREADS), args, 0, stream));
+    HIPCHK(hipLaunchKernel(kern, dim3(h->G), dim3(NTHREADS), args, 0, stream));
   } else {
-    HIPCHK(hipLaunchCooperativeKernel(h->kernel, dim3(h->G), dim3(NTHREADS), args, 0, stream));
+    HIPCHK(hipLaunchCooperativeKernel(kern, dim3(h->G), dim3(NTHREADS), args, 0, stream));
   }
   h->last_nbar = mkx_barriers(h, a->n_steps);
   return MKX_OK;

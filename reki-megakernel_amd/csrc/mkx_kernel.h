@@ -1057,6 +1057,242 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
 }
 
 // ------------------------------------------------------------------------------------------------
+// Row-wise GEMM stages, for launches whose tasks cover more row tiles than one pass of gemm_stage holds
+// (batched samples, long chunks): gemm_stage runs such a task as passes that each wait for their operands,
+// sum the four waves' K quarters through LDS and run the epilogue, one after the other. Here each wave
+// computes whole-K products of its own rows instead: groups of ROWS_NR consecutive row tiles of the task,
+// round-robin over the waves, with the operand fragments streamed by loads issued ROWS_PF k-blocks ahead of
+// the MFMAs, and the epilogue of a group run from the wave's own accumulators. No cross-wave reduction and no
+// barrier between groups; every wave reads all k-blocks of the task's weight tiles from LDS. AdaRMS tasks
+// compute the shift row tile once per task (a quarter of K per wave, summed through LDS), and each lane loads
+// the sums of squares of its row's quarter of the tiles (summed across the four lanes holding the row).
+// The host uses this form only where every task has at most two column tiles (the layout with one task per
+// workgroup and stage).
+constexpr int ROWS_NR = 2;  // row tiles per group
+constexpr int ROWS_PF = 8;  // k-blocks of operand loads in flight ahead of the MFMAs
+
+// D^T = W A^T (SWAP: D = A W^T) of NT weight tiles (LDS, [tile][k-block] chunks) over ROWS_NR row tiles
+// (operand blocks at soffset roff[r] of k-block 0) and every k-block of the task from kb0; consecutive
+// k-blocks alternate between two accumulators per product. Each k-block's step issues the operand loads of
+// k-block i + ROWS_PF and the LDS reads of the weight fragments of k-block i + 1 before its MFMAs, and ends in
+// a scheduling barrier: left to itself, the scheduler moves every load down to its use (fewer live
+// registers), which leaves one memory round trip per k-block.
+template <class S, int NT, bool SWAP>
+__device__ __forceinline__ void rows_mma(f32x4 (&acc)[ROWS_NR][NT][2], __amdgpu_buffer_rsrc_t ra, const uint32_t (&roff)[ROWS_NR],
+                                         int kb0, int RT, const char* wl, int lane) {
+  constexpr int NKB = S::NKB, PF = ROWS_PF < NKB ? ROWS_PF : NKB;
+  const uint32_t vl = (uint32_t)lane * 16;
+  f16x8 a[NKB][ROWS_NR];
+#pragma unroll
+  for (int i = 0; i < PF; ++i)
+#pragma unroll
+    for (int r = 0; r < ROWS_NR; ++r)
+      a[i][r] = __builtin_bit_cast(f16x8, bload(ra, vl, (uint32_t)((kb0 + i) * RT) * 2048 + roff[r]));
+  f16x8 wn[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) wn[nt] = wfrag_lds<S>(wl + (nt * NKB) * S::CH, lane);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < NKB; ++i) {
+    if (i + PF < NKB) {
+#pragma unroll
+      for (int r = 0; r < ROWS_NR; ++r)
+        a[i + PF][r] = __builtin_bit_cast(f16x8, bload(ra, vl, (uint32_t)((kb0 + i + PF) * RT) * 2048 + roff[r]));
+    }
+    f16x8 wf[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) wf[nt] = wn[nt];
+    if (i + 1 < NKB) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) wn[nt] = wfrag_lds<S>(wl + (nt * NKB + i + 1) * S::CH, lane);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < ROWS_NR; ++r) {
+        f32x4& x = acc[r][nt][i & 1];
+        x = SWAP ? mfma16h(a[i][r], wf[nt], x) : mfma16h(wf[nt], a[i][r], x);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// One group of a wave: row tiles rt0 .. rt0 + ROWS_NR - 1 (those from rt_hi on repeat the last valid one and
+// store nothing). NT = 2: AdaRMS tasks (QKV, gate/up; SWAP: V), whose shift-tile partials the waves left in
+// LDS; NT = 1: gated-residual (K_RES) or down-projection split (K_SPLIT) tasks.
+template <class S, int NT, bool SWAP>
+__device__ __forceinline__ void rows_group(Ctx<S>& c, const Desc& d, int rt0, int rt_hi, int kb0, int tile, int split, int qkind,
+                                           int qhd, int qj) {
+  constexpr int NR = ROWS_NR, HT = S::HT;
+  CP& p = c.p;
+  const int RT = c.RT, L = c.lane;
+  const char* red = c.smem + p.lds_red;  // [wave][2 tiles][64 lanes] x 16 bytes: shift-tile partials
+  int rts[NR];
+  uint32_t roff[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    rts[r] = min(rt0 + r, rt_hi - 1);
+    roff[r] = (uint32_t)rts[r] * 2048;
+  }
+  // the epilogue's operands, issued before the operand stream: sums of squares (this lane's quarter of its
+  // row's tile pairs), constants (RoPE tables, norm weights, fp8 scales) and residual pieces
+  u32x2 ssv[NR][HT / 8];
+  EpiPre ep[NR];
+  f32x4 res[NR];
+  const int col = tile * 16 + 4 * (L >> 4);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int row = rts[r] * 16 + (L & 15);
+    if constexpr (NT == 2) {
+      const __amdgpu_buffer_rsrc_t rs_ = rsrc(d.ssin);
+      const uint32_t so = ss_slot<HT>(row, (L >> 4) * (HT / 4));
+#pragma unroll
+      for (int i = 0; i < HT / 8; ++i) ssv[r][i] = bload8(rs_, so, (uint32_t)i * 128);
+    }
+    ep[r] = epi_const(c, d, qkind, qj, tile, row, L);
+    if constexpr (NT == 1) {
+      if (d.kind == K_RES) res[r] = as_f4(ld16((const char*)d.res + fpiece(row, col, RT)));
+    }
+  }
+  f32x4 acc[NR][NT][2];
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[r][nt][0] = acc[r][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  rows_mma<S, NT, SWAP>(acc, rsrc(d.a), roff, kb0, RT, c.smem + S::WBUF, L);
+  auto sum4 = [](const f32x4 (&pw)[NWAVES]) { return ((pw[0] + pw[1]) + pw[2]) + pw[3]; };
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (rt0 + r >= rt_hi) break;
+    const int row = rts[r] * 16 + (L & 15);
+    if constexpr (NT == 1) {
+      const f32x4 v = acc[r][0][0] + acc[r][0][1];
+      if (d.kind == K_SPLIT) st_sc1(d.part, (uint32_t)((((split * d.tiles + tile) * RT + rts[r]) * 64 + L) * 16), as_u4(v));
+      else res_piece(c, d, tile, row, col, L, S::W8 ? v * ep[r].sa : v, res[r]);
+    } else {
+      // the row's sum of squares: this lane's quarter, then the four lanes holding the row
+      const float ss = xor32_sum(xor16_sum(ss_pairs_sum<HT / 8>(ssv[r])));
+      if constexpr (SWAP) {
+        // V: lane L holds column 16 j + 32 nt + L % 16 of the head for rows (keys) 4 (L / 16) + e of a
+        // 16-row tile of one sample; their RMS factors come from the lanes holding those rows
+        const int row0 = rts[r] * 16, b = c.sample_of(row0);
+        const int ib = row0 - b * p.Mqp + 4 * (L >> 4);
+        const int KBO = ceil_to(p.Mq, 32) / 32;
+        const int cl = L & 15, bl = b + 16 * (cl >> 2);
+        float rsv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rsv[e] = rsqrtf(__shfl(ss, 4 * (L >> 4) + e) * (1.0f / (float)S::H) + p.eps);
+        float b0[NWAVES], b1[NWAVES];
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+          b0[w] = ((const float*)(red + ((w * 2 + 0) * 64 + bl) * 16))[cl & 3];
+          b1[w] = ((const float*)(red + ((w * 2 + 1) * 64 + bl) * 16))[cl & 3];
+        }
+        lds_batch(b0);
+        lds_batch(b1);
+        const uint32_t vo = (uint32_t)(((b * S::NH + qhd) * KBO + (ib >> 5)) * 8192 + L * 16 + ((ib >> 4) & 1) * 8);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const f32x4 a = acc[r][nt][0] + acc[r][nt][1];
+          const float* bb = nt ? b1 : b0;
+          const float bias = ((bb[0] + bb[1]) + bb[2]) + bb[3];
+          const float sv = S::W8 ? ep[r].sa[nt] : 1.0f;
+          f32x4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = ib + e < p.Mq ? (a[e] * rsv[e] + bias) * sv : 0.f;
+          st_split4(d.part, vo + (uint32_t)((qj + 2 * nt) * 2048), x);
+        }
+      } else {
+        const float rsr = rsqrtf(ss * (1.0f / (float)S::H) + p.eps);
+        const int bl = c.sample_of(row) + 16 * (L >> 4);
+        f32x4 pb0[NWAVES], pb1[NWAVES];
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+          pb0[w] = ldf4((const float*)(red + ((w * 2 + 0) * 64 + bl) * 16));
+          pb1[w] = ldf4((const float*)(red + ((w * 2 + 1) * 64 + bl) * 16));
+        }
+        lds_batch(pb0);
+        lds_batch(pb1);
+        f32x4 v = (acc[r][0][0] + acc[r][0][1]) * rsr + sum4(pb0);
+        f32x4 u = (acc[r][1][0] + acc[r][1][1]) * rsr + sum4(pb1);
+        if (S::W8) {
+          v *= ep[r].sa;
+          u *= ep[r].sb;
+        }
+        if (d.kind == K_GU) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = act_fn(v[j], p.act) * u[j];
+          if (st_h4(d.out, spiece(row, col, RT), v)) range_error(p.bar);
+        } else {
+          qk_piece(c, d, qkind, qhd, qj, row, L, v, u, ep[r]);
+        }
+      }
+    }
+  }
+}
+
+template <class S>
+__device__ __forceinline__ void gemm_stage_rows(Ctx<S>& c, const Desc& d, BarCtx& bc, int g) {
+  constexpr int KPW = S::KPW, NKB = S::NKB, NR = ROWS_NR;
+  CP& p = c.p;
+  const int RT = c.RT, L = c.lane;
+  const bool ada = d.kind == K_QKV || d.kind == K_GU;
+  const int t0 = task_first(c, d.pk);
+  for (int t = t0; t < d.ntask; t += c.G) {
+    const int tile = t % d.tiles, split = t / d.tiles;
+    const int qkind = d.kind == K_QKV ? tile / (2 * S::NH) : 0, qhd = (tile >> 1) % S::NH, qj = tile & 1;
+    if (t != t0) {
+      wait_vm0();
+      __syncthreads();
+      dma_task_w(c, d, t, c.smem + S::WBUF);
+    }
+    const int kb0 = d.kind == K_SPLIT ? split * NKB : 0;
+    const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
+    const int rt_hi = d.kind == K_SPLIT ? RT : (split + 1) * RT / d.rgs;
+    gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
+    // the task's weight tiles and the stage's shift fragments (the prefetch's DMA) have landed
+    wait_vm0();
+    __syncthreads();
+    if (ada) {
+      // shift row tile (rows = samples; zeros for the samples >= B) over this wave's k-blocks, into LDS
+      const char* shl = c.smem + p.lds_mods;
+      const char* wl = c.smem + S::WBUF;
+      const bool has = (L & 15) < p.B;
+      f32x4 accs[2][2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) accs[nt][0] = accs[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KPW; ++i) {
+        const int kb = c.wave + NWAVES * i;
+        const f16x8 sh = has ? ldsfrag_h(shl + (((L & 15) * NKB + kb) * 4 + (L >> 4)) * 32) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) accs[nt][i & 1] = mfma16h(wfrag_lds<S>(wl + (nt * NKB + kb) * S::CH, L), sh, accs[nt][i & 1]);
+      }
+      char* red = c.smem + p.lds_red;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) sts16(red + ((c.wave * 2 + nt) * 64 + L) * 16, as_u4(accs[nt][0] + accs[nt][1]));
+      __syncthreads();
+    }
+    const int ng = (rt_hi - rt_lo + NR - 1) / NR;
+    for (int gi = c.wave; gi < ng; gi += NWAVES) {
+      const int rt0 = rt_lo + gi * NR;
+      if (d.kind == K_QKV && qkind == 2) rows_group<S, 2, true>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj);
+      else if (ada) rows_group<S, 2, false>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj);
+      else rows_group<S, 1, false>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj);
+    }
+    flag_publish(bc, d.st == ST_QKV ? F_QKV : d.st == ST_O ? F_O : d.st == ST_CAO ? F_CAO : d.st == ST_GU ? F_GU : F_DPART, t,
+                 (unsigned long long)g + 1);
+  }
+  if (d.kind == K_SPLIT) {
+    const int r = task_first(c, PL_RED);
+    if (r < p.nred) {
+      if (p.tpr == S::NTW) down_reduce<S, S::NTW>(c, d, bc, g, r);
+      else down_reduce<S, 1>(c, d, bc, g, r);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Attention. One task per (sample, head, 16-query tile); its 4 waves take the 32-key blocks round-robin
 // and merge their online-softmax states through LDS at the end.
 // K chunk (key tile kt, d-block db), 1 KB: lane l holds K[kt*16 + l%16][db*32 + 8(l/16) + j] (the split
@@ -2106,7 +2342,7 @@ __device__ __forceinline__ StagePos next_stage(unsigned mask, StagePos q, int to
 }
 
 // ------------------------------------------------------------------------------------------------
-template <int H, int I, bool W8>
+template <int H, int I, bool W8, bool ROWWISE>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   using S = Shape<H, I, W8>;
   __shared__ __attribute__((aligned(1024))) char smem[S::LDS];
@@ -2158,6 +2394,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       if (cur.st == ST_SA) sa_stage(c, cur, s_ks, bc, g);
       else if (cur.st == ST_CA) ca_stage(c, cur, s_ks, bc, g);
       else if (cur.st == ST_TAIL) tail_stage(c, cur, bc, g);
+      else if constexpr (ROWWISE) gemm_stage_rows(c, cur, bc, g);
       else gemm_stage(c, cur, bc, g);
       if (g == 0) {
         transpose_caches(c, s_ks);

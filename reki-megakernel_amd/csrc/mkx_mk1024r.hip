@@ -1,0 +1,8 @@
+// The megakernel's instantiations for H = 1024, I = 4096 (bf16 and fp8 weights) with row-wise GEMM stages (the
+// form for launches whose GEMM tasks cover more row tiles than one pass holds), in a translation unit of their own.
+#include "mkx_kernel.h"
+
+namespace mkx {
+template __global__ void mkx_megakernel<1024, 4096, false, true>(Params);
+template __global__ void mkx_megakernel<1024, 4096, true, true>(Params);
+}  // namespace mkx

@@ -1,8 +1,8 @@
-// The megakernel's instantiations for H = 256, I = 512 (bf16 and fp8 weights), in a translation unit of their
-// own so that the build can give them their own code-generation options (mkx/_build.py).
+// The megakernel's instantiations for H = 256, I = 512 (bf16 and fp8 weights) with GEMM stages in passes,
+// in a translation unit of their own so that the build can give them their own code-generation options.
 #include "mkx_kernel.h"
 
 namespace mkx {
-template __global__ void mkx_megakernel<256, 512, false>(Params);
-template __global__ void mkx_megakernel<256, 512, true>(Params);
+template __global__ void mkx_megakernel<256, 512, false, false>(Params);
+template __global__ void mkx_megakernel<256, 512, true, false>(Params);
 }  // namespace mkx

@@ -26,6 +26,9 @@ UNITS = (
     ("mkx_mk768.hip", ("-mllvm", "-amdgpu-sched-strategy=max-memory-clause")),
     ("mkx_mk1024.hip", ()),
     ("mkx_mk256.hip", ()),
+    ("mkx_mk768r.hip", ()),
+    ("mkx_mk1024r.hip", ()),
+    ("mkx_mk256r.hip", ()),
 )
 COMMON = ("--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
           # packed fp32 instructions stay off: every HIP source is compiled without them

@@ -149,6 +149,50 @@ def test_gelu_variant_at_config_A_size():
     _check_loop("A gelu_tanh", make_case(replace(SY.WORKLOADS["A"], act="gelu_tanh")))
 
 
+class _gemm_form:
+    """Forces the megakernel's GEMM form for the handles created inside the block (MKX_GEMM_FORM is read when
+    a handle is created): "passes" (row tiles in passes, the K quarters of the four waves summed through LDS)
+    or "rows" (each wave whole-K products of its own row tiles)."""
+
+    def __init__(self, form):
+        self.form = form
+
+    def __enter__(self):
+        import os
+        self.old = os.environ.get("MKX_GEMM_FORM")
+        os.environ["MKX_GEMM_FORM"] = self.form
+
+    def __exit__(self, *exc):
+        import os
+        if self.old is None:
+            os.environ.pop("MKX_GEMM_FORM", None)
+        else:
+            os.environ["MKX_GEMM_FORM"] = self.old
+
+
+def test_tiny_batch_of_four_both_gemm_forms():
+    # 4 x 16 rows: more row tiles than one GEMM pass holds, so the launch takes the row-wise form by itself;
+    # forced into passes it must agree with the oracle as well
+    from dataclasses import replace
+    case = make_case(replace(TINY, B=4))
+    _check_loop("tiny b4 (row-wise GEMMs)", case)
+    with _gemm_form("passes"):
+        _check_loop("tiny b4 (GEMM passes)", case)
+
+
+def test_tiny_fp8_gelu_rowwise():
+    # fp8 weights (scales in every row-wise epilogue kind) and the GELU MLP on the row-wise form
+    from dataclasses import replace
+    with _gemm_form("rows"):
+        _check_loop("tiny fp8 gelu (row-wise GEMMs)", make_case(replace(TINY, B=3, weight_dtype="fp8_e4m3", act="gelu_tanh")))
+
+
+def test_tiny_single_row_tile_rowwise():
+    # one row tile per sample: groups of two row tiles whose second repeats the first and stores nothing
+    with _gemm_form("rows"):
+        _check_loop("tiny (row-wise GEMMs)", make_case(TINY))
+
+
 def test_barrier_count_invariant_and_determinism():
     case = make_case(TINY)
     cfg = case["cfg"]
