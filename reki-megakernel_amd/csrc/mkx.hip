@@ -158,9 +158,13 @@ struct Layout {
   int rgs_qkv, rgs_o, rgs_cao, nt_o, nt_cao, nt_down, lds_red, lds_mods, tpr, nred;
   bool disjoint;
 };
-Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A) {
+// step-tail output tasks: TAIL_AC dims each, or, in the row-wise form, TAIL_DG dims of TAIL_RCH rows each
+int tail_outputs(bool rows, int nrows, int A) {
+  return rows ? (nrows + TAIL_RCH - 1) / TAIL_RCH * ((A + TAIL_DG - 1) / TAIL_DG) : (A + TAIL_AC - 1) / TAIL_AC;
+}
+Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A, int nout) {
   Layout L{};
-  const int nattn = B * k.NH * nqt, nout = (A + TAIL_AC - 1) / TAIL_AC, mods = B * 2 * H * 4;
+  const int nattn = B * k.NH * nqt, mods = B * 2 * H * 4;
   const bool wide = k.NTW > 1 && k.W_WIDE + std::max(k.RED_WIDE, k.RED_NARROW) + mods <= k.SMALL;
   const int nt = wide ? k.NTW : 1;
   auto clampi = [](int v, int lo, int hi) { return std::max(lo, std::min(hi, v)); };
@@ -538,7 +542,14 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   // the GEMM stages stage every sample's modulation slices (2 H floats) in 56 KB.
   if ((long long)a->B * 2 * H * 4 > 56 * 1024) return fail(MKX_EUNSUPPORTED, "batch too large to stage its modulation slices in LDS");
   const ShapeK sk = shape_k(H, I, h->w8 != 0);
-  const Layout lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A);
+  Layout lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(false, a->B * a->T_act, d.A));
+  // Row-wise GEMM stages where a gate/up task would need more than one pass of row tiles (the form takes
+  // gated-residual and down-projection tasks of one column tile, and its step tail's output tasks, over row
+  // chunks, must number at most 64)
+  const bool one_tile = lay.nt_o == 1 && lay.nt_cao == 1 && lay.nt_down == 1;
+  const bool rows = one_tile && tail_outputs(true, a->B * a->T_act, d.A) <= 64 &&
+                    (h->gemm_form == 1 || (h->gemm_form < 0 && NRP / 16 > sk.RBMAX));
+  if (rows) lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(true, a->B * a->T_act, d.A));
   {
     // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes): gate/up on every CA out-projection
     // task, an out-projection task on every head of its rows; and on at most 64 (one load per poll) where
@@ -644,10 +655,6 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
   p.tpr = lay.tpr; p.nred = lay.nred;
   void* args[] = {&p};
-  // Row-wise GEMM stages where a gate/up task would need more than one pass of row tiles (the form takes
-  // gated-residual and down-projection tasks of one column tile)
-  const bool one_tile = lay.nt_o == 1 && lay.nt_cao == 1 && lay.nt_down == 1;
-  const bool rows = one_tile && (h->gemm_form == 1 || (h->gemm_form < 0 && NRP / 16 > sk.RBMAX));
   const void* kern = rows ? h->kernel_rows : h->kernel;
   if (capturing) h->captured = 1;
   if (capturing || h->plain_launch) {

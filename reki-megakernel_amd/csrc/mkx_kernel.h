@@ -104,9 +104,11 @@ typedef const __attribute__((address_space(4))) Params CP;
 
 __host__ __device__ constexpr int ceil_to(int a, int m) { return (a + m - 1) / m * m; }
 
-template <int H_, int I_, bool W8_ = false>
+template <int H_, int I_, bool W8_ = false, bool RW_ = false>
 struct Shape {
   static constexpr int H = H_, I = I_, NH = H / HD, NKB = H / 32, HT = H / 16, IT = I / 16, SK = I / H;
+  // RW: the launch form for many row tiles (row-wise GEMM stages, step-tail output tasks over row chunks)
+  static constexpr bool RW = RW_;
   // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): fp16 (packed
   // from bf16), or fp8 e4m3 decoded to fp16 fragments when read (weight-only quantisation)
   static constexpr bool W8 = W8_;
@@ -1062,32 +1064,52 @@ __device__ __forceinline__ void gemm_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
 // sum the four waves' K quarters through LDS and run the epilogue, one after the other. Here each wave
 // computes whole-K products of its own rows instead: groups of ROWS_NR consecutive row tiles of the task,
 // round-robin over the waves, with the operand fragments streamed by loads issued ROWS_PF k-blocks ahead of
-// the MFMAs, and the epilogue of a group run from the wave's own accumulators. No cross-wave reduction and no
-// barrier between groups; every wave reads all k-blocks of the task's weight tiles from LDS. AdaRMS tasks
-// compute the shift row tile once per task (a quarter of K per wave, summed through LDS), and each lane loads
-// the sums of squares of its row's quarter of the tiles (summed across the four lanes holding the row).
+// the MFMAs (the first group's first loads are issued before the shift tile), and the epilogue of a group run from the wave's own accumulators. No
+// cross-wave reduction and no barrier between groups; every wave reads all k-blocks of the task's weight tiles
+// from LDS. AdaRMS tasks compute the shift row tile once per task (a quarter of K per wave, summed through
+// LDS), and each lane loads the sums of squares of its row's quarter of the tiles (summed across the four
+// lanes holding the row).
 // The host uses this form only where every task has at most two column tiles (the layout with one task per
 // workgroup and stage).
 constexpr int ROWS_NR = 2;  // row tiles per group
 constexpr int ROWS_PF = 8;  // k-blocks of operand loads in flight ahead of the MFMAs
+template <class S>
+constexpr int rows_pf() { return ROWS_PF < S::NKB ? ROWS_PF : S::NKB; }
+
+// soffsets of the operand blocks (k-block 0) of the group at row tile rt0: row tiles from rt_hi on repeat the
+// last valid one
+__device__ __forceinline__ void rows_roff(uint32_t (&roff)[ROWS_NR], int rt0, int rt_hi) {
+#pragma unroll
+  for (int r = 0; r < ROWS_NR; ++r) roff[r] = (uint32_t)min(rt0 + r, rt_hi - 1) * 2048;
+}
+// the operand loads of a group's first rows_pf() k-blocks
+template <class S>
+__device__ __forceinline__ void rows_head(f16x8 (&pre)[rows_pf<S>()][ROWS_NR], __amdgpu_buffer_rsrc_t ra, const uint32_t (&roff)[ROWS_NR],
+                                          int kb0, int RT, int lane) {
+#pragma unroll
+  for (int i = 0; i < rows_pf<S>(); ++i)
+#pragma unroll
+    for (int r = 0; r < ROWS_NR; ++r)
+      pre[i][r] = __builtin_bit_cast(f16x8, bload(ra, (uint32_t)lane * 16, (uint32_t)((kb0 + i) * RT) * 2048 + roff[r]));
+}
 
 // D^T = W A^T (SWAP: D = A W^T) of NT weight tiles (LDS, [tile][k-block] chunks) over ROWS_NR row tiles
 // (operand blocks at soffset roff[r] of k-block 0) and every k-block of the task from kb0; consecutive
-// k-blocks alternate between two accumulators per product. Each k-block's step issues the operand loads of
+// k-blocks alternate between two accumulators per product. pre holds the loads of the first rows_pf()
+// k-blocks (issued by rows_head). Each k-block's step issues the operand loads of
 // k-block i + ROWS_PF and the LDS reads of the weight fragments of k-block i + 1 before its MFMAs, and ends in
 // a scheduling barrier: left to itself, the scheduler moves every load down to its use (fewer live
 // registers), which leaves one memory round trip per k-block.
 template <class S, int NT, bool SWAP>
 __device__ __forceinline__ void rows_mma(f32x4 (&acc)[ROWS_NR][NT][2], __amdgpu_buffer_rsrc_t ra, const uint32_t (&roff)[ROWS_NR],
-                                         int kb0, int RT, const char* wl, int lane) {
-  constexpr int NKB = S::NKB, PF = ROWS_PF < NKB ? ROWS_PF : NKB;
+                                         int kb0, int RT, const char* wl, int lane, const f16x8 (&pre)[rows_pf<S>()][ROWS_NR]) {
+  constexpr int NKB = S::NKB, PF = rows_pf<S>();
   const uint32_t vl = (uint32_t)lane * 16;
   f16x8 a[NKB][ROWS_NR];
 #pragma unroll
   for (int i = 0; i < PF; ++i)
 #pragma unroll
-    for (int r = 0; r < ROWS_NR; ++r)
-      a[i][r] = __builtin_bit_cast(f16x8, bload(ra, vl, (uint32_t)((kb0 + i) * RT) * 2048 + roff[r]));
+    for (int r = 0; r < ROWS_NR; ++r) a[i][r] = pre[i][r];
   f16x8 wn[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) wn[nt] = wfrag_lds<S>(wl + (nt * NKB) * S::CH, lane);
@@ -1118,11 +1140,11 @@ __device__ __forceinline__ void rows_mma(f32x4 (&acc)[ROWS_NR][NT][2], __amdgpu_
 }
 
 // One group of a wave: row tiles rt0 .. rt0 + ROWS_NR - 1 (those from rt_hi on repeat the last valid one and
-// store nothing). NT = 2: AdaRMS tasks (QKV, gate/up; SWAP: V), whose shift-tile partials the waves left in
-// LDS; NT = 1: gated-residual (K_RES) or down-projection split (K_SPLIT) tasks.
+// store nothing), whose first loads (pre) rows_head has issued. NT = 2: AdaRMS tasks (QKV, gate/up; SWAP: V), whose shift-tile partials the waves left in LDS; NT = 1:
+// gated-residual (K_RES) or down-projection split (K_SPLIT) tasks.
 template <class S, int NT, bool SWAP>
 __device__ __forceinline__ void rows_group(Ctx<S>& c, const Desc& d, int rt0, int rt_hi, int kb0, int tile, int split, int qkind,
-                                           int qhd, int qj) {
+                                           int qhd, int qj, const f16x8 (&pre)[rows_pf<S>()][ROWS_NR]) {
   constexpr int NR = ROWS_NR, HT = S::HT;
   CP& p = c.p;
   const int RT = c.RT, L = c.lane;
@@ -1130,10 +1152,8 @@ __device__ __forceinline__ void rows_group(Ctx<S>& c, const Desc& d, int rt0, in
   int rts[NR];
   uint32_t roff[NR];
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    rts[r] = min(rt0 + r, rt_hi - 1);
-    roff[r] = (uint32_t)rts[r] * 2048;
-  }
+  for (int r = 0; r < NR; ++r) rts[r] = min(rt0 + r, rt_hi - 1);
+  rows_roff(roff, rt0, rt_hi);
   // the epilogue's operands, issued before the operand stream: sums of squares (this lane's quarter of its
   // row's tile pairs), constants (RoPE tables, norm weights, fp8 scales) and residual pieces
   u32x2 ssv[NR][HT / 8];
@@ -1159,7 +1179,7 @@ __device__ __forceinline__ void rows_group(Ctx<S>& c, const Desc& d, int rt0, in
   for (int r = 0; r < NR; ++r)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[r][nt][0] = acc[r][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  rows_mma<S, NT, SWAP>(acc, rsrc(d.a), roff, kb0, RT, c.smem + S::WBUF, L);
+  rows_mma<S, NT, SWAP>(acc, rsrc(d.a), roff, kb0, RT, c.smem + S::WBUF, L, pre);
   auto sum4 = [](const f32x4 (&pw)[NWAVES]) { return ((pw[0] + pw[1]) + pw[2]) + pw[3]; };
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
@@ -1249,10 +1269,22 @@ __device__ __forceinline__ void gemm_stage_rows(Ctx<S>& c, const Desc& d, BarCtx
     const int kb0 = d.kind == K_SPLIT ? split * NKB : 0;
     const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
     const int rt_hi = d.kind == K_SPLIT ? RT : (split + 1) * RT / d.rgs;
+    MKX_TR(c, 14);
     gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
+    MKX_TR(c, 0);
     // the task's weight tiles and the stage's shift fragments (the prefetch's DMA) have landed
     wait_vm0();
     __syncthreads();
+    MKX_TR(c, 1);
+    // the operand loads of this wave's first group go out before the shift tile
+    const int ng = (rt_hi - rt_lo + NR - 1) / NR;
+    const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
+    f16x8 pre[rows_pf<S>()][NR];
+    if (c.wave < ng) {
+      uint32_t roff0[NR];
+      rows_roff(roff0, rt_lo + c.wave * NR, rt_hi);
+      rows_head<S>(pre, ra, roff0, kb0, RT, L);
+    }
     if (ada) {
       // shift row tile (rows = samples; zeros for the samples >= B) over this wave's k-blocks, into LDS
       const char* shl = c.smem + p.lds_mods;
@@ -1273,12 +1305,18 @@ __device__ __forceinline__ void gemm_stage_rows(Ctx<S>& c, const Desc& d, BarCtx
       for (int nt = 0; nt < 2; ++nt) sts16(red + ((c.wave * 2 + nt) * 64 + L) * 16, as_u4(accs[nt][0] + accs[nt][1]));
       __syncthreads();
     }
-    const int ng = (rt_hi - rt_lo + NR - 1) / NR;
+    MKX_TR(c, 2);
     for (int gi = c.wave; gi < ng; gi += NWAVES) {
       const int rt0 = rt_lo + gi * NR;
-      if (d.kind == K_QKV && qkind == 2) rows_group<S, 2, true>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj);
-      else if (ada) rows_group<S, 2, false>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj);
-      else rows_group<S, 1, false>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj);
+      if (gi != c.wave) {  // the wave's later groups: their first loads now
+        uint32_t roffg[NR];
+        rows_roff(roffg, rt0, rt_hi);
+        rows_head<S>(pre, ra, roffg, kb0, RT, L);
+      }
+      if (d.kind == K_QKV && qkind == 2) rows_group<S, 2, true>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj, pre);
+      else if (ada) rows_group<S, 2, false>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj, pre);
+      else rows_group<S, 1, false>(c, d, rt0, rt_hi, kb0, tile, split, qkind, qhd, qj, pre);
+      MKX_TR(c, gi < 4 ? 3 : gi < 8 ? 5 : gi < 12 ? 11 : 12);  // wave 0's groups
     }
     flag_publish(bc, d.st == ST_QKV ? F_QKV : d.st == ST_O ? F_O : d.st == ST_CAO ? F_CAO : d.st == ST_GU ? F_GU : F_DPART, t,
                  (unsigned long long)g + 1);
@@ -2048,6 +2086,17 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
 // operands (Win columns, bias, register tokens, layer-0 scale) are loaded with the first batch.
 constexpr int TAIL_RPW = 3;  // action rows per wave and batch
 constexpr int TAIL_AC = 8;   // action dims reduced together
+// Launches of the row-wise form (many rows) split the output tasks by rows as well: TAIL_RCH rows (one batch
+// per wave) and TAIL_DG dims per task, written to x of the next step before the in-projection tasks, which
+// read them there instead of each recomputing the velocity of every row.
+constexpr int TAIL_RCH = NWAVES * TAIL_RPW;
+constexpr int TAIL_DG = 2 * TAIL_AC;
+// output tasks of a step tail (not the launch's first)
+template <class S>
+__device__ __forceinline__ int tail_nout(CP& p) {
+  if constexpr (S::RW) return (p.B * p.T + TAIL_RCH - 1) / TAIL_RCH * ((p.A + TAIL_DG - 1) / TAIL_DG);
+  else return (p.A + TAIL_AC - 1) / TAIL_AC;
+}
 
 template <int N>
 __device__ __forceinline__ void wave_sum_n(float* v) {
@@ -2061,7 +2110,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   constexpr int NP = S::H / 256;  // pieces per lane
   constexpr int R = TAIL_RPW;
   const int nin = d.last ? 0 : S::NIN;
-  const int nout = d.first ? 0 : (p.A + TAIL_AC - 1) / TAIL_AC;
+  const int nout = d.first ? 0 : tail_nout<S>(p);
   const int nrows = p.B * p.T;
   const int adim = p.action_dim;
   const float* xcur = (d.first || d.s == 0) ? p.x_in : c.xstep(d.s);
@@ -2075,7 +2124,9 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
   bool first_task = true;
   for (int k = 0; k < 2; ++k) {
     int t = -1;
-    if (k == 0) t = tin < nin ? tin : -1;
+    // the row-wise form's in-projection tasks read the output tasks' x, so a workgroup with both runs its
+    // output task first
+    if (k == (S::RW ? 1 : 0)) t = tin < nin ? tin : -1;
     else t = tout < nout ? nin + tout : -1;
     if (t < 0) continue;
     if (!first_task) __syncthreads();  // the previous task's LDS (the first task's is free already)
@@ -2097,7 +2148,10 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       }
       if (c.tid < adim * 8) wt = ldf4(p.win + (long long)(c.tid >> 3) * S::H + t * 32 + 4 * (c.tid & 7));
     }
-    if (!d.first) {
+    if (!d.first && S::RW && inproj) {
+      // x after the step, from this step tail's output tasks
+      flag_wait<1>(bc, F_TAIL_OUT, nout, [](int i) { return i; }, (unsigned long long)g + 1);
+    } else if (!d.first) {
       // every tile of the last layer's output (its reducers), and x of this step (the previous step tail's
       // output dims)
       flag_wait<1>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
@@ -2107,21 +2161,38 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     wait_vm0();
     __syncthreads();
     MKX_TR(c, 0);
-    if (!d.first) {
+    if (!d.first && S::RW && inproj) {
+      const float* xn = c.xstep(d.s + 1);
+      for (int it = c.tid; it < nrows * adim; it += NTHREADS) {
+        const int ri = it / adim, a = it - ri * adim;
+        xp[it] = xn[(long long)ri * p.A + a];
+      }
+    } else if (!d.first) {
       const __amdgpu_buffer_rsrc_t rh = rsrc(hL);
       // dims [a_lo, a_hi) of this task (Wout rows staged in LDS from row a_lo): the in-projection's real dims,
-      // or an output task's TAIL_AC dims. Lane a holds bout[a] and, in xc[k], x of row k's dim a.
-      const int a_lo = inproj ? 0 : a_out * TAIL_AC, a_hi = inproj ? adim : min(a_lo + TAIL_AC, p.A);
+      // or an output task's TAIL_AC dims (row-wise form: TAIL_DG dims of rows [r_lo, r_hi)). Lane a holds
+      // bout[a] and, in xc[k], x of row k's dim a.
+      int a_lo, a_hi, r_lo = 0, r_hi = nrows;
+      if constexpr (S::RW) {
+        const int ndg = (p.A + TAIL_DG - 1) / TAIL_DG;
+        a_lo = inproj ? 0 : (a_out % ndg) * TAIL_DG;
+        a_hi = inproj ? adim : min(a_lo + TAIL_DG, p.A);
+        r_lo = (a_out / ndg) * TAIL_RCH;
+        r_hi = min(r_lo + TAIL_RCH, nrows);
+      } else {
+        a_lo = inproj ? 0 : a_out * TAIL_AC;
+        a_hi = inproj ? adim : min(a_lo + TAIL_AC, p.A);
+      }
       const float bo = p.bout[min(c.lane, p.A - 1)];
       float* xn = d.last ? p.x_out : c.xstep(d.s + 1);
       // a launch whose synchronisation gave up (a wait exceeded its spin bound) returns NaN, not a result
       const bool poisoned = d.last && __hip_atomic_load(&p.bar->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-      for (int r0 = c.wave; r0 < nrows; r0 += NWAVES * R) {
+      for (int r0 = r_lo + c.wave; r0 < r_hi; r0 += NWAVES * R) {
         f32x4 x[R][NP];
         float xc[R];
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-          const int ri = min(r0 + NWAVES * k, nrows - 1);
+          const int ri = min(r0 + NWAVES * k, r_hi - 1);
           const int b = ri / p.T, grow = b * p.Mqp + (ri - b * p.T);
 #pragma unroll
           for (int q = 0; q < NP; ++q) x[k][q] = as_f4(bload(rh, fpiece(grow, 4 * (c.lane + 64 * q), c.RT), 0));
@@ -2137,7 +2208,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
         wave_sum_n<R>(ss);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-          const int ri = min(r0 + NWAVES * k, nrows - 1);
+          const int ri = min(r0 + NWAVES * k, r_hi - 1);
           const float rs = rsqrtf(ss[k] * (1.0f / (float)S::H) + p.eps);
           const float* ml = tail_mods_lds(c, ri / p.T);
 #pragma unroll
@@ -2175,7 +2246,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
 #pragma unroll
             for (int k = 0; k < R; ++k) {
               const int ri = r0 + NWAVES * k;
-              if (ri >= nrows) continue;
+              if (ri >= r_hi) continue;
               if (inproj) {
                 xp[ri * adim + c.lane] = xc[k] + c.dt * (sel[k] + bo);
               } else {
@@ -2255,11 +2326,18 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
     // dims for an in-projection task)
     char* mb = c.smem + S::MODS;
     const int tout = task_first(c, PL_TOUT);
-    const bool tin = task_first(c, PL_TIN) < (d.last ? 0 : S::NIN);
-    if (!d.first && (tin || tout < (p.A + TAIL_AC - 1) / TAIL_AC)) {
+    // (the row-wise form's in-projection tasks read x after the step instead)
+    const bool tin = !S::RW && task_first(c, PL_TIN) < (d.last ? 0 : S::NIN);
+    if (!d.first && (tin || tout < tail_nout<S>(p))) {
       for (int b = 0; b < p.B; ++b) dma_f32(c, mb + b * 2 * S::H * 4, c.modrow(b, d.s) + 9 * p.L * S::H, 2 * S::H);
-      if (tin) dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
-      else dma_f32(c, c.smem + S::WBUF, p.wout + (long long)tout * TAIL_AC * S::H, min(TAIL_AC, p.A - tout * TAIL_AC) * S::H);
+      if (tin) {
+        dma_f32(c, c.smem + S::WBUF, p.wout, p.action_dim * S::H);
+      } else if constexpr (S::RW) {
+        const int a_lo = (tout % ((p.A + TAIL_DG - 1) / TAIL_DG)) * TAIL_DG;
+        dma_f32(c, c.smem + S::WBUF, p.wout + (long long)a_lo * S::H, min(TAIL_DG, p.A - a_lo) * S::H);
+      } else {
+        dma_f32(c, c.smem + S::WBUF, p.wout + (long long)tout * TAIL_AC * S::H, min(TAIL_AC, p.A - tout * TAIL_AC) * S::H);
+      }
     }
   } else {
     const int t = task_first(c, d.pk);
@@ -2315,7 +2393,7 @@ template <class S>
 __device__ __forceinline__ unsigned task_mask(Ctx<S>& c) {
   CP& p = c.p;
   if (c.wg == 0) return ~0u;
-  const int nattn = attn_count(p.Mqp / 16, p.B * S::NH), nout = (p.A + TAIL_AC - 1) / TAIL_AC;
+  const int nattn = attn_count(p.Mqp / 16, p.B * S::NH), nout = tail_nout<S>(p);
   unsigned m = 0;
   if (task_first(c, PL_QKV) < 6 * S::NH * p.rgs_qkv) m |= 1u << ST_QKV;
   if (task_first(c, PL_SA) < nattn) m |= 1u << ST_SA;
@@ -2344,7 +2422,7 @@ __device__ __forceinline__ StagePos next_stage(unsigned mask, StagePos q, int to
 // ------------------------------------------------------------------------------------------------
 template <int H, int I, bool W8, bool ROWWISE>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
-  using S = Shape<H, I, W8>;
+  using S = Shape<H, I, W8, ROWWISE>;
   __shared__ __attribute__((aligned(1024))) char smem[S::LDS];
   CP& p = *(CP*)(__builtin_amdgcn_kernarg_segment_ptr());
   Ctx<S> c(p, smem);
@@ -2394,7 +2472,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       if (cur.st == ST_SA) sa_stage(c, cur, s_ks, bc, g);
       else if (cur.st == ST_CA) ca_stage(c, cur, s_ks, bc, g);
       else if (cur.st == ST_TAIL) tail_stage(c, cur, bc, g);
-      else if constexpr (ROWWISE) gemm_stage_rows(c, cur, bc, g);
+      else if constexpr (S::RW) gemm_stage_rows(c, cur, bc, g);
       else gemm_stage(c, cur, bc, g);
       if (g == 0) {
         transpose_caches(c, s_ks);
