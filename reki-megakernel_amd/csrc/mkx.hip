@@ -162,10 +162,11 @@ struct Layout {
 int tail_outputs(bool rows, int nrows, int A) {
   return rows ? (nrows + TAIL_RCH - 1) / TAIL_RCH * ((A + TAIL_DG - 1) / TAIL_DG) : (A + TAIL_AC - 1) / TAIL_AC;
 }
-Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A, int nout) {
+// nqt: query tiles per sample; rows: the row-wise form (tasks of one column tile)
+Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A, int nout, bool rows) {
   Layout L{};
   const int nattn = B * k.NH * nqt, mods = B * 2 * H * 4;
-  const bool wide = k.NTW > 1 && k.W_WIDE + std::max(k.RED_WIDE, k.RED_NARROW) + mods <= k.SMALL;
+  const bool wide = !rows && k.NTW > 1 && k.W_WIDE + std::max(k.RED_WIDE, k.RED_NARROW) + mods <= k.SMALL;
   const int nt = wide ? k.NTW : 1;
   auto clampi = [](int v, int lo, int hi) { return std::max(lo, std::min(hi, v)); };
   const int ndown_d = (k.HT / nt) * k.SK, nred_d = k.HT / nt;
@@ -542,14 +543,12 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   // the GEMM stages stage every sample's modulation slices (2 H floats) in 56 KB.
   if ((long long)a->B * 2 * H * 4 > 56 * 1024) return fail(MKX_EUNSUPPORTED, "batch too large to stage its modulation slices in LDS");
   const ShapeK sk = shape_k(H, I, h->w8 != 0);
-  Layout lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(false, a->B * a->T_act, d.A));
-  // Row-wise GEMM stages where a gate/up task would need more than one pass of row tiles (the form takes
-  // gated-residual and down-projection tasks of one column tile, and its step tail's output tasks, over row
-  // chunks, must number at most 64)
-  const bool one_tile = lay.nt_o == 1 && lay.nt_cao == 1 && lay.nt_down == 1;
-  const bool rows = one_tile && tail_outputs(true, a->B * a->T_act, d.A) <= 64 &&
+  Layout lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(false, a->B * a->T_act, d.A), false);
+  // Row-wise form where a gate/up task would need more than one pass of row tiles (its layout has tasks of one
+  // column tile, and its step tail's output tasks, over row chunks, must number at most 64)
+  const bool rows = tail_outputs(true, a->B * a->T_act, d.A) <= 64 &&
                     (h->gemm_form == 1 || (h->gemm_form < 0 && NRP / 16 > sk.RBMAX));
-  if (rows) lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(true, a->B * a->T_act, d.A));
+  if (rows) lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(true, a->B * a->T_act, d.A), true);
   {
     // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes): gate/up on every CA out-projection
     // task, an out-projection task on every head of its rows; and on at most 64 (one load per poll) where

@@ -187,6 +187,19 @@ def test_tiny_fp8_gelu_rowwise():
         _check_loop("tiny fp8 gelu (row-wise GEMMs)", make_case(replace(TINY, B=3, weight_dtype="fp8_e4m3", act="gelu_tanh")))
 
 
+def test_batch_of_eight_long_source_rowwise():
+    # batch 8 at H 768 in the row-wise form with 520 source rows: the cross-attention K/V are streamed through
+    # the LDS ring, and the workgroups with two attention tasks stream them once per task
+    from dataclasses import replace
+    _check_loop("b8 S 520 (row-wise, tile pairs, streamed source)", make_case(replace(SY.WORKLOADS["B"], L=2, S=520, SP=520)))
+
+
+def test_config_A_rowwise_form():
+    # the headline shape forced into the row-wise form (one-tile tasks, row-wise GEMMs and step tail)
+    with _gemm_form("rows"):
+        _check_loop("A (row-wise form)", make_case(SY.WORKLOADS["A"]))
+
+
 def test_tiny_single_row_tile_rowwise():
     # one row tile per sample: groups of two row tiles whose second repeats the first and stores nothing
     with _gemm_form("rows"):
