@@ -763,14 +763,39 @@ int source_args_check(const mkx_source* h, const mkx_source_args* a, const char*
   return MKX_OK;
 }
 
+// Row tiles per wave of prepare_source_kernel for nrows source rows: the one whose busiest CU has the least
+// work, counting a workgroup's fixed cost (its first k-blocks in flight, the epilogue) as one row tile.
+int prep_rtw(int nrows, int ncol_groups) {
+  int dev = 0, ncu = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    hipDeviceProp_t pr;
+    if (hipGetDeviceProperties(&pr, dev) == hipSuccess && pr.multiProcessorCount > 0) ncu = pr.multiProcessorCount;
+  }
+  const int nrt = (nrows + 15) / 16;
+  int best = 2;
+  long long best_cost = -1;
+  for (int rtw = 2; rtw <= 5; ++rtw) {
+    const long long nwg = (long long)((nrt + 2 * rtw - 1) / (2 * rtw)) * ncol_groups;
+    const long long cost = (nwg + ncu - 1) / ncu * (rtw + 1);
+    if (best_cost < 0 || cost < best_cost) { best_cost = cost; best = rtw; }
+  }
+  return best;
+}
+// Packed context bytes of a preparation of nrows rows (padded to a whole workgroup of the largest kind)
+long long prep_ctx_bytes(int nrows, int C) { return (long long)((nrows + 31) / 32 * 32 + PREP_ROW_PAD) * C * 2; }
+
 // The two launches of a source preparation, the packed context staged at ctxp.
 int source_launch(const mkx_source* h, const mkx_source_args* a, bf16_t* ctxp, hipStream_t stream) {
   const mkx_source_dims& d = h->dims;
   const int nrows = a->B * a->SP;
-  const int tiles = (nrows + 63) / 64;
-  const long long n_x = (long long)tiles * 64 * d.C / 8;  // packed pieces, rows padded to 64 with zeros
+  const int np = (d.NH + 1) / 2, ncg = d.L * 2 * np;
+  const int rtw = prep_rtw(nrows, ncg), wg_rows = 32 * rtw;
+  const int ngroups = (nrows + wg_rows - 1) / wg_rows;
+  // packed pieces: rows padded with zeros to whole workgroups
+  const long long n_x = (long long)ngroups * wg_rows * d.C / 8;
+  // packed in groups of a workgroup's 2 rtw row tiles, so that one k-block of a workgroup's rows is contiguous
   hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)((n_x + 255) / 256)), dim3(256), 0, stream, (const bf16_t*)a->ctx,
-                     ctxp, nrows, d.C, 1, n_x);
+                     ctxp, nrows, d.C, 2 * rtw, n_x);
   SourceParams p{};
   p.L = d.L; p.NH = d.NH; p.C = d.C; p.B = a->B; p.SP = a->SP;
   p.ctxp = ctxp; p.wkp = h->wkp; p.wvp = h->wvp; p.k_norm = h->kn;
@@ -778,8 +803,13 @@ int source_launch(const mkx_source* h, const mkx_source_args* a, bf16_t* ctxp, h
   for (int l = 0; l < d.L; ++l) { p.kca[l] = a->kca[l]; p.vca[l] = a->vca[l]; }
   p.src_sb = a->src_stride_b;
   p.eps = d.eps;
-  hipLaunchKernelGGL(prepare_source_kernel, dim3((unsigned)tiles, (unsigned)(d.L * 2 * d.NH)), dim3(PREP_BLOCK), 0,
-                     stream, p);
+  const dim3 grid((unsigned)ngroups, (unsigned)ncg);
+  switch (rtw) {
+    case 2: hipLaunchKernelGGL(prepare_source_kernel<2>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
+    case 3: hipLaunchKernelGGL(prepare_source_kernel<3>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(prepare_source_kernel<4>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
+    default: hipLaunchKernelGGL(prepare_source_kernel<5>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
+  }
   HIPCHK(hipGetLastError());
   return MKX_OK;
 }
@@ -805,13 +835,12 @@ int mkx_source_create(const mkx_source_dims* d, const void* wk, const void* wv, 
   mkx_source* h = new mkx_source();
   h->dims = *d;
   const int64_t wel = (int64_t)d->L * d->NH * 64 * d->C;
-  const int64_t rows_pad = ((int64_t)d->max_rows + 63) / 64 * 64;
   auto cleanup = [&](int code, const std::string& msg) {
     free_source(h);
     return fail(code, msg);
   };
   if (hipMalloc(&h->wkp, wel * 2) != hipSuccess || hipMalloc(&h->wvp, wel * 2) != hipSuccess ||
-      hipMalloc(&h->kn, (size_t)d->L * 64 * 2) != hipSuccess || hipMalloc(&h->ctxp, rows_pad * d->C * 2) != hipSuccess)
+      hipMalloc(&h->kn, (size_t)d->L * 64 * 2) != hipSuccess || hipMalloc(&h->ctxp, (size_t)prep_ctx_bytes(d->max_rows, d->C)) != hipSuccess)
     return cleanup(MKX_ENOMEM, "mkx_source_create: device allocation failed");
   // weights in fragment order: 16-row groups of one head (S = 4) per head of every layer
   const long long n_w = wel / 8;
@@ -846,7 +875,7 @@ int mkx_source_run(mkx_source* h, const mkx_source_args* a, void* stream_) {
 int mkx_source_run_noalloc(mkx_source* h, const mkx_source_args* a, void* stream_) {
   const int rc = source_args_check(h, a, "mkx_source_run_noalloc");
   if (rc != MKX_OK) return rc;
-  const long long need = (long long)((a->B * a->SP + 63) / 64) * 64 * h->dims.C * 2;
+  const long long need = prep_ctx_bytes(a->B * a->SP, h->dims.C);
   if (need > SOURCE_SCRATCH_BYTES)
     return fail(MKX_EINVAL, "mkx_source_run_noalloc: the packed context (" + std::to_string(need) +
                                 " bytes) exceeds the static scratch of " + std::to_string(SOURCE_SCRATCH_BYTES) + " bytes");

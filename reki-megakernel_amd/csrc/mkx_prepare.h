@@ -4,15 +4,15 @@
 // past.cross_attn_kv (src/mk_expert.py:491-492), produced by REKI's register_prepare (README.md:279-281:
 // "the cross-attention K/V projections of the VLM source (31 M weights)").
 //
-// One workgroup = 64 source rows x one head (64 columns) of K or V of one layer; 4 waves of 16 rows. The
-// product runs on v_mfma_f32_16x16x32_bf16 with the weight rows as the first operand, so a lane ends with
-// 4 consecutive columns of each 16-column group for one source row: the RMS of a row is a sum over the
+// The product runs on v_mfma_f32_16x16x32_bf16 with the weight rows as the first operand, so a lane ends
+// with 4 consecutive columns of each 16-column group for one source row: the RMS of a row is a sum over the
 // lane's 16 values and two cross-lane swaps, and each column's RoPE partner (d +- 32) sits in the same
-// lane. Both operands are read in fragment order, one 1 KB contiguous block per wave and load: the
-// weights are packed so once at creation and the context at each call (pack_rows_kernel). Read in place,
-// the rows of a fragment sit C * 2 bytes apart and the same kernel ran 2.6x slower (221 us against 84 us
-// for 10 layers of a 300 x 2048 context). Chunks of 2 k-steps keep it at 80 VGPRs, so a whole grid of that
-// size is resident at once (75 us; chunks of 4: 132 VGPRs, 83 us).
+// lane. Both operands are read in fragment order, one contiguous 1 KB block per fragment: the weights are
+// packed so once at creation and the context at each call (pack_rows_kernel). A workgroup stages the
+// fragments of each k-block in LDS once and shares them between its waves (below); when every wave streamed
+// its own weight fragments from memory (64 rows x one head per workgroup, no LDS), the four waves of a
+// workgroup read each weight fragment four times and the kernel took 75 us for 10 layers of a 300 x 2048
+// context, 10 % of the MFMA peak.
 #pragma once
 
 #include "mkx.h"
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const bf16_t* __restrict
 
 struct SourceParams {
   int L, NH, C, B, SP;
-  const bf16_t* ctxp;   // context in fragment order, S = 1, rows padded to a multiple of 64
+  const bf16_t* ctxp;   // context in fragment order, S = 2 RTW (one group per workgroup), rows padded to whole groups
   const bf16_t* wkp;    // K weights in fragment order, S = 4 (16-row groups of one head)
   const bf16_t* wvp;
   const bf16_t* k_norm; // [L, 64]
@@ -55,105 +55,153 @@ struct SourceParams {
   float eps;
 };
 
-// grid: x = ceil(B * SP / 64) row tiles, y = (layer * 2 + (0: K, 1: V)) * NH + head
+// Row tiles of 16 per wave (the workgroup covers 2 * RTW of them, 32 * RTW rows) and k-blocks of 32 staged
+// ahead in LDS: the packed context is padded to PREP_ROW_PAD more rows than the largest workgroup covers.
+constexpr int PREP_ROW_PAD = 32 * 5;
+// LDS ring stages of prepare_source_kernel<RTW>: as many as 140 KB hold
+__host__ __device__ constexpr int prep_nstage(int rtw) { return 140 * 1024 / (4 * ((2 * rtw + 8 + 3) / 4) * 1024) < 8 ? 140 * 1024 / (4 * ((2 * rtw + 8 + 3) / 4) * 1024) : 8; }
+
+// grid: x = row groups of 32 * RTW rows, y = (layer * 2 + (0: K, 1: V)) * ceil(NH / 2) + head pair.
+// Workgroup = 32 RTW source rows x two heads (128 columns) of K or V of one layer; wave (wr, wc) computes
+// rows [16 RTW wr, 16 RTW (wr + 1)) of head 2 * pair + wc. Every k-block's operand fragments (2 RTW context
+// fragments, 8 weight fragments, each a contiguous 1 KB block) are DMA'd into an LDS ring of PREP_NSTAGE
+// stages, PREP_NSTAGE - 1 k-blocks ahead of the MFMAs, so each weight fragment is read from memory once per
+// workgroup and shared by its 2 RTW row tiles, and each context fragment is shared by the two heads. Per
+// k-block a wave reads RTW + 4 fragments from LDS for 4 RTW MFMAs. The products are accumulated over k in
+// order, exactly as a single wave streaming its operands would.
+template <int RTW>
 __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int NH = a.NH, C = a.C;
-  const int h = blockIdx.y % NH, lk = blockIdx.y / NH, l = lk >> 1, is_v = lk & 1;
+  constexpr int NXF = 2 * RTW, NF = NXF + 8;      // fragments per k-block: context, then weights
+  constexpr int ND = (NF + 3) / 4;                // DMAs per wave and k-block (the last ones may be dummies)
+  constexpr int STAGE = (4 * ND) * 1024;          // bytes per stage (a dummy DMA lands past the real ones)
+  constexpr int PREP_NSTAGE = prep_nstage(RTW);
+  __shared__ __attribute__((aligned(1024))) char sm[PREP_NSTAGE * STAGE];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
+  const int NH = a.NH, C = a.C, T = C / 32, NP = (NH + 1) / 2;
+  const int pair = blockIdx.y % NP, lk = blockIdx.y / NP, l = lk >> 1, is_v = lk & 1;
+  const int h = min(2 * pair + wc, NH - 1);
+  const bool head_ok = 2 * pair + wc < NH;
   const int nrows = a.B * a.SP;
-  const int row = blockIdx.x * 64 + wave * 16 + (lane & 15);
-  const int rowc = min(row, nrows - 1);  // rows past the end (zero in the packed context) are not stored
-  const int T = C / 32;
-  const bf16_t* xp = a.ctxp + ((int64_t)(blockIdx.x * 4 + wave) * T * 64 + lane) * 8;
-  const bf16_t* wbase = (is_v ? a.wvp : a.wkp) + ((int64_t)(l * NH + h) * T * 4 * 64 + lane) * 8;
-  f32x4 acc[4];
+  const int g0 = blockIdx.x * NXF;  // first 16-row tile of the workgroup
+  const bf16_t* wsrc = is_v ? a.wvp : a.wkp;
+  // this wave's DMA sources of k-block 0 (fragment f = wave + 4 i; f >= NF: a dummy copy of fragment 0) and the
+  // element stride between consecutive k-blocks (context: 1 KB, weights: 4 KB per k-block)
+  const bf16_t* src[ND];
+  int kstride[ND];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // k in chunks of KU steps of 32, two chunks in flight: the loads of chunk c + 1 are issued before the
-  // MFMAs of chunk c. Steps past C load the last valid step (in bounds) and multiply a zeroed context
-  // fragment, so every wave runs the same straight-line code.
-  constexpr int KU = 2;
-  u32x4 xs[2][KU], ws[2][KU][4];
-  auto load = [&](int buf, int k0) {
-#pragma unroll
-    for (int u = 0; u < KU; ++u) {
-      const int k = min(k0 + 32 * u, C - 32);
-      xs[buf][u] = ld16(xp + (int64_t)(k / 32) * 64 * 8);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ws[buf][u][j] = ld16(wbase + ((int64_t)(k / 32) * 4 + j) * 64 * 8);
+  for (int i = 0; i < ND; ++i) {
+    const int f = wave + 4 * i;
+    if (f < NXF) {
+      src[i] = a.ctxp + (((int64_t)blockIdx.x * T * NXF + f) * 64 + lane) * 8;
+      kstride[i] = NXF * 64 * 8;
+    } else if (f < NF) {
+      const int hw = min(2 * pair + (f - NXF) / 4, NH - 1), j = (f - NXF) & 3;
+      src[i] = wsrc + (((int64_t)(l * NH + hw) * T * 4 + j) * 64 + lane) * 8;
+      kstride[i] = 4 * 64 * 8;
+    } else {
+      src[i] = a.ctxp + ((int64_t)blockIdx.x * T * NXF * 64 + lane) * 8;
+      kstride[i] = NXF * 64 * 8;
     }
-  };
-  auto mma = [&](int buf, int k0) {
-#pragma unroll
-    for (int u = 0; u < KU; ++u) {
-      const bool in = k0 + 32 * u < C;
-      u32x4 xv = xs[buf][u];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xv[e] = in ? xv[e] : 0u;
-      const bf16x8 xf = __builtin_bit_cast(bf16x8, xv);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = mfma16(__builtin_bit_cast(bf16x8, ws[buf][u][j]), xf, acc[j]);
-    }
-  };
-  constexpr int CH = 32 * KU;
-  load(0, 0);
-  for (int k0 = 0; k0 < C; k0 += 2 * CH) {
-    load(1, k0 + CH);
-    mma(0, k0);
-    load(0, k0 + 2 * CH);
-    mma(1, k0 + CH);
   }
-  // lane holds columns d = 16 j + 4 (lane >> 4) + i of source row `row`
-  const int b = rowc / a.SP, s = rowc - b * a.SP;
-  const bool live = s < min(max(a.ca_len[b], 0), a.SP);
-  float y[4][4];
+  auto issue = [&](int kb) {
+    const int k = min(kb, T - 1);  // k-blocks past the end reload the last one into a stage never read
+    char* st = sm + (kb % PREP_NSTAGE) * STAGE;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+    for (int i = 0; i < ND; ++i) dma16(src[i] + (int64_t)k * kstride[i], st + (wave + 4 * i) * 1024);
+  };
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[j][i] = rbf(acc[j][i]);
+  for (int s = 0; s < PREP_NSTAGE - 1; ++s) issue(s);
+  f32x4 acc[RTW][4];
+#pragma unroll
+  for (int rt = 0; rt < RTW; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[rt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < T; ++kb) {
+    // this wave's DMAs of k-block kb have landed (those of the PREP_NSTAGE - 2 later k-blocks may not have);
+    // after the barrier every wave's have, and every wave is done reading the stage of k-block kb - 1
+    wait_vm_le<(PREP_NSTAGE - 2) * ND>();
+    exec_barrier();
+    issue(kb + PREP_NSTAGE - 1);
+    const char* st = sm + (kb % PREP_NSTAGE) * STAGE;
+    bf16x8 xf[RTW], wf[4];
+#pragma unroll
+    for (int rt = 0; rt < RTW; ++rt) xf[rt] = *reinterpret_cast<const bf16x8*>(st + (wr * RTW + rt) * 1024 + lane * 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wf[j] = *reinterpret_cast<const bf16x8*>(st + (NXF + wc * 4 + j) * 1024 + lane * 16);
+#pragma unroll
+    for (int rt = 0; rt < RTW; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[rt][j] = mfma16(wf[j], xf[rt], acc[rt][j]);
+  }
+  wait_vm0();  // no DMA is in flight when the workgroup ends
+  // the K norm weights of this lane's 16 columns d = 16 j + 4 (lane >> 4) + i (4 bf16 per j)
+  uint2 wnv[4];
   if (!is_v) {
-    float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) wnv[j] = *reinterpret_cast<const uint2*>(a.k_norm + l * 64 + 16 * j + 4 * (lane >> 4));
+  }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ss += y[j][i] * y[j][i];
-    ss = xor32_sum(xor16_sum(ss));
-    const float r = rsqrtf(ss / 64.f + a.eps);
-    const bf16_t* wn = a.k_norm + l * 64;
+  for (int rt = 0; rt < RTW; ++rt) {
+    // lane holds columns d = 16 j + 4 (lane >> 4) + i of source row `row`
+    const int row = (g0 + wr * RTW + rt) * 16 + (lane & 15);
+    const int rowc = min(row, nrows - 1);  // rows past the end (zero in the packed context) are not stored
+    const int b = rowc / a.SP, s = rowc - b * a.SP;
+    // the row's loads are issued together: its sample's valid length and its RoPE table entries
+    const int cal = a.ca_len[b];
+    f32x4 csv[4], snv[4];
+    if (!is_v) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 16 * j + 4 * (lane >> 4) + i;
-        y[j][i] = rbf(y[j][i] * r * (1.f + bf2f(wn[d])));
+      for (int j = 0; j < 4; ++j) {
+        csv[j] = *reinterpret_cast<const f32x4*>(a.cos + (int64_t)s * 64 + 16 * j + 4 * (lane >> 4));
+        snv[j] = *reinterpret_cast<const f32x4*>(a.sin + (int64_t)s * 64 + 16 * j + 4 * (lane >> 4));
       }
-    const float* cs = a.cos + (int64_t)s * 64;
-    const float* sn = a.sin + (int64_t)s * 64;
-    float z[4][4];
-    {
-#pragma clang fp contract(off)
+    }
+    float y[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[j][i] = rbf(acc[rt][j][i]);
+    if (!is_v) {
+      float ss = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = 16 * j + 4 * (lane >> 4) + i;
-          const float rot = j < 2 ? -y[j + 2][i] : y[j - 2][i];
-          z[j][i] = rbf(y[j][i] * cs[d] + rot * sn[d]);
-        }
+        for (int i = 0; i < 4; ++i) ss += y[j][i] * y[j][i];
+      ss = xor32_sum(xor16_sum(ss));
+      const float r = rsqrtf(ss / 64.f + a.eps);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float wv[4] = {__uint_as_float(wnv[j].x << 16), __uint_as_float(wnv[j].x & 0xffff0000u),
+                             __uint_as_float(wnv[j].y << 16), __uint_as_float(wnv[j].y & 0xffff0000u)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[j][i] = rbf(y[j][i] * r * (1.f + wv[i]));
+      }
+      float z[4][4];
+      {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float rot = j < 2 ? -y[j + 2][i] : y[j - 2][i];
+            z[j][i] = rbf(y[j][i] * csv[j][i] + rot * snv[j][i]);
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[j][i] = z[j][i];
     }
+    const bool live = s < min(max(cal, 0), a.SP);
+    if (row >= nrows || !head_ok) continue;
+    bf16_t* out = (bf16_t*)(is_v ? a.vca[l] : a.kca[l]) + (int64_t)b * a.src_sb + ((int64_t)s * NH + h) * 64;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) y[j][i] = z[j][i];
-  }
-  if (row >= nrows) return;
-  bf16_t* out = (bf16_t*)(is_v ? a.vca[l] : a.kca[l]) + (int64_t)b * a.src_sb + ((int64_t)s * NH + h) * 64;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    u32x2 v;
-    v[0] = live ? pack2(y[j][0], y[j][1]) : 0u;
-    v[1] = live ? pack2(y[j][2], y[j][3]) : 0u;
-    *reinterpret_cast<u32x2*>(out + 16 * j + 4 * (lane >> 4)) = v;
+    for (int j = 0; j < 4; ++j) {
+      u32x2 v;
+      v[0] = live ? pack2(y[j][0], y[j][1]) : 0u;
+      v[1] = live ? pack2(y[j][2], y[j][3]) : 0u;
+      *reinterpret_cast<u32x2*>(out + 16 * j + 4 * (lane >> 4)) = v;
+    }
   }
 }
 
