@@ -98,10 +98,17 @@ def rounder(mode: str):
 
 
 def operand_rounder(mode: str):
-    """Rounding of the GEMM operands: fp16 round trip (round to nearest even) in ``f16`` mode, identity
-    otherwise."""
+    """Rounding of the GEMM operands: fp16 round trip (round to nearest even) in ``f16`` mode; in ``f8``
+    mode fp8 e4m3 with one absmax scale per row (per token: the finest scaling an fp8 MFMA with
+    per-row epilogue scales could apply), which gives the error an fp8-activation kernel would have;
+    identity otherwise."""
     if mode == "f16":
         return lambda t: t.to(torch.float16).to(t.dtype)
+    if mode == "f8":
+        def f8(t):
+            s = t.abs().amax(-1, keepdim=True).clamp_min(1e-30) / 448.0
+            return (t / s).to(torch.float8_e4m3fn).to(t.dtype) * s
+        return f8
     return lambda t: t
 
 
@@ -179,7 +186,7 @@ def layer_forward(h: torch.Tensor, l: int, W: dict, mrow: torch.Tensor, cache: d
     def ada(x, sc, sh):
         # AdaRMS as a GEMM operand: mode f16 rounds the unnormalised operand and the shift where the kernel
         # stores them (rstd(x) is applied to the product; AdaRMS is linear in both)
-        if mode == "f16":
+        if mode in ("f16", "f8"):
             return rstd(x, d.eps) * Q(x * (1.0 + sc)) + Q(sh)
         return adarms(x, sc, sh, d.eps, R)
 
