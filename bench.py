@@ -168,14 +168,14 @@ def modulations_bench(cfg, n: int) -> int:
 
 
 def expert_call_bench(cfg, n: int, name: str) -> int:
-    """Times one whole expert call as a policy step runs it, on this library's kernels: the modulation
-    MLP (small layers in PyTorch, the MODW-wide projection on mkx_modulations), the cross-attention source
-    caches (mkx_source_run), Euler steps 1..N in one launch (run_all) and the register-memory append
-    (mkx_ring_append); beside it the same call with the modulations and source caches in PyTorch and
-    step 1 as its own launch (the reference's split, src/mk_expert.py:527-533)."""
+    """Times one whole expert call as a policy step runs it, on this library's kernels: the step
+    modulations (mkx_modulation_input: timestep embedding and the small MLP; mkx_modulations: the MODW-wide
+    projection), the cross-attention source caches (mkx_source_run), Euler steps 1..N in one launch (run_all)
+    and the register-memory append (mkx_ring_append); beside it the same call with the modulations and
+    source caches in PyTorch and step 1 as its own launch (the reference's split, src/mk_expert.py:527-533)."""
     import torch
     from mkx import ExpertMegakernel, synthetic as SY
-    from mkx.modulations import ModulationProjection
+    from mkx.modulations import StepModulations
     from mkx.prepare import SourcePrepare
 
     dev = torch.device("cuda:0")
@@ -186,14 +186,12 @@ def expert_call_bench(cfg, n: int, name: str) -> int:
     noise, ctx, sc = inp["noise"].to(dev), inp["ctx"].to(dev), inp["state_cond"].to(dev)
     mk = ExpertMegakernel(model)
     prep = SourcePrepare(model)
-    proj = ModulationProjection(W["mod_w"].to(dev), W["mod_b"].float().to(dev))
+    step_mods = StepModulations(*(W[k].to(dev) for k in ("t1_w", "t1_b", "t2_w", "t2_b", "mod_w", "mod_b")))
     ring = model.register_ring(past)
-    dt = torch.full((1,), -1.0 / cfg.num_steps, device=dev)
     ca_len = [cfg.S] * cfg.B
 
     def kernels():
-        mods = proj(model.modulation_input(cfg.num_steps, sc))
-        mods = mods[0] if cfg.B == 1 else mods
+        mods, dt = step_mods(cfg.num_steps, sc)
         cross = prep(ctx, ca_len)
         past.cross_attn_kv = [(k[0], v[0]) for k, v in cross] if cfg.B == 1 else cross
         x, ck, cv = mk.run_all(noise, mods, dt, past, cfg.action_dim)

@@ -269,6 +269,29 @@ typedef struct {
 
 int mkx_modulations(const mkx_modproj_args* args, void* stream);
 
+/* Modulation input: c[b][k] = silu(temb(t_k) W1^T + b1) W2^T + b2 + state_cond[b] for the Euler schedule
+ * t_k = 1 - k / N (k < N), temb(t) = [cos(1000 t f_i) | sin(1000 t f_i)], f_i = 10000^(-i / (tdim / 2)): the small
+ * MLP whose output mkx_modulations projects, the rest of REKI's _step_modulations (src/mk_expert.py:529:
+ * mods, dt = model._step_modulations(num_steps, state_cond)) in one launch. bf16 weights, fp32 biases, input
+ * and output; the embedding is computed in fp64 and rounded to fp32. Asynchronous. */
+typedef struct {
+  int32_t N;               /* Euler steps (rows per sample), 1 .. 4096 */
+  int32_t B;               /* samples, >= 1 */
+  int32_t H;               /* width: 256, 512, 768 or 1024 */
+  int32_t tdim;            /* embedding width: a multiple of 32, 32 .. 512 */
+  const void* t1_w;        /* [H, tdim] bf16, 16-byte aligned */
+  const float* t1_b;       /* [H] fp32, 16-byte aligned */
+  const void* t2_w;        /* [H, H] bf16, 16-byte aligned */
+  const float* t2_b;       /* [H] fp32, 16-byte aligned */
+  const float* state_cond; /* [B, sc_stride] fp32, 16-byte aligned */
+  int64_t sc_stride;       /* a multiple of 4, >= H */
+  float* out;              /* c: element (b, k, n) at b * out_stride_b + k * out_stride_k + n, 16-byte aligned */
+  int64_t out_stride_b;    /* multiples of 4 */
+  int64_t out_stride_k;
+} mkx_modin_args;
+
+int mkx_modulation_input(const mkx_modin_args* args, void* stream);
+
 int64_t mkx_query(const mkx_handle* h, int32_t key);
 int mkx_destroy(mkx_handle* h);
 const char* mkx_last_error(void);

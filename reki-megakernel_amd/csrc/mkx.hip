@@ -913,6 +913,25 @@ int mkx_modulations(const mkx_modproj_args* a, void* stream_) {
   return MKX_OK;
 }
 
+int mkx_modulation_input(const mkx_modin_args* a, void* stream_) {
+  if (!a) return fail(MKX_EINVAL, "mkx_modulation_input: args is NULL");
+  if (a->N < 1 || a->N > 4096 || a->B < 1 || a->B > (1 << 20))
+    return fail(MKX_EINVAL, "mkx_modulation_input: need 1 <= N <= 4096 and B >= 1");
+  if (a->H != 256 && a->H != 512 && a->H != 768 && a->H != 1024)
+    return fail(MKX_EUNSUPPORTED, "mkx_modulation_input: H must be 256, 512, 768 or 1024");
+  if (a->tdim < 32 || a->tdim > 32 * MODIN_MAX_TKB || (a->tdim & 31))
+    return fail(MKX_EUNSUPPORTED, "mkx_modulation_input: tdim must be a multiple of 32 in [32, 512]");
+  if (a->sc_stride < a->H || (a->sc_stride & 3) || (a->out_stride_k & 3) || (a->out_stride_b & 3) ||
+      a->out_stride_k < a->H || (a->B > 1 && a->out_stride_b < (int64_t)a->N * a->out_stride_k))
+    return fail(MKX_EINVAL, "mkx_modulation_input: strides must cover a row (and a sample) and be multiples of 4");
+  auto bad16 = [](const void* p) { return p == nullptr || ((uintptr_t)p & 15u) != 0; };
+  if (bad16(a->t1_w) || bad16(a->t1_b) || bad16(a->t2_w) || bad16(a->t2_b) || bad16(a->state_cond) || bad16(a->out))
+    return fail(MKX_EINVAL, "mkx_modulation_input: a pointer is NULL or not 16-byte aligned");
+  hipLaunchKernelGGL(modin_kernel, dim3((unsigned)(a->H / 64)), dim3(MODP_BLOCK), 0, (hipStream_t)stream_, *a);
+  HIPCHK(hipGetLastError());
+  return MKX_OK;
+}
+
 int mkx_check(mkx_handle* h, void* stream_) {
   if (!h) return fail(MKX_EINVAL, "null handle");
   HIPCHK(hipStreamSynchronize((hipStream_t)stream_));

@@ -15,7 +15,7 @@ Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WE
 
 EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
            "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append", "mkx_source_create", "mkx_source_run", "mkx_source_destroy",
-           "mkx_modulations", "mkx_set_spin_limit", "mkx_source_run_noalloc")
+           "mkx_modulations", "mkx_set_spin_limit", "mkx_source_run_noalloc", "mkx_modulation_input")
 
 _vp = ctypes.c_void_p
 
@@ -67,6 +67,13 @@ class MkxModprojArgs(ctypes.Structure):
                 ("w", _vp), ("bias", _vp), ("out", _vp), ("out_stride", ctypes.c_int64), ("w_fragment_order", ctypes.c_int32)]
 
 
+class MkxModinArgs(ctypes.Structure):
+    _fields_ = [("N", ctypes.c_int32), ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("tdim", ctypes.c_int32),
+                ("t1_w", _vp), ("t1_b", _vp), ("t2_w", _vp), ("t2_b", _vp), ("state_cond", _vp),
+                ("sc_stride", ctypes.c_int64), ("out", _vp), ("out_stride_b", ctypes.c_int64),
+                ("out_stride_k", ctypes.c_int64)]
+
+
 class MkxError(RuntimeError):
     def __init__(self, status: int, where: str, detail: str):
         super().__init__(f"{where}: mkx status {status} ({detail})")
@@ -102,6 +109,7 @@ def lib() -> ctypes.CDLL:
         L.mkx_source_run_noalloc.argtypes = [_vp, ctypes.POINTER(MkxSourceArgs), _vp]
         L.mkx_source_destroy.argtypes = [_vp]
         L.mkx_modulations.argtypes = [ctypes.POINTER(MkxModprojArgs), _vp]
+        L.mkx_modulation_input.argtypes = [ctypes.POINTER(MkxModinArgs), _vp]
         L.mkx_set_spin_limit.argtypes = [_vp, ctypes.c_uint32]
         _LIB = L
     return _LIB

@@ -81,7 +81,8 @@ def test_every_args_struct_matches_the_header_layout(tmp_path):
     import subprocess
     structs = {"mkx_dims": _lib.MkxDims, "mkx_weights": _lib.MkxWeights, "mkx_step_args": _lib.MkxStepArgs,
                "mkx_ring_args": _lib.MkxRingArgs, "mkx_source_dims": _lib.MkxSourceDims,
-               "mkx_source_args": _lib.MkxSourceArgs, "mkx_modproj_args": _lib.MkxModprojArgs}
+               "mkx_source_args": _lib.MkxSourceArgs, "mkx_modproj_args": _lib.MkxModprojArgs,
+               "mkx_modin_args": _lib.MkxModinArgs}
     lines = ['#include <stdio.h>', '#include "mkx.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
