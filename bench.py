@@ -188,7 +188,7 @@ def expert_call_bench(cfg, n: int, name: str) -> int:
     prep = SourcePrepare(model)
     step_mods = StepModulations(*(W[k].to(dev) for k in ("t1_w", "t1_b", "t2_w", "t2_b", "mod_w", "mod_b")))
     ring = model.register_ring(past)
-    ca_len = [cfg.S] * cfg.B
+    ca_len = torch.full((cfg.B,), cfg.S, dtype=torch.int32, device=dev)  # on the device: capturable
 
     def kernels():
         mods, dt = step_mods(cfg.num_steps, sc)
@@ -196,7 +196,8 @@ def expert_call_bench(cfg, n: int, name: str) -> int:
         past.cross_attn_kv = [(k[0], v[0]) for k, v in cross] if cfg.B == 1 else cross
         x, ck, cv = mk.run_all(noise, mods, dt, past, cfg.action_dim)
         ring.append_frame(ck, cv)
-        ring.update_past(past)
+        if not torch.cuda.is_current_stream_capturing():
+            ring.update_past(past)
         return x
 
     def torch_side():
@@ -221,8 +222,22 @@ def expert_call_bench(cfg, n: int, name: str) -> int:
 
     ms_k = timed(kernels)
     ms_t = timed(torch_side)
+    # the same call captured as one HIP graph (the ring append included; replays keep appending into the same
+    # buffer set, which changes nothing measured), replayed after a warm-up replay
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        kernels()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels()
+    ms_g = timed(graph.replay)
+    mk.check()
     print(json.dumps({"expert_call": {"workload": name, "calls": n,
-                                      "ms_median_kernels": round(ms_k, 3), "ms_median_pytorch_prep": round(ms_t, 3),
+                                      "ms_median_kernels": round(ms_k, 3), "ms_median_graph": round(ms_g, 3),
+                                      "ms_median_pytorch_prep": round(ms_t, 3),
                                       "parts": "modulations + source caches + steps 1-10 + ring append"}}), flush=True)
     return 0
 
