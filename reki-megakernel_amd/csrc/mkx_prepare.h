@@ -58,6 +58,7 @@ struct SourceParams {
 // Row tiles of 16 per wave (the workgroup covers 2 * RTW of them, 32 * RTW rows) and k-blocks of 32 staged
 // ahead in LDS: the packed context is padded to PREP_ROW_PAD more rows than the largest workgroup covers.
 constexpr int PREP_ROW_PAD = 32 * 5;
+constexpr int PREP_XCDS = 8;  // XCDs the dispatcher deals consecutive workgroups to
 // LDS ring stages of prepare_source_kernel<RTW>: as many as 140 KB hold
 __host__ __device__ constexpr int prep_nstage(int rtw) { return 140 * 1024 / (4 * ((2 * rtw + 8 + 3) / 4) * 1024) < 8 ? 140 * 1024 / (4 * ((2 * rtw + 8 + 3) / 4) * 1024) : 8; }
 
@@ -78,11 +79,18 @@ __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams
   __shared__ __attribute__((aligned(1024))) char sm[PREP_NSTAGE * STAGE];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
   const int NH = a.NH, C = a.C, T = C / 32, NP = (NH + 1) / 2;
-  const int pair = blockIdx.y % NP, lk = blockIdx.y / NP, l = lk >> 1, is_v = lk & 1;
+  // XCD-aware order: consecutive workgroups run on different XCDs (round-robin dispatch), so the linear index
+  // is regrouped to give each XCD a contiguous run of (column group, row group) tiles, row group fastest: the
+  // row groups of one column group then share its weight fragments (and the context rows) in their XCD's L2.
+  const int ngr = gridDim.x, nwg = ngr * gridDim.y, lin = blockIdx.y * ngr + blockIdx.x;
+  const int nfull = nwg - nwg % PREP_XCDS, per = nfull / PREP_XCDS;
+  const int tix = lin < nfull ? (lin % PREP_XCDS) * per + lin / PREP_XCDS : lin;
+  const int rg = tix % ngr, cgp = tix / ngr;
+  const int pair = cgp % NP, lk = cgp / NP, l = lk >> 1, is_v = lk & 1;
   const int h = min(2 * pair + wc, NH - 1);
   const bool head_ok = 2 * pair + wc < NH;
   const int nrows = a.B * a.SP;
-  const int g0 = blockIdx.x * NXF;  // first 16-row tile of the workgroup
+  const int g0 = rg * NXF;  // first 16-row tile of the workgroup
   const bf16_t* wsrc = is_v ? a.wvp : a.wkp;
   // this wave's DMA sources of k-block 0 (fragment f = wave + 4 i; f >= NF: a dummy copy of fragment 0) and the
   // element stride between consecutive k-blocks (context: 1 KB, weights: 4 KB per k-block)
@@ -92,14 +100,14 @@ __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams
   for (int i = 0; i < ND; ++i) {
     const int f = wave + 4 * i;
     if (f < NXF) {
-      src[i] = a.ctxp + (((int64_t)blockIdx.x * T * NXF + f) * 64 + lane) * 8;
+      src[i] = a.ctxp + (((int64_t)rg * T * NXF + f) * 64 + lane) * 8;
       kstride[i] = NXF * 64 * 8;
     } else if (f < NF) {
       const int hw = min(2 * pair + (f - NXF) / 4, NH - 1), j = (f - NXF) & 3;
       src[i] = wsrc + (((int64_t)(l * NH + hw) * T * 4 + j) * 64 + lane) * 8;
       kstride[i] = 4 * 64 * 8;
     } else {
-      src[i] = a.ctxp + ((int64_t)blockIdx.x * T * NXF * 64 + lane) * 8;
+      src[i] = a.ctxp + ((int64_t)rg * T * NXF * 64 + lane) * 8;
       kstride[i] = NXF * 64 * 8;
     }
   }
