@@ -126,22 +126,22 @@ def test_prepare_rejects_more_rows_than_the_handle_stages():
 
 
 def test_whole_call_captured_in_one_graph_replays_match_eager():
-    """Modulation projection, source caches and Euler steps 1..N captured as one HIP graph: every replay,
-    with eager work and a synchronisation between replays, equals the eager call bit for bit."""
-    from mkx.modulations import ModulationProjection
+    """Step modulations (modulation input and projection), source caches and Euler steps 1..N captured as one
+    HIP graph: every replay, with eager work and a synchronisation between replays, equals the eager call bit
+    for bit."""
+    from mkx.modulations import StepModulations
     case = make_case(SY.WORKLOADS["A"])
     cfg, model, past, W = case["cfg"], case["model"], case["past"], case["W"]
     mk = ExpertMegakernel(model)
     prep = SourcePrepare(model)
-    proj = ModulationProjection(W["mod_w"].cuda(), W["mod_b"].float().cuda())
+    step_mods = StepModulations(*(W[k].cuda() for k in ("t1_w", "t1_b", "t2_w", "t2_b", "mod_w", "mod_b")))
     sc = case["inp"]["state_cond"].cuda()
     ctx = case["inp"]["ctx"].cuda()
     ca_len = torch.tensor([cfg.S], dtype=torch.int32, device="cuda")
-    dt = torch.full((1,), -1.0 / cfg.num_steps, device="cuda")
     out = {}
 
     def call():
-        mods = proj(model.modulation_input(cfg.num_steps, sc))[0]
+        mods, dt = step_mods(cfg.num_steps, sc)
         past.cross_attn_kv = [(k[0], v[0]) for k, v in prep(ctx, ca_len)]
         out["x"], out["k"], out["v"] = mk.run_all(case["noise"], mods, dt, past, cfg.action_dim)
 
