@@ -128,3 +128,20 @@ def test_host_tensors_are_refused_before_any_launch():
         mk.run(torch.zeros(1, 2, 32), torch.zeros(2, 9 * 64 + 2 * 64), -0.1, past, 7)
     with pytest.raises(ValueError, match="GPU"):
         ModulationProjection(torch.zeros(32, 64), torch.zeros(32))
+    from mkx.modulations import StepModulations
+    with pytest.raises(ValueError, match="GPU"):
+        StepModulations(torch.zeros(256, 32), torch.zeros(256), torch.zeros(256, 256), torch.zeros(256),
+                        torch.zeros(2 * 256, 256), torch.zeros(2 * 256))
+
+
+def test_modulation_input_rejects_bad_arguments_without_launching():
+    L = _lib.lib()
+    assert L.mkx_modulation_input(None, None) == _lib.EINVAL
+    a = _lib.MkxModinArgs(N=10, B=1, H=768, tdim=256, sc_stride=768, out_stride_b=7680, out_stride_k=768)
+    assert L.mkx_modulation_input(ctypes.byref(a), None) == _lib.EINVAL  # NULL pointers
+    a.H = 640
+    assert L.mkx_modulation_input(ctypes.byref(a), None) == _lib.EUNSUPPORTED
+    a.H, a.tdim = 768, 48
+    assert L.mkx_modulation_input(ctypes.byref(a), None) == _lib.EUNSUPPORTED
+    a.tdim, a.N = 256, 0
+    assert L.mkx_modulation_input(ctypes.byref(a), None) == _lib.EINVAL
