@@ -56,6 +56,11 @@ def test_prepare_tiny():
     _check_prepare("prepare tiny (C 96, SP 48)", TINY)
 
 
+def test_prepare_odd_head_count():
+    # three heads: the workgroups take heads in pairs, so the last pair's second head is computed and not stored
+    _check_prepare("prepare NH 3 (odd head pair)", replace(TINY, H=192, NH=3, I=384))
+
+
 def test_prepare_config_A_context():
     _check_prepare("prepare A (L10, C 2048, S 300)", SY.WORKLOADS["A"])
 
