@@ -804,11 +804,17 @@ int source_launch(const mkx_source* h, const mkx_source_args* a, bf16_t* ctxp, h
   p.src_sb = a->src_stride_b;
   p.eps = d.eps;
   const dim3 grid((unsigned)ngroups, (unsigned)ncg);
+  // the production context width (2048) runs the fully unrolled k-loop
+  const bool c2048 = d.C == 2048;
   switch (rtw) {
-    case 2: hipLaunchKernelGGL(prepare_source_kernel<2>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
-    case 3: hipLaunchKernelGGL(prepare_source_kernel<3>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL(prepare_source_kernel<4>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
-    default: hipLaunchKernelGGL(prepare_source_kernel<5>, grid, dim3(PREP_BLOCK), 0, stream, p); break;
+    case 2: if (c2048) hipLaunchKernelGGL((prepare_source_kernel<2, 64>), grid, dim3(PREP_BLOCK), 0, stream, p);
+            else hipLaunchKernelGGL((prepare_source_kernel<2, 0>), grid, dim3(PREP_BLOCK), 0, stream, p); break;
+    case 3: if (c2048) hipLaunchKernelGGL((prepare_source_kernel<3, 64>), grid, dim3(PREP_BLOCK), 0, stream, p);
+            else hipLaunchKernelGGL((prepare_source_kernel<3, 0>), grid, dim3(PREP_BLOCK), 0, stream, p); break;
+    case 4: if (c2048) hipLaunchKernelGGL((prepare_source_kernel<4, 64>), grid, dim3(PREP_BLOCK), 0, stream, p);
+            else hipLaunchKernelGGL((prepare_source_kernel<4, 0>), grid, dim3(PREP_BLOCK), 0, stream, p); break;
+    default: if (c2048) hipLaunchKernelGGL((prepare_source_kernel<5, 64>), grid, dim3(PREP_BLOCK), 0, stream, p);
+             else hipLaunchKernelGGL((prepare_source_kernel<5, 0>), grid, dim3(PREP_BLOCK), 0, stream, p); break;
   }
   HIPCHK(hipGetLastError());
   return MKX_OK;

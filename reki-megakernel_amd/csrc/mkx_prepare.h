@@ -55,30 +55,30 @@ struct SourceParams {
   float eps;
 };
 
-// Row tiles of 16 per wave (the workgroup covers 2 * RTW of them, 32 * RTW rows) and k-blocks of 32 staged
-// ahead in LDS: the packed context is padded to PREP_ROW_PAD more rows than the largest workgroup covers.
+// Row tiles of 16 per wave (the workgroup covers 2 * RTW of them, 32 * RTW rows): the packed context is padded
+// to PREP_ROW_PAD more rows than the largest workgroup covers.
 constexpr int PREP_ROW_PAD = 32 * 5;
 constexpr int PREP_XCDS = 8;  // XCDs the dispatcher deals consecutive workgroups to
-// LDS ring stages of prepare_source_kernel<RTW>: as many as 140 KB hold
-__host__ __device__ constexpr int prep_nstage(int rtw) { return 140 * 1024 / (4 * ((2 * rtw + 8 + 3) / 4) * 1024) < 8 ? 140 * 1024 / (4 * ((2 * rtw + 8 + 3) / 4) * 1024) : 8; }
 
 // grid: x = row groups of 32 * RTW rows, y = (layer * 2 + (0: K, 1: V)) * ceil(NH / 2) + head pair.
 // Workgroup = 32 RTW source rows x two heads (128 columns) of K or V of one layer; wave (wr, wc) computes
-// rows [16 RTW wr, 16 RTW (wr + 1)) of head 2 * pair + wc. Every k-block's operand fragments (2 RTW context
-// fragments, 8 weight fragments, each a contiguous 1 KB block) are DMA'd into an LDS ring of PREP_NSTAGE
-// stages, PREP_NSTAGE - 1 k-blocks ahead of the MFMAs, so each weight fragment is read from memory once per
-// workgroup and shared by its 2 RTW row tiles, and each context fragment is shared by the two heads. Per
-// k-block a wave reads RTW + 4 fragments from LDS for 4 RTW MFMAs. The products are accumulated over k in
-// order, exactly as a single wave streaming its operands would.
-template <int RTW>
+// rows [16 RTW wr, 16 RTW (wr + 1)) of head 2 * pair + wc. Each k-block's operand fragments (2 RTW context
+// fragments, 8 weight fragments, each a contiguous 1 KB block) are loaded into registers PV k-blocks ahead,
+// each wave 16 bytes per lane of its share, then written to one of two LDS stages and shared by the waves:
+// each weight fragment is read from memory once per workgroup and shared by its 2 RTW row tiles, and each
+// context fragment serves the two heads. Per k-block a wave reads RTW + 4 fragments from LDS for 4 RTW
+// MFMAs. The products are accumulated over k in order, exactly as a single wave streaming its operands would.
+// TK > 0: the k-loop over TK k-blocks fully unrolled (the production context width), so that the compiler's
+// wait counts follow each k-block's loads instead of draining them at a loop head; TK = 0: any C / 32.
+template <int RTW, int TK>
 __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams a) {
   constexpr int NXF = 2 * RTW, NF = NXF + 8;      // fragments per k-block: context, then weights
-  constexpr int ND = (NF + 3) / 4;                // DMAs per wave and k-block (the last ones may be dummies)
-  constexpr int STAGE = (4 * ND) * 1024;          // bytes per stage (a dummy DMA lands past the real ones)
-  constexpr int PREP_NSTAGE = prep_nstage(RTW);
-  __shared__ __attribute__((aligned(1024))) char sm[PREP_NSTAGE * STAGE];
+  constexpr int ND = (NF + 3) / 4;                // fragments per wave and k-block (past NF: repeats of fragment 0)
+  constexpr int STAGE = (4 * ND) * 1024;          // bytes per LDS stage (a repeat lands past the real fragments)
+  constexpr int PV = 4;                           // k-blocks of loads in flight
+  __shared__ __attribute__((aligned(1024))) char sm[2 * STAGE];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wr = wave >> 1, wc = wave & 1;
-  const int NH = a.NH, C = a.C, T = C / 32, NP = (NH + 1) / 2;
+  const int NH = a.NH, C = a.C, T = TK > 0 ? TK : C / 32, NP = (NH + 1) / 2;
   // XCD-aware order: consecutive workgroups run on different XCDs (round-robin dispatch), so the linear index
   // is regrouped to give each XCD a contiguous run of (column group, row group) tiles, row group fastest: the
   // row groups of one column group then share its weight fragments (and the context rows) in their XCD's L2.
@@ -92,8 +92,8 @@ __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams
   const int nrows = a.B * a.SP;
   const int g0 = rg * NXF;  // first 16-row tile of the workgroup
   const bf16_t* wsrc = is_v ? a.wvp : a.wkp;
-  // this wave's DMA sources of k-block 0 (fragment f = wave + 4 i; f >= NF: a dummy copy of fragment 0) and the
-  // element stride between consecutive k-blocks (context: 1 KB, weights: 4 KB per k-block)
+  // this wave's fragment sources at k-block 0 (fragment f = wave + 4 i; f >= NF: a repeat of fragment 0) and
+  // the element stride between consecutive k-blocks
   const bf16_t* src[ND];
   int kstride[ND];
 #pragma unroll
@@ -111,26 +111,28 @@ __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams
       kstride[i] = NXF * 64 * 8;
     }
   }
-  auto issue = [&](int kb) {
-    const int k = min(kb, T - 1);  // k-blocks past the end reload the last one into a stage never read
-    char* st = sm + (kb % PREP_NSTAGE) * STAGE;
+  u32x4 rgb[PV][ND];
+  auto load = [&](int slot, int kb) {
+    const int k = min(kb, T - 1);  // k-blocks past the end reload the last one, never stored
 #pragma unroll
-    for (int i = 0; i < ND; ++i) dma16(src[i] + (int64_t)k * kstride[i], st + (wave + 4 * i) * 1024);
+    for (int i = 0; i < ND; ++i) rgb[slot][i] = ld16(src[i] + (int64_t)k * kstride[i]);
   };
 #pragma unroll
-  for (int s = 0; s < PREP_NSTAGE - 1; ++s) issue(s);
+  for (int s = 0; s < PV; ++s) load(s, s);
   f32x4 acc[RTW][4];
 #pragma unroll
   for (int rt = 0; rt < RTW; ++rt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[rt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < T; ++kb) {
-    // this wave's DMAs of k-block kb have landed (those of the PREP_NSTAGE - 2 later k-blocks may not have);
-    // after the barrier every wave's have, and every wave is done reading the stage of k-block kb - 1
-    wait_vm_le<(PREP_NSTAGE - 2) * ND>();
-    exec_barrier();
-    issue(kb + PREP_NSTAGE - 1);
-    const char* st = sm + (kb % PREP_NSTAGE) * STAGE;
+  // k-block kb: its fragments (loaded PV k-blocks earlier) into LDS stage kb % 2, the slot's next loads, a
+  // barrier (every wave's fragments of kb are in LDS; the stage written was last read at kb - 2, before the
+  // previous barrier), then the MFMAs
+  auto step = [&](int slot, int kb) {
+    char* st = sm + (kb & 1) * STAGE;
+#pragma unroll
+    for (int i = 0; i < ND; ++i) *reinterpret_cast<u32x4*>(st + (wave + 4 * i) * 1024 + lane * 16) = rgb[slot][i];
+    load(slot, kb + PV);
+    __syncthreads();
     bf16x8 xf[RTW], wf[4];
 #pragma unroll
     for (int rt = 0; rt < RTW; ++rt) xf[rt] = *reinterpret_cast<const bf16x8*>(st + (wr * RTW + rt) * 1024 + lane * 16);
@@ -140,8 +142,18 @@ __global__ __launch_bounds__(PREP_BLOCK) void prepare_source_kernel(SourceParams
     for (int rt = 0; rt < RTW; ++rt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[rt][j] = mfma16(wf[j], xf[rt], acc[rt][j]);
+  };
+  if constexpr (TK > 0) {
+#pragma unroll
+    for (int kb = 0; kb < TK; ++kb) step(kb % PV, kb);
+  } else {
+    for (int kb0 = 0; kb0 < T; kb0 += PV) {
+#pragma unroll
+      for (int u = 0; u < PV; ++u)
+        if (kb0 + u < T) step(u, kb0 + u);
+    }
   }
-  wait_vm0();  // no DMA is in flight when the workgroup ends
+  wait_vm0();  // no load is in flight when the workgroup ends
   // the K norm weights of this lane's 16 columns d = 16 j + 4 (lane >> 4) + i (4 bf16 per j)
   uint2 wnv[4];
   if (!is_v) {
