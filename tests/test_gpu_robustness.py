@@ -118,6 +118,8 @@ def test_boundary_timestamps_are_monotonic_and_inside_the_launch():
     assert diff(x, ref, cfg.action_dim)[0] <= 1e-3  # profiling changes no result
 
 
+# the refused capture records nothing, so torch reports its graph as empty: that is the expected outcome
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
 def test_scratch_growth_is_refused_under_and_after_capture():
     """A call that needs more scratch than the handle holds reallocates it. Under stream capture that is
     refused (MKX_EINVAL, nothing recorded); after a launch of the handle has been captured it is refused too
