@@ -908,12 +908,12 @@ int mkx_modulations(const mkx_modproj_args* a, void* stream_) {
   if (bad16(a->c) || bad16(a->w) || bad16(a->bias) || bad16(a->out))
     return fail(MKX_EINVAL, "mkx_modulations: c, w, bias, out: NULL or not 16-byte aligned");
   hipStream_t stream = (hipStream_t)stream_;
-  const dim3 grid((unsigned)((a->N / 16 + 3) / 4));
+  const dim3 grid((unsigned)((a->N / 16 + 3) / 4)), block(MODP_BLOCK * MODP_KSPLIT);
   switch (a->K / 32) {
-    case 8: hipLaunchKernelGGL(modproj_kernel<8>, grid, dim3(MODP_BLOCK), 8 * 64 * 32, stream, *a); break;
-    case 16: hipLaunchKernelGGL(modproj_kernel<16>, grid, dim3(MODP_BLOCK), 16 * 64 * 32, stream, *a); break;
-    case 24: hipLaunchKernelGGL(modproj_kernel<24>, grid, dim3(MODP_BLOCK), 24 * 64 * 32, stream, *a); break;
-    default: hipLaunchKernelGGL(modproj_kernel<32>, grid, dim3(MODP_BLOCK), 32 * 64 * 32, stream, *a); break;
+    case 8: hipLaunchKernelGGL(modproj_kernel<8>, grid, block, modproj_lds_bytes<8>(), stream, *a); break;
+    case 16: hipLaunchKernelGGL(modproj_kernel<16>, grid, block, modproj_lds_bytes<16>(), stream, *a); break;
+    case 24: hipLaunchKernelGGL(modproj_kernel<24>, grid, block, modproj_lds_bytes<24>(), stream, *a); break;
+    default: hipLaunchKernelGGL(modproj_kernel<32>, grid, block, modproj_lds_bytes<32>(), stream, *a); break;
   }
   HIPCHK(hipGetLastError());
   return MKX_OK;

@@ -3,13 +3,14 @@
 // (MODW = 9 L H + 2 H columns; the reference's kernel reads these rows, src/mk_expert.py:336-340, and
 // REKI's _step_modulations makes them, mk_expert.py:529).
 //
-// HBM-bound on W (bf16 [MODW, H]: 108.5 MB for L10 H768), so each weight byte is read once: a wave owns 16
-// output columns and holds their whole K extent as MFMA fragments in registers (H / 32 fragments of 16
-// bytes per lane), issued before anything else. The workgroup stages silu(c) of each 16-row tile once in
-// LDS, split into bf16 hi + lo parts in fragment order (two MFMAs per fragment, as exact as fp32 to ~2^-16
-// relative), and every wave sweeps the tile against its fragments. Computed per wave from global memory
-// instead, the 24 dependent loads of c per tile made the kernel latency-bound (69 us for 10 rows; 31 us
-// staged). Issuing the first tile's rows ahead of the weights changed nothing measurable.
+// HBM-bound on W (bf16 [MODW, H]: 108.5 MB for L10 H768), so each weight byte is read once: two waves own 16
+// output columns, each holding half their K extent as MFMA fragments in registers (H / 64 fragments of 16
+// bytes per lane), issued before anything else, and the second wave's partial sums are added through LDS. The
+// workgroup stages silu(c) of each 16-row tile once in LDS, split into bf16 hi + lo parts in fragment order
+// (two MFMAs per fragment, as exact as fp32 to ~2^-16 relative; silu with the hardware reciprocal and the
+// split with the packed bf16 conversion, since every workgroup repeats this work for every tile), and every
+// wave sweeps the tile against its fragments. Computed per wave from global memory instead, the 24 dependent
+// loads of c per tile made the kernel latency-bound (69 us for 10 rows; 31 us staged).
 #pragma once
 
 #include "mkx.h"
@@ -19,13 +20,22 @@ namespace mkx {
 
 constexpr int MODP_BLOCK = 256;
 constexpr int MODP_MAX_KT = 32;  // H <= 1024
+constexpr int MODP_KSPLIT = 2;   // waves sharing one 16-column tile, each over 1 / MODP_KSPLIT of K
+
+typedef float modp_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 modp_bf16x2 __attribute__((ext_vector_type(2)));
+
+// two floats rounded to nearest-even bf16 by the packed hardware conversion, low element in the low half
+__device__ __forceinline__ uint32_t modp_cvt2(float x, float y) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((modp_f32x2){x, y}, modp_bf16x2));
+}
 
 // silu(c) of one 16-row tile in bf16 hi + lo parts, in MFMA fragment order: [t][lane][8] per part
-template <int KT>
+template <int KT, int THREADS>
 __device__ __forceinline__ void modproj_stage(const mkx_modproj_args& a, int r0, char* lds) {
   constexpr int PIECES = KT * 64;
 #pragma unroll 1
-  for (int p = threadIdx.x; p < PIECES; p += MODP_BLOCK) {
+  for (int p = threadIdx.x; p < PIECES; p += THREADS) {
     const int t = p >> 6, ln = p & 63;
     const int r = min(r0 + (ln & 15), a.R - 1);  // rows past R stage a valid row, never stored
     const float* cp = a.c + (int64_t)r * a.c_stride + 32 * t + 8 * (ln >> 4);
@@ -35,53 +45,68 @@ __device__ __forceinline__ void modproj_stage(const mkx_modproj_args& a, int r0,
     u32x4 hi, lo;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v0 = g[2 * e] / (1.f + __expf(-g[2 * e]));  // silu
-      const float v1 = g[2 * e + 1] / (1.f + __expf(-g[2 * e + 1]));
-      const bf16_t h0 = f2bf(v0), h1 = f2bf(v1);
-      hi[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-      lo[e] = pack2(v0 - bf2f(h0), v1 - bf2f(h1));
+      const float v0 = g[2 * e] * __builtin_amdgcn_rcpf(1.f + __expf(-g[2 * e]));  // silu
+      const float v1 = g[2 * e + 1] * __builtin_amdgcn_rcpf(1.f + __expf(-g[2 * e + 1]));
+      const uint32_t h = modp_cvt2(v0, v1);
+      hi[e] = h;
+      lo[e] = modp_cvt2(v0 - __uint_as_float(h << 16), v1 - __uint_as_float(h & 0xffff0000u));
     }
     *reinterpret_cast<u32x4*>(lds + p * 16) = hi;
     *reinterpret_cast<u32x4*>(lds + (PIECES + p) * 16) = lo;
   }
 }
 
-// grid: N / 64 workgroups (rounded up) of 4 waves, each wave 16 output columns
+// dynamic LDS bytes of one projection workgroup: the staged tile (hi + lo)
 template <int KT>
-__global__ __launch_bounds__(MODP_BLOCK) void modproj_kernel(mkx_modproj_args a) {
+constexpr int modproj_lds_bytes() { return KT * 64 * 32; }
+
+// grid: N / 64 workgroups (rounded up) of 4 column tiles x MODP_KSPLIT waves; wave w owns columns
+// n0 .. n0 + 15 (tile w % 4) over k-blocks [KH (w / 4), KH (w / 4 + 1)), KH = KT / MODP_KSPLIT. Half the
+// weight fragments per wave fit 4 waves per SIMD, two workgroups per CU, for H <= 768 (all K in one wave held
+// 188 VGPRs: 2 waves), so more weight bytes are in flight and the waves finish in fewer rounds; H = 1024 keeps
+// 2 waves per SIMD (4 would spill).
+template <int KT>
+__global__ __launch_bounds__(MODP_BLOCK * MODP_KSPLIT, KT <= 24 ? 4 : 2) void modproj_kernel(mkx_modproj_args a) {
+  constexpr int KS = MODP_KSPLIT, KH = KT / KS, THREADS = MODP_BLOCK * KS;
+  static_assert(KT % KS == 0, "k-blocks split evenly");
   extern __shared__ __align__(16) char lds[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = (blockIdx.x * 4 + wave) * 16;
+  __shared__ f32x4 part[(KS - 1) * 4 * 64];  // partial sums of the upper K parts: [ks - 1][tile][lane]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ct = wave & 3, ks = wave >> 2;
+  const int n0 = (blockIdx.x * 4 + ct) * 16;
   const bool active = n0 < a.N;  // inactive waves still stage rows and meet the barriers
   const int K = a.K;
-  // weight fragments: row n0 + (lane & 15), k = 32 t + 8 (lane >> 4), all issued before the first tile
-  // (fragment order: one 1 KB contiguous block per load and wave; row-major: 16 rows x 64 B per load)
+  // weight fragments: row n0 + (lane & 15), k = 32 t + 8 (lane >> 4), t in this wave's half, all issued before
+  // the first tile (fragment order: one 1 KB contiguous block per load and wave; row-major: 16 rows x 64 B)
   const int g = active ? n0 / 16 : 0;
   const bool fo = a.w_fragment_order != 0;
   const bf16_t* wp = (const bf16_t*)a.w + (fo ? ((int64_t)g * KT * 64 + lane) * 8
                                               : (int64_t)(g * 16 + (lane & 15)) * K + 8 * (lane >> 4));
   const int wstep = fo ? 64 * 8 : 32;
-  bf16x8 wf[KT];
+  bf16x8 wf[KH];
 #pragma unroll
-  for (int t = 0; t < KT; ++t) wf[t] = __builtin_bit_cast(bf16x8, ld16(wp + (int64_t)t * wstep));
+  for (int t = 0; t < KH; ++t) wf[t] = __builtin_bit_cast(bf16x8, ld16(wp + (int64_t)(ks * KH + t) * wstep));
   const int nout = active ? n0 + 4 * (lane >> 4) : 0;
   const f32x4 bias = *reinterpret_cast<const f32x4*>(a.bias + nout);
   for (int r0 = 0; r0 < a.R; r0 += 16) {
-    if (r0) __syncthreads();  // the previous tile's fragments have been read
-    modproj_stage<KT>(a, r0, lds);
+    if (r0) __syncthreads();  // the previous tile's fragments and partial sums have been read
+    modproj_stage<KT, THREADS>(a, r0, lds);
     __syncthreads();
     f32x4 acc_h = {0.f, 0.f, 0.f, 0.f}, acc_l = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < KT; ++t) {
+    for (int u = 0; u < KH; ++u) {
+      const int t = ks * KH + u;
       const bf16x8 hi = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + (t * 64 + lane) * 16));
       const bf16x8 lo = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + ((KT + t) * 64 + lane) * 16));
-      acc_h = mfma16(wf[t], hi, acc_h);
-      acc_l = mfma16(wf[t], lo, acc_l);
+      acc_h = mfma16(wf[u], hi, acc_h);
+      acc_l = mfma16(wf[u], lo, acc_l);
     }
-    if (active && r0 + (lane & 15) < a.R) {
-      f32x4 o;
+    f32x4 o = acc_h + acc_l;
+    if (ks) part[((ks - 1) * 4 + ct) * 64 + lane] = o;
+    __syncthreads();
+    if (!ks && active && r0 + (lane & 15) < a.R) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = acc_h[i] + acc_l[i] + bias[i];
+      for (int j = 1; j < KS; ++j) o += part[((j - 1) * 4 + ct) * 64 + lane];
+      o += bias;
       *reinterpret_cast<f32x4*>(a.out + (int64_t)(r0 + (lane & 15)) * a.out_stride + nout) = o;
     }
   }
