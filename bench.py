@@ -124,6 +124,8 @@ def prepare_source_bench(cfg, n: int) -> int:
         ends[i].record(stream)
     torch.cuda.synchronize()
     us = statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends)) * 1e3
+    prep.close()
+    torch.cuda.synchronize()
     H, C = cfg.H, cfg.ctx_dim
     nbytes = cfg.L * 2 * H * C * 2 + cfg.B * cfg.SP * C * 2 + cfg.L * 2 * cfg.B * cfg.SP * H * 2
     flops = 2 * cfg.B * cfg.SP * C * 2 * H * cfg.L
@@ -164,6 +166,34 @@ def modulations_bench(cfg, n: int) -> int:
     print(json.dumps({"modulations": {"workload": {"rows": R, "H": cfg.H, "MODW": cfg.modw}, "launches": n,
                                       "us_per_launch_median": round(us, 3), "algorithmic_bytes": nbytes,
                                       "GB_s": round(nbytes / us / 1e3, 1)}}), flush=True)
+    return 0
+
+
+def probe_bench(reps: int) -> int:
+    """Prices the megakernel's synchronisation with mkx_probe: its grid barrier (the reference's barrier-only
+    micro-benchmark, src/tune_mk.py:28-33, timed at :66-68), and one stage boundary, a producer -> consumer
+    hand-off (store write-through, acknowledgement, ready epoch; poll, operand load), for the operand sizes
+    the stages load (4 KB; 24 KB = one 16-row tile of a 768-wide fp16 operand; 72 KB = 48 rows) with one
+    consumer and with the fan-outs the stages have (24, 128 consumers of the same data)."""
+    import ctypes
+    from mkx import _lib
+
+    L = _lib.lib()
+    res = {"barrier": None, "handoff": {}}
+    a = _lib.MkxProbeArgs(kind=_lib.PROBE_BARRIER, n=1000, bytes=0, fan=0, reps=reps)
+    _lib.check(L.mkx_probe(ctypes.byref(a), None), "mkx_probe(barrier)")
+    res["barrier"] = {"us_median": round(a.us_median, 3), "us_min": round(a.us_min, 3), "barriers": a.n,
+                      "timed_out": bool(a.timed_out)}
+    xcd = None
+    for nbytes in (4096, 24576, 73728):
+        for fan in (1, 24, 128):
+            a = _lib.MkxProbeArgs(kind=_lib.PROBE_HANDOFF, n=200, bytes=nbytes, fan=fan, reps=reps)
+            _lib.check(L.mkx_probe(ctypes.byref(a), None), "mkx_probe(handoff)")
+            res["handoff"][f"{nbytes // 1024}KB_x{fan}"] = {"us_median": round(a.us_median, 3), "us_min": round(a.us_min, 3),
+                                                           "timed_out": bool(a.timed_out)}
+            xcd = [a.xcd_first[0], a.xcd_first[1]]
+    res["handoff_xcds_first_producer_consumer"] = xcd
+    print(json.dumps({"probe": res}), flush=True)
     return 0
 
 
@@ -239,6 +269,16 @@ def expert_call_bench(cfg, n: int, name: str) -> int:
                                       "ms_median_kernels": round(ms_k, 3), "ms_median_graph": round(ms_g, 3),
                                       "ms_median_pytorch_prep": round(ms_t, 3),
                                       "parts": "modulations + source caches + steps 1-10 + ring append"}}), flush=True)
+    # the captured graph, the library handles and the device tensors are released here, not left to
+    # interpreter teardown, where they would be destroyed after (or among) the profilers' exit hooks
+    torch.cuda.synchronize()
+    graph.reset()
+    del graph, kernels, torch_side
+    prep.close()
+    mk.close()
+    del ring, step_mods, past, model
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     return 0
 
 
@@ -262,6 +302,8 @@ def main() -> int:
                     help="only time N modulation projections of the workload's rows (samples x Euler steps)")
     ap.add_argument("--expert-call", type=int, default=0, metavar="N",
                     help="only time N whole expert calls (modulations, source caches, steps 1..N, ring append)")
+    ap.add_argument("--probe", type=int, default=0, metavar="REPS",
+                    help="only run the synchronisation probes (grid barrier, stage hand-off), REPS launches each")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the megakernel runs on a single MI355X (batch samples would shard "
@@ -271,6 +313,8 @@ def main() -> int:
     import torch
     from mkx import ExpertMegakernel, synthetic as SY
 
+    if args.probe:
+        return probe_bench(args.probe)
     if args.copy_calibration:
         n = args.copy_calibration << 20
         src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
@@ -422,7 +466,9 @@ def main() -> int:
     torch.cuda.synchronize()
     del plan
     mk.close()
+    del past, model
     torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     return 0
 
 

@@ -8,7 +8,7 @@
  *   mkx_run      <- ExpertMegakernel.run        (src/mk_expert.py:483-515: marshal caches, one launch)
  *   mkx_barriers <- ExpertMegakernel.barriers   (src/mk_expert.py:517-518: stage boundaries per launch)
  *   mkx_query    <- attributes the reference reads off the object (nprog, bar, prof; test_mk.py:44-45,
- *                   tune_mk.py:131-153)
+ *                   tune_mk.py:79-95)
  *   mkx_ring_append <- the register cache's per-frame append after each expert call (append_frame,
  *                   src/profile_breakdown.py:97-104) that refills past.register_step['mem_kv'] / cu_kv
  *   mkx_source_create / _run / _destroy <- the cross-attention source K/V of REKI's register_prepare
@@ -129,7 +129,10 @@ typedef enum {
   MKX_Q_ERROR_FLAG = 3,    /* device error flag of the last launch (spin bound exceeded = 1) */
   MKX_Q_PROFILE_LEN = 5,   /* entries of the caller's timestamp buffer, 0 when profiling is off */
   MKX_Q_WEIGHT_BYTES = 6,  /* bytes of packed linear weights streamed per Euler step */
-  MKX_Q_LDS_BYTES = 7      /* dynamic LDS per workgroup */
+  MKX_Q_LDS_BYTES = 7,     /* dynamic LDS per workgroup */
+  MKX_Q_GEMM_FORM = 8      /* GEMM form of the last launch: 0 passes, 1 row-wise, -1 before the first launch
+                              (no reference counterpart: the reference has one form; tune_mk.py:69-72 overrides
+                              its tile config instead) */
 } mkx_query_key;
 
 /* ExpertMegakernel.__init__ (src/mk_expert.py:436-481). Validates dims, copies and repacks the weights
@@ -242,8 +245,8 @@ int mkx_source_run(mkx_source* h, const mkx_source_args* args, void* stream);
  * loops, harnesses that forbid hipMalloc); no counterpart in the reference. Same arguments, kernels and
  * results as mkx_source_run, but the call's packed context is staged in a static device array of the
  * library (16 MiB per GPU, held until the process ends) instead of the handle's buffer, and the call
- * allocates nothing. A context whose packed form (B * SP rows rounded up to 64, times C * 2 bytes) exceeds
- * 16 MiB is refused with MKX_EINVAL. Every call on one GPU shares that array: calls that overlap on one GPU
+ * allocates nothing. A context whose packed form ((ceil32(B * SP) + 160) rows of C * 2 bytes: the rows rounded
+ * up to 32 plus 160 rows of padding for the largest workgroup's reads) exceeds 16 MiB is refused with MKX_EINVAL. Every call on one GPU shares that array: calls that overlap on one GPU
  * (concurrent streams, other threads) race and must be serialised by the caller. */
 int mkx_source_run_noalloc(mkx_source* h, const mkx_source_args* args, void* stream);
 int mkx_source_destroy(mkx_source* h);
@@ -291,6 +294,30 @@ typedef struct {
 } mkx_modin_args;
 
 int mkx_modulation_input(const mkx_modin_args* args, void* stream);
+
+/* Synchronisation micro-benchmarks (no handle). Reference: the barrier-only kernel _barrier_only
+ * (src/tune_mk.py:28-33), timed at :66-68 to price the reference's grid barrier (results/opt/tune/v5.json:3-4).
+ * MKX_PROBE_BARRIER: every workgroup of a one-per-CU grid passes n grid barriers (this library's barrier,
+ * the one the Euler launch runs after its first stage) with nothing between them; reports microseconds per
+ * barrier. MKX_PROBE_HANDOFF: a chain of n hand-offs between two groups of `fan` workgroups on different
+ * XCDs: a producer stores `bytes` write-through, waits for the acknowledgements and publishes a ready epoch;
+ * `fan` consumers poll the epoch and then load all `bytes`; a consumer produces the next hand-off. Reports
+ * microseconds per hand-off: the cost of one stage boundary of the Euler launch for an operand of that size.
+ * Launches `reps` times (median and minimum reported); allocates and frees its own buffers; synchronous. */
+typedef enum { MKX_PROBE_BARRIER = 0, MKX_PROBE_HANDOFF = 1 } mkx_probe_kind;
+typedef struct {
+  int32_t kind;       /* mkx_probe_kind */
+  int32_t n;          /* barriers, or hand-offs in the chain: even, 2 .. 2048 */
+  int32_t bytes;      /* hand-off: bytes each consumer loads: 4096, 24576 or 73728 */
+  int32_t fan;        /* hand-off: consumers per hand-off, 1 .. CUs / 2 */
+  int32_t reps;       /* launches, 1 .. 100 */
+  int32_t timed_out;  /* out: 1 if a wait of some launch exceeded its spin bound (the times are then invalid) */
+  int32_t xcd_first[2]; /* out, hand-off: the XCDs of the first producer and its first consumer (workgroups 0, 1) */
+  double us_median;   /* out: microseconds per barrier or hand-off, median over the launches */
+  double us_min;      /* out: the fastest launch's */
+} mkx_probe_args;
+
+int mkx_probe(mkx_probe_args* args, void* stream);
 
 int64_t mkx_query(const mkx_handle* h, int32_t key);
 int mkx_destroy(mkx_handle* h);

@@ -15,6 +15,7 @@
 #include "mkx_ring.h"
 #include "mkx_prepare.h"
 #include "mkx_modproj.h"
+#include "mkx_probe.h"
 
 using namespace mkx;
 
@@ -286,6 +287,7 @@ struct mkx_handle {
   int plain_launch = 0;  // MKX_PLAIN_LAUNCH=1 at creation: hipLaunchKernel instead of the cooperative launch
   const void* kernel_rows = nullptr;  // the instantiation with row-wise GEMM stages
   int gemm_form = -1;    // MKX_GEMM_FORM at creation: 0 passes, 1 row-wise, -1 chosen per launch
+  int last_form = -1;    // form of the last launch (0 passes, 1 row-wise; -1 before the first)
   unsigned spin_limit = SPIN_LIMIT;
   int captured = 0;      // a launch of this handle was captured into a graph: its scratch pointers are frozen
   unsigned long long gen_before = 0;
@@ -308,6 +310,7 @@ struct mkx_source {
   bf16_t* wvp = nullptr;
   bf16_t* kn = nullptr;    // [L, 64]
   bf16_t* ctxp = nullptr;  // staging: the call's context in fragment order
+  int ncu = 256;           // compute units of the handle's device (read once, at creation)
 };
 
 static void free_source(mkx_source* h) {
@@ -546,8 +549,11 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   Layout lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(false, a->B * a->T_act, d.A), false);
   // Row-wise form where a gate/up task would need more than one pass of row tiles (its layout has tasks of one
   // column tile, and its step tail's output tasks, over row chunks, must number at most 64)
-  const bool rows = tail_outputs(true, a->B * a->T_act, d.A) <= 64 &&
-                    (h->gemm_form == 1 || (h->gemm_form < 0 && NRP / 16 > sk.RBMAX));
+  const bool rows_fit = tail_outputs(true, a->B * a->T_act, d.A) <= 64;
+  if (h->gemm_form == 1 && !rows_fit)
+    return fail(MKX_EUNSUPPORTED, "MKX_GEMM_FORM=rows: the row-wise form's step tail needs at most 64 output tasks "
+                                  "(B * T_act too large for it)");
+  const bool rows = rows_fit && (h->gemm_form == 1 || (h->gemm_form < 0 && NRP / 16 > sk.RBMAX));
   if (rows) lay = plan_layout(sk, h->G, NRP / 16, a->B, Mqp / 16, H, d.A, tail_outputs(true, a->B * a->T_act, d.A), true);
   {
     // a task waits on at most 256 ready epochs (one poll of 4 x 64 lanes): gate/up on every CA out-projection
@@ -663,6 +669,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
     HIPCHK(hipLaunchCooperativeKernel(kern, dim3(h->G), dim3(NTHREADS), args, 0, stream));
   }
   h->last_nbar = mkx_barriers(h, a->n_steps);
+  h->last_form = rows ? 1 : 0;
   return MKX_OK;
 }
 
@@ -713,8 +720,8 @@ int mkx_ring_append(const mkx_ring_args* a, void* stream_) {
 
 }  // extern "C"
 
-// Static staging for mkx_source_run_noalloc: the call's context in fragment order (rows padded to 64) lives
-// in this file-scope device array instead of the handle's allocation. Each GPU holds its own copy until the
+// Static staging for mkx_source_run_noalloc: the call's context in fragment order (ceil32(B * SP) + PREP_ROW_PAD
+// rows of C bf16 values, prep_ctx_bytes) lives in this file-scope device array instead of the handle's allocation. Each GPU holds its own copy until the
 // process ends; calls on one GPU share it (the last call's contents stay, and calls that overlap race).
 constexpr long long SOURCE_SCRATCH_BYTES = 16LL << 20;
 static __device__ __align__(256) char scratch[SOURCE_SCRATCH_BYTES];
@@ -763,14 +770,10 @@ int source_args_check(const mkx_source* h, const mkx_source_args* a, const char*
   return MKX_OK;
 }
 
-// Row tiles per wave of prepare_source_kernel for nrows source rows: the one whose busiest CU has the least
-// work, counting a workgroup's fixed cost (its first k-blocks in flight, the epilogue) as one row tile.
-int prep_rtw(int nrows, int ncol_groups) {
-  int dev = 0, ncu = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    hipDeviceProp_t pr;
-    if (hipGetDeviceProperties(&pr, dev) == hipSuccess && pr.multiProcessorCount > 0) ncu = pr.multiProcessorCount;
-  }
+// Row tiles per wave of prepare_source_kernel for nrows source rows on ncu compute units: the one whose
+// busiest CU has the least work, counting a workgroup's fixed cost (its first k-blocks in flight, the
+// epilogue) as one row tile.
+int prep_rtw(int nrows, int ncol_groups, int ncu) {
   const int nrt = (nrows + 15) / 16;
   int best = 2;
   long long best_cost = -1;
@@ -789,7 +792,7 @@ int source_launch(const mkx_source* h, const mkx_source_args* a, bf16_t* ctxp, h
   const mkx_source_dims& d = h->dims;
   const int nrows = a->B * a->SP;
   const int np = (d.NH + 1) / 2, ncg = d.L * 2 * np;
-  const int rtw = prep_rtw(nrows, ncg), wg_rows = 32 * rtw;
+  const int rtw = prep_rtw(nrows, ncg, h->ncu), wg_rows = 32 * rtw;
   const int ngroups = (nrows + wg_rows - 1) / wg_rows;
   // packed pieces: rows padded with zeros to whole workgroups
   const long long n_x = (long long)ngroups * wg_rows * d.C / 8;
@@ -840,6 +843,13 @@ int mkx_source_create(const mkx_source_dims* d, const void* wk, const void* wv, 
   hipStream_t stream = (hipStream_t)stream_;
   mkx_source* h = new mkx_source();
   h->dims = *d;
+  {
+    // the device's CU count, which sizes every call's launch (read here so that calls query nothing)
+    int dev = 0;
+    hipDeviceProp_t pr;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&pr, dev) == hipSuccess && pr.multiProcessorCount > 0)
+      h->ncu = pr.multiProcessorCount;
+  }
   const int64_t wel = (int64_t)d->L * d->NH * 64 * d->C;
   auto cleanup = [&](int code, const std::string& msg) {
     free_source(h);
@@ -953,6 +963,99 @@ int mkx_check(mkx_handle* h, void* stream_) {
   return MKX_OK;
 }
 
+int mkx_probe(mkx_probe_args* a, void* stream_) {
+  if (!a) return fail(MKX_EINVAL, "mkx_probe: args is NULL");
+  a->us_median = a->us_min = 0.0;
+  a->timed_out = 0;
+  a->xcd_first[0] = a->xcd_first[1] = -1;
+  if (a->kind != MKX_PROBE_BARRIER && a->kind != MKX_PROBE_HANDOFF) return fail(MKX_EINVAL, "mkx_probe: unknown kind");
+  if (a->n < 2 || a->n > FLAG_MAX || (a->n & 1)) return fail(MKX_EINVAL, "mkx_probe: n must be even and in [2, 2048]");
+  if (a->reps < 1 || a->reps > 100) return fail(MKX_EINVAL, "mkx_probe: reps must be in [1, 100]");
+  const void* kern = nullptr;
+  if (a->kind == MKX_PROBE_BARRIER) {
+    kern = reinterpret_cast<const void*>(&barrier_probe_kernel);
+  } else if (a->bytes == 4096) {
+    kern = reinterpret_cast<const void*>(&handoff_probe_kernel<1>);
+  } else if (a->bytes == 24576) {
+    kern = reinterpret_cast<const void*>(&handoff_probe_kernel<6>);
+  } else if (a->bytes == 73728) {
+    kern = reinterpret_cast<const void*>(&handoff_probe_kernel<18>);
+  } else {
+    return fail(MKX_EINVAL, "mkx_probe: bytes must be 4096, 24576 or 73728");
+  }
+  hipStream_t stream = (hipStream_t)stream_;
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, dev));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return fail(MKX_EUNSUPPORTED, "mkx_probe: built for gfx950");
+  const int G = prop.multiProcessorCount;
+  if (G < 2 || G > 256) return fail(MKX_EUNSUPPORTED, "mkx_probe: 2 to 256 CUs");
+  if (a->kind == MKX_PROBE_HANDOFF && (a->fan < 1 || 2 * a->fan > G)) return fail(MKX_EINVAL, "mkx_probe: fan must be in [1, CUs / 2]");
+  int per_cu = 0;
+  HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NTHREADS, 0));
+  if (per_cu < 1) return fail(MKX_ENORESIDENT, "mkx_probe: kernel does not fit one workgroup per CU");
+  ProbeParams p{};
+  // every allocation is released on every path below
+  unsigned* dx = nullptr;
+  char* data = nullptr;
+  void* sync = nullptr;  // BarState, then the flag table, then out[4]
+  const size_t flag_bytes = sizeof(unsigned long long) * FLAG_MAX * FLAG_STRIDE;
+  const size_t sync_bytes = sizeof(BarState) + flag_bytes + 4 * sizeof(long long);
+  const size_t data_bytes = a->kind == MKX_PROBE_HANDOFF ? (size_t)a->n * a->bytes : 256;
+  std::vector<double> us;
+  int status = MKX_OK;
+  auto run = [&]() -> int {
+    HIPCHK(hipMalloc(&dx, sizeof(unsigned) * G));
+    HIPCHK(hipMalloc(&data, data_bytes));
+    HIPCHK(hipMalloc(&sync, sync_bytes));
+    // workgroups per XCD of a G-workgroup grid (the barrier's arrival targets)
+    hipLaunchKernelGGL(xcc_probe, dim3(G), dim3(NTHREADS), 0, stream, dx);
+    std::vector<unsigned> hx(G);
+    HIPCHK(hipMemcpyAsync(hx.data(), dx, sizeof(unsigned) * G, hipMemcpyDeviceToHost, stream));
+    HIPCHK(hipStreamSynchronize(stream));
+    unsigned cnt[MAX_XCD] = {};
+    for (int i = 0; i < G; ++i) {
+      if (hx[i] >= MAX_XCD) return fail(MKX_EUNSUPPORTED, "mkx_probe: unexpected XCC id");
+      ++cnt[hx[i]];
+      p.xmask |= 1u << hx[i];
+    }
+    for (int x = 0; x < MAX_XCD; ++x) p.nx[x] = cnt[x];
+    p.bar = (BarState*)sync;
+    p.flags = (unsigned long long*)((char*)sync + sizeof(BarState));
+    p.out = (long long*)((char*)sync + sizeof(BarState) + flag_bytes);
+    p.data = data;
+    p.n = a->n;
+    p.fan = a->kind == MKX_PROBE_HANDOFF ? a->fan : 0;
+    p.spin_limit = SPIN_LIMIT;
+    HIPCHK(hipMemsetAsync(data, 0, data_bytes, stream));
+    for (int r = 0; r < a->reps; ++r) {
+      HIPCHK(hipMemsetAsync(sync, 0, sync_bytes, stream));
+      void* args[] = {&p};
+      HIPCHK(hipLaunchCooperativeKernel(kern, dim3(G), dim3(NTHREADS), args, 0, stream));
+      long long out[4] = {0, 0, -1, -1};
+      int err = 0;
+      HIPCHK(hipMemcpyAsync(out, p.out, sizeof(out), hipMemcpyDeviceToHost, stream));
+      HIPCHK(hipMemcpyAsync(&err, &p.bar->err, sizeof(int), hipMemcpyDeviceToHost, stream));
+      HIPCHK(hipStreamSynchronize(stream));
+      if (err) a->timed_out = 1;
+      a->xcd_first[0] = (int32_t)out[2];
+      a->xcd_first[1] = (int32_t)out[3];
+      us.push_back(out[0] * 0.01 / a->n);  // 100 MHz clock
+    }
+    return MKX_OK;
+  };
+  status = run();
+  if (dx) (void)hipFree(dx);
+  if (data) (void)hipFree(data);
+  if (sync) (void)hipFree(sync);
+  if (status != MKX_OK) return status;
+  std::sort(us.begin(), us.end());
+  a->us_median = us[us.size() / 2];
+  a->us_min = us[0];
+  return MKX_OK;
+}
+
 int64_t mkx_query(const mkx_handle* h, int32_t key) {
   if (!h) return -1;
   switch (key) {
@@ -979,6 +1082,7 @@ int64_t mkx_query(const mkx_handle* h, int32_t key) {
     case MKX_Q_PROFILE_LEN: return h->prof_len;
     case MKX_Q_WEIGHT_BYTES: return h->weight_bytes;
     case MKX_Q_LDS_BYTES: return lds_of(h->d.H, h->d.I);
+    case MKX_Q_GEMM_FORM: return h->last_form;
     default: return -1;
   }
 }

@@ -13,9 +13,11 @@
 //    producer tasks whose output it reads. One grid barrier per launch remains, after the launch's first
 //    stage (whose per-launch copies every later stage reads).
 //  * The grid barrier is hierarchical and fence-free: each workgroup waits for its own stores to be
-//    acknowledged, bumps its XCD's arrival counter with an L2 atomic, the last arrival of an XCD publishes
-//    the epoch with a device-scope store, and every workgroup polls the eight per-XCD flags with
-//    device-scope loads. Counters are 64-bit and monotonic across launches, so nothing is reset.
+//    acknowledged, bumps its XCD's arrival counter with a device-scope atomic (the counter is shared by the
+//    XCD's workgroups, so the HIP memory model asks for agent scope; it runs once per launch), the last
+//    arrival of an XCD publishes the epoch with a device-scope store, and every workgroup polls the eight
+//    per-XCD flags with device-scope loads. Counters are 64-bit and monotonic across launches, so nothing
+//    is reset.
 //  * Waits are bounded: a wait that exceeds its spin bound sets an error flag, and every later wait of the
 //    launch returns immediately, so a broken launch still drains.
 #pragma once
@@ -146,13 +148,19 @@ __device__ __forceinline__ float xor32_max(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return xor32_sum(xor16_sum(row_sum16(v))); }
 
 // ---------------------------------------------------------------------------------------------
+// Error bits of BarState::err, each set with an atomic OR so that neither clears the other: a wait exceeded
+// its spin bound (the launch's synchronisation is broken), or a GEMM operand exceeded the fp16 range (the
+// launch completes and returns NaN).
+constexpr int ERR_TIMEOUT = 1;
+constexpr int ERR_RANGE = 2;
+
 // grid barrier state (device memory, zeroed at handle creation)
 struct BarState {
   unsigned long long arrive[MAX_XCD][32];   // per-XCD arrival counters (L2 atomics), 256 B apart
   unsigned long long done[MAX_XCD][512];    // per-XCD published epochs (device scope), 4 KB apart
   unsigned long long gen;                   // epoch base: stage boundaries passed by earlier launches
   unsigned long long pad0[15];
-  int err;                                  // 1 = a wait exceeded its spin bound
+  int err;                                  // ERR_TIMEOUT | ERR_RANGE bits, set with atomic OR
   int pad1[31];
   unsigned long long arrivals_last;         // barriers x workgroups recorded by the last launch
 };
@@ -183,7 +191,7 @@ __device__ __forceinline__ void bar_arrive(BarCtx& c, unsigned long long e) {
   if (threadIdx.x == 0) {
     unsigned long long t = c.base + e;
     unsigned long long old =
-        __hip_atomic_fetch_add(&c.bs->arrive[c.x][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_fetch_add(&c.bs->arrive[c.x][0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old + 1 == t * c.nx) __hip_atomic_store(&c.bs->done[c.x][0], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -199,7 +207,7 @@ __device__ __forceinline__ void bar_wait(BarCtx& c, unsigned long long e) {
         ok = __hip_atomic_load(&c.bs->done[lane][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= t;
       if (__all(ok)) break;
       if (++n > c.spin_limit) {
-        if (lane == 0) __hip_atomic_store(&c.bs->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_fetch_or(&c.bs->err, ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         c.failed = true;
         break;
       }
@@ -255,7 +263,7 @@ __device__ __forceinline__ void flag_wait(BarCtx& c, int kind, int n, F idx, uns
       for (int k = 0; k < NCH; ++k) ok = ok && v[k] >= t;
       if (__all(ok)) break;
       if (++spins > c.spin_limit) {
-        if (lane == 0) __hip_atomic_store(&c.bs->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_fetch_or(&c.bs->err, ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         c.failed = true;
         break;
       }

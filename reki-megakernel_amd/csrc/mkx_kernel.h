@@ -364,7 +364,7 @@ __device__ __forceinline__ bool st_h4(void* base, uint32_t off, f32x4 v) {
 // records that a GEMM operand of this launch exceeded the fp16 range (error bit 2): the launch returns NaN and
 // mkx_check reports MKX_ERANGE
 __device__ __forceinline__ void range_error(BarState* bs) {
-  __hip_atomic_fetch_or(&bs->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_or(&bs->err, ERR_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ u32x4 lds16(const char* p) { return *reinterpret_cast<const u32x4*>(p); }
 // Marks LDS values as needed together: the reads that produced them are issued back to back and waited for
@@ -2433,9 +2433,13 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
     s_ks[c.tid] = min(max(p.kv_start[c.tid], 0), p.PM);
     s_ks[MAX_BATCH + c.tid] = min(max(p.ca_len[c.tid], 0), p.SP);
   }
-  // A launch after one that timed out (error flag still set: the caller has not run mkx_check, which resets
-  // the synchronisation state) does no work and returns NaN, so the failure cannot pass unnoticed.
-  if (__hip_atomic_load(&p.bar->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+  // A launch after one that timed out (timeout bit still set: the caller has not run mkx_check, which resets
+  // the synchronisation state) does no work and returns NaN, so the failure cannot pass unnoticed. Only the
+  // timeout bit decides: the range bit may be set by a workgroup of this very launch (its first stage stores
+  // GEMM operands), and a workgroup that returned here would leave the others waiting for its arrivals. A
+  // range error latched by an earlier launch still poisons this launch's output (the last step tail reads
+  // both bits) until mkx_check reports it.
+  if (__hip_atomic_load(&p.bar->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ERR_TIMEOUT) {
     if (c.wg == 0)
       for (int i = c.tid; i < p.B * p.T * p.A; i += NTHREADS) p.x_out[i] = __uint_as_float(0x7fc00000u);
     return;
@@ -2510,7 +2514,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
   // arrival counters then read (gen + total) x workgroups, the state the next launch's barrier expects)
   wait_vm0();
   __syncthreads();
-  if (c.tid == 0) __hip_atomic_fetch_add(&p.bar->arrive[bc.x][0], (unsigned long long)(total - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (c.tid == 0) __hip_atomic_fetch_add(&p.bar->arrive[bc.x][0], (unsigned long long)(total - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (c.wg == 0 && c.tid == 0) __hip_atomic_store(&p.bar->gen, bc.base + (unsigned long long)total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

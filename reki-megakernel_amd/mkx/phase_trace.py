@@ -78,11 +78,9 @@ def trace(workload: str) -> dict:
     t0 = int(raw[raw > 0].min())
     us = torch.where(raw > 0, (raw - t0).double() * 0.01, torch.full_like(raw, float("nan"), dtype=torch.float64))
     per = 7 * cfg.L + 1
-    # the launch's form (as the library chooses it): row-wise where a gate/up task would need more than one
-    # pass of row tiles; its GEMM stages stamp other points, so only the pass form's phases are reported
-    rt = cfg.B * ((cfg.m_q + 15) // 16)
-    form = os.environ.get("MKX_GEMM_FORM", "")
-    rows_form = form == "rows" or (form != "passes" and rt > (2 if cfg.H == 1024 else 3))
+    # the form the library chose for the traced launch (row-wise GEMM stages stamp other points, so only the
+    # pass form's phases are reported)
+    rows_form = int(_lib.lib().mkx_query(mk._h, _lib.Q_GEMM_FORM)) == 1
     rows = {k: [] for k in STAGES + ["tail"]}
     for g in range(1, total):
         j = (g - 1) % per

@@ -82,7 +82,7 @@ def test_every_args_struct_matches_the_header_layout(tmp_path):
     structs = {"mkx_dims": _lib.MkxDims, "mkx_weights": _lib.MkxWeights, "mkx_step_args": _lib.MkxStepArgs,
                "mkx_ring_args": _lib.MkxRingArgs, "mkx_source_dims": _lib.MkxSourceDims,
                "mkx_source_args": _lib.MkxSourceArgs, "mkx_modproj_args": _lib.MkxModprojArgs,
-               "mkx_modin_args": _lib.MkxModinArgs}
+               "mkx_modin_args": _lib.MkxModinArgs, "mkx_probe_args": _lib.MkxProbeArgs}
     lines = ['#include <stdio.h>', '#include "mkx.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -145,3 +145,25 @@ def test_modulation_input_rejects_bad_arguments_without_launching():
     assert L.mkx_modulation_input(ctypes.byref(a), None) == _lib.EUNSUPPORTED
     a.tdim, a.N = 256, 0
     assert L.mkx_modulation_input(ctypes.byref(a), None) == _lib.EINVAL
+
+
+def test_query_keys_match_the_header():
+    """mkx_query_key values in include/mkx.h equal the binding's constants (a drifted key would query
+    something else without any error)."""
+    text = open(os.path.join(ROOT, "include", "mkx.h")).read()
+    keys = dict((k, int(v)) for k, v in re.findall(r"\bMKX_(Q_[A-Z_]+)\s*=\s*(\d+)", text))
+    assert keys, "no query keys found"
+    for name, val in keys.items():
+        assert getattr(_lib, name) == val, name
+    assert keys["Q_GEMM_FORM"] == 8
+
+
+@pytest.mark.parametrize("over", [dict(kind=5), dict(n=3), dict(n=0), dict(n=4096), dict(reps=0), dict(bytes=1000)])
+def test_probe_validates_arguments_before_touching_the_device(over):
+    L = _lib.lib()
+    a = dict(kind=_lib.PROBE_HANDOFF, n=200, bytes=24576, fan=1, reps=3)
+    a.update(over)
+    args = _lib.MkxProbeArgs(**a)
+    assert L.mkx_probe(ctypes.byref(args), None) == _lib.EINVAL
+    assert "mkx_probe" in L.mkx_last_error().decode()
+    assert L.mkx_probe(None, None) == _lib.EINVAL

@@ -1,0 +1,62 @@
+"""Parity over many inputs, as the reference measures it: for each of 32 seeds of workload A and of its
+reference layout A-ref (flow noise, VLM context, memory states and state conditioning all redrawn; weights
+fixed), Euler steps 2-10 on the megakernel against the fp32 oracle, reported the way the reference's
+compare.py summarises its 440 chunks (src/compare.py:20-27: max and mean |delta| over the real action dims,
+p99 and median of the per-chunk max; its eager-vs-megakernel figures on H100 are 5.8e-3 / 6.9e-4 / 4.8e-3 /
+2.3e-3, results/opt/run_a/correctness.json:116-121)."""
+import json
+import statistics
+
+import pytest
+import torch
+
+from _cases import oracle_steps
+from mkx import ExpertMegakernel, synthetic as SY
+
+pytestmark = pytest.mark.gpu
+torch.set_grad_enabled(False)
+
+N_SEEDS = 32
+# the parity bound (against the fp32 eager expert, real action dims) and this kernel's own level: its fp16
+# GEMM operands keep every single-input case of A within 2e-3 max / 4e-4 mean (tests/test_gpu_parity.py)
+FP32_MAX, FP32_MEAN = 1e-2, 2e-3
+TIGHT_MAX, TIGHT_MEAN = 2e-3, 4e-4
+
+
+def _quantile(v, q):
+    s = sorted(v)
+    pos = q * (len(s) - 1)
+    lo = int(pos)
+    hi = min(lo + 1, len(s) - 1)
+    return s[lo] + (s[hi] - s[lo]) * (pos - lo)
+
+
+@pytest.mark.parametrize("name", ["A", "A-ref"])
+def test_parity_statistics_over_seeds(name):
+    cfg = SY.WORKLOADS[name]
+    W = SY.make_weights(cfg, 0)
+    model = SY.SyntheticReki(cfg, W, device="cuda")
+    mk = ExpertMegakernel(model)
+    adim = cfg.action_dim
+    chunk_max, sums, count = [], 0.0, 0
+    for s in range(N_SEEDS):
+        inp = SY.make_inputs(cfg, seed_ctx=1 + 1000 * s, seed_noise=1234 + 1000 * s, seed_state=2 + 1000 * s)
+        past = model.register_prepare(inp["ctx"], inp["mem_states"])
+        mods, dt = model._step_modulations(cfg.num_steps, inp["state_cond"])
+        x1, _, _ = model._expert_first_step(inp["noise"].to("cuda"), past, None, mods[..., :1, :], dt, adim)
+        x = mk.run(x1, mods, dt, past, adim)
+        mk.check()
+        case = {"cfg": cfg, "W": W, "past": past, "mods": mods, "dt": dt}
+        ref = oracle_steps(case, x1, 1, cfg.num_steps - 1, "fp32")
+        d = (x.float().cpu()[..., :adim] - ref[..., :adim]).abs()
+        assert torch.isfinite(d).all(), f"seed {s}: non-finite output"
+        chunk_max.append(float(d.max()))
+        sums += float(d.sum())
+        count += d.numel()
+        print(json.dumps({"case": f"{name} seed {s}", "chunk_max": chunk_max[-1]}), flush=True)
+    stats = {"workload": name, "chunks": N_SEEDS, "max_abs": max(chunk_max), "mean_abs": sums / count,
+             "p99_chunk_max_abs": _quantile(chunk_max, 0.99), "median_chunk_max_abs": statistics.median(chunk_max)}
+    print(json.dumps({"case": f"{name} parity over seeds", **stats}), flush=True)
+    assert stats["max_abs"] <= FP32_MAX and stats["mean_abs"] <= FP32_MEAN, stats
+    assert stats["max_abs"] <= TIGHT_MAX and stats["mean_abs"] <= TIGHT_MEAN, stats
+    mk.close()

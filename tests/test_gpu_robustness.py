@@ -235,3 +235,62 @@ def test_ring_copies_its_inputs():
     assert ring.mem_kv[0][0].shape == (8, 2, 64) and int(ring.kv_start[0]) == 0
     with pytest.raises(ValueError, match="cur_k is on cpu"):
         ring.append_frame(torch.zeros(1, 1, 2, 2, 64, dtype=torch.bfloat16), torch.zeros(1, 1, 2, 2, 64, dtype=torch.bfloat16))
+
+
+def test_fp16_operand_range_headroom_of_workload_a():
+    """How far workload A's residual stream can grow before a GEMM operand leaves the fp16 range (the
+    drop-in limit of this kernel's fp16 operands; a bf16-operand kernel has none): the step input x is
+    scaled by 4^k, which scales the action rows' residual stream (h0 = x Win + bin, and every later
+    residual add keeps it), until a launch reports MKX_ERANGE. The CPU oracle, run with the kernel's operand
+    rounding and its largest GEMM operand recorded, must put 65504 between the last factor that passed and
+    the first that failed; at factor 1 it gives the margin of the synthetic weights."""
+    from oracle import expert_ref as ER
+
+    cfg = SY.WORKLOADS["A"]
+    case = make_case(cfg)
+    x1 = _first_step(case)
+    mk = ExpertMegakernel(case["model"])
+    n = cfg.num_steps - 1
+
+    def oracle_max_operand(f):
+        seen = [0.0]
+        orig = ER.operand_rounder
+
+        def recording(mode):
+            q = orig(mode)
+
+            def rq(t):
+                seen[0] = max(seen[0], float(t.abs().max()))
+                return q(t)
+            return rq
+        ER.operand_rounder = recording
+        try:
+            oracle_steps(case, x1 * f, 1, n, "f16")
+        finally:
+            ER.operand_rounder = orig
+        return seen[0]
+
+    k_bad = None
+    for k in range(0, 16):
+        x = mk.run(x1 * float(4 ** k), case["mods"], case["dt"], case["past"], cfg.action_dim)
+        torch.cuda.synchronize()
+        try:
+            mk.check()
+        except MkxError as e:
+            assert e.status == _lib.ERANGE, e
+            assert torch.isnan(x).all()
+            k_bad = k
+            break
+        assert torch.isfinite(x).all(), k
+    assert k_bad is not None and k_bad >= 1, k_bad
+    y1 = oracle_max_operand(1.0)
+    y_ok = oracle_max_operand(float(4 ** (k_bad - 1)))
+    y_bad = oracle_max_operand(float(4 ** k_bad))
+    _report("fp16 operand headroom (A)", largest_operand_at_1=y1, headroom=65504.0 / y1, first_failing_scale=4 ** k_bad,
+            largest_operand_last_passing=y_ok, largest_operand_first_failing=y_bad)
+    assert y_ok <= 65504.0 * 1.01 and y_bad >= 65504.0 * 0.99, (y_ok, y_bad)
+    assert 65504.0 / y1 >= 100.0  # the synthetic residual stream is far inside the range
+    x = mk.run(x1, case["mods"], case["dt"], case["past"], cfg.action_dim)
+    mk.check()
+    assert torch.isfinite(x).all()
+    mk.close()
