@@ -45,7 +45,7 @@ def _nanmed(v):
     return statistics.median(v) if v else float("nan")
 
 
-def trace(workload: str) -> dict:
+def trace(workload: str, raw_out: str = "") -> dict:
     from mkx import _lib
     _lib.LIB_PATH = TRACE_LIB
     import torch
@@ -75,6 +75,8 @@ def trace(workload: str) -> dict:
     torch.cuda.synchronize()
     mk.check()
     raw = prof.cpu()[TRACE_BASE: TRACE_BASE + (total + 1) * G * TRACE_SLOTS].view(total + 1, G, TRACE_SLOTS)
+    if raw_out:  # every workgroup's stamps, [boundary][workgroup][slot] (100 MHz ticks; 0 = not stamped)
+        torch.save(raw.clone(), raw_out)
     t0 = int(raw[raw > 0].min())
     us = torch.where(raw > 0, (raw - t0).double() * 0.01, torch.full_like(raw, float("nan"), dtype=torch.float64))
     per = 7 * cfg.L + 1
@@ -118,11 +120,12 @@ def main() -> int:
     ap.add_argument("--build", action="store_true", help="compile libmkx_trace.so and exit")
     ap.add_argument("--workload", default="A")
     ap.add_argument("--out", default="")
+    ap.add_argument("--raw", default="", help="also save every workgroup's raw stamps (torch.save)")
     a = ap.parse_args()
     if a.build:
         print(build())
         return 0
-    res = trace(a.workload)
+    res = trace(a.workload, a.raw)
     text = json.dumps(res, indent=1)
     if a.out:
         with open(a.out, "w") as f:
