@@ -539,6 +539,19 @@ __device__ __forceinline__ void dma_task_w(Ctx<S>& c, const Desc& d, int t, char
   }
 }
 
+// The row-wise form's gated-residual tasks and reducers cover one 16-column tile: they stage only that tile's
+// gate and next scale, [sample][gate 16 | scale 16] floats (128 bytes per sample), instead of B x 2H floats
+// (48 KB for 8 samples of width 768, all DMA'd ahead of the task's ready-epoch poll, which returns after them).
+// One 1 KB DMA per 8 samples: lane l copies piece l % 4 of vector (l / 4) % 2 of sample l / 8.
+template <class S>
+__device__ __forceinline__ void dma_mods_tile(Ctx<S>& c, const Desc& d, int tile) {
+  const int nb = (c.p.B + 7) >> 3;
+  for (int k = c.dw; k < nb; k += c.dn) {
+    const int b = min(k * 8 + (c.lane >> 3), c.p.B - 1), v = (c.lane >> 2) & 1, q = c.lane & 3;
+    dma16(c.modrow(b, d.s) + (v ? d.mod_off2 : d.mod_off) + tile * 16 + 4 * q, c.smem + c.p.lds_mods + k * 1024);
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // GEMM stage: out tile (16 columns, all rows) of A @ W^T for each task of this workgroup, computed
 // transposed (D^T = W_tile A^T) so that each lane's accumulator is 4 consecutive output columns of one row:
@@ -566,10 +579,12 @@ __device__ __forceinline__ uint32_t ss_slot(int row, int t) {
 template <class S>
 __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, int row, int col, int L, f32x4 v, f32x4 res) {
   const uint32_t off = fpiece(row, col, c.RT);
-  const float* ml = mods_lds(c, c.sample_of(row), 2 * S::H);
-  const f32x4 h = res + v * ldf4(ml + col);
+  // [gate | next scale] of the row's sample: full rows of H, or (row-wise form) the tile's 16 columns
+  const float* ml = S::RW ? mods_lds(c, c.sample_of(row), 32) + (col & 15) : mods_lds(c, c.sample_of(row), 2 * S::H) + col;
+  const int so = S::RW ? 16 : S::H;
+  const f32x4 h = res + v * ldf4(ml);
   st_sc1(d.out, off, as_u4(h));
-  if (st_h4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + S::H + col)))) range_error(c.p.bar);
+  if (st_h4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + so)))) range_error(c.p.bar);
   float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
   ss = xor32_sum(xor16_sum(ss));
   if (L < 16) st_sc1_b32(d.ssout, ss_slot<S::HT>(row, tile), __float_as_uint(ss));
@@ -1265,6 +1280,7 @@ __device__ __forceinline__ void gemm_stage_rows(Ctx<S>& c, const Desc& d, BarCtx
       wait_vm0();
       __syncthreads();
       dma_task_w(c, d, t, c.smem + S::WBUF);
+      if (d.kind == K_RES) dma_mods_tile(c, d, tile);
     }
     const int kb0 = d.kind == K_SPLIT ? split * NKB : 0;
     const int rt_lo = d.kind == K_SPLIT ? 0 : split * RT / d.rgs;
@@ -1272,10 +1288,23 @@ __device__ __forceinline__ void gemm_stage_rows(Ctx<S>& c, const Desc& d, BarCtx
     MKX_TR(c, 14);
     gemm_wait(c, d, bc, g, split, rt_lo, rt_hi);
     MKX_TR(c, 0);
-    // the task's weight tiles and the stage's shift fragments (the prefetch's DMA) have landed
+    // the task's weight tiles (and a gated-residual task's modulation slices: the prefetch's DMA) have landed
     wait_vm0();
     __syncthreads();
     MKX_TR(c, 1);
+    // AdaRMS tasks: the fp16 shift fragments of this wave's k-blocks (lane l: sample l % 16, zeros for the
+    // samples >= B), loaded from the launch's copy after the poll rather than staged in LDS ahead of it (the
+    // poll returns only after every load issued before it), and before the operand loads, so they land first
+    f16x8 shv[KPW];
+    if (ada) {
+      const bool has = (L & 15) < p.B;
+      const int sb = min(L & 15, p.B - 1);
+#pragma unroll
+      for (int i = 0; i < KPW; ++i) {
+        const f16x8 v = __builtin_bit_cast(f16x8, ld16(d.shs + ((sb * NKB + c.wave + NWAVES * i) * 4 + (L >> 4)) * 32));
+        shv[i] = has ? v : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
     // the operand loads of this wave's first group go out before the shift tile
     const int ng = (rt_hi - rt_lo + NR - 1) / NR;
     const __amdgpu_buffer_rsrc_t ra = rsrc(d.a);
@@ -1286,19 +1315,16 @@ __device__ __forceinline__ void gemm_stage_rows(Ctx<S>& c, const Desc& d, BarCtx
       rows_head<S>(pre, ra, roff0, kb0, RT, L);
     }
     if (ada) {
-      // shift row tile (rows = samples; zeros for the samples >= B) over this wave's k-blocks, into LDS
-      const char* shl = c.smem + p.lds_mods;
+      // shift row tile (rows = samples) over this wave's k-blocks, into LDS
       const char* wl = c.smem + S::WBUF;
-      const bool has = (L & 15) < p.B;
       f32x4 accs[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) accs[nt][0] = accs[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < KPW; ++i) {
         const int kb = c.wave + NWAVES * i;
-        const f16x8 sh = has ? ldsfrag_h(shl + (((L & 15) * NKB + kb) * 4 + (L >> 4)) * 32) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) accs[nt][i & 1] = mfma16h(wfrag_lds<S>(wl + (nt * NKB + kb) * S::CH, L), sh, accs[nt][i & 1]);
+        for (int nt = 0; nt < 2; ++nt) accs[nt][i & 1] = mfma16h(wfrag_lds<S>(wl + (nt * NKB + kb) * S::CH, L), shv[i], accs[nt][i & 1]);
       }
       char* red = c.smem + p.lds_red;
 #pragma unroll
@@ -2348,7 +2374,11 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
     }
     // gate and the next AdaRMS scale: the residual stages' tasks, and the down projection's reducers (its
     // split tasks only store partial sums)
-    if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && task_first(c, PL_RED) < p.nred)) {
+    if constexpr (S::RW) {
+      // one 16-column tile per gated-residual task and per reducer (Params::tpr = 1): its slices only
+      if (d.kind == K_RES && t < d.ntask) dma_mods_tile(c, d, t % d.tiles);
+      else if (d.kind == K_SPLIT && task_first(c, PL_RED) < p.nred) dma_mods_tile(c, d, task_first(c, PL_RED));
+    } else if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && task_first(c, PL_RED) < p.nred)) {
       for (int b = 0; b < p.B; ++b) {
         const float* mr = c.modrow(b, d.s);
         dma_f32(c, mb + b * 2 * S::H * 4, mr + d.mod_off, S::H);
@@ -2374,7 +2404,8 @@ __device__ __forceinline__ void prefetch(Ctx<S>& c, const Desc& d, const int* s_
 // into LDS, by waves 1-3
 template <class S>
 __device__ __forceinline__ void prefetch_shifts(Ctx<S>& c, const Desc& d) {
-  if (c.wave == 0 || !(d.kind == K_QKV || d.kind == K_GU) || d.st == ST_TAIL || d.st == ST_SA || d.st == ST_CA ||
+  // (the row-wise form's tasks load their shift fragments after the poll)
+  if (S::RW || c.wave == 0 || !(d.kind == K_QKV || d.kind == K_GU) || d.st == ST_TAIL || d.st == ST_SA || d.st == ST_CA ||
       task_first(c, d.pk) >= d.ntask)
     return;
   c.dw = c.wave - 1;
