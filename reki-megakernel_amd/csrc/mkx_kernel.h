@@ -109,6 +109,10 @@ struct Shape {
   static constexpr int H = H_, I = I_, NH = H / HD, NKB = H / 32, HT = H / 16, IT = I / 16, SK = I / H;
   // RW: the launch form for many row tiles (row-wise GEMM stages, step-tail output tasks over row chunks)
   static constexpr bool RW = RW_;
+  // attention tasks beyond the grid run as second query tiles of a sample-head (attn_task); compiled into the
+  // row-wise form with fp16-packed weights only: the fp8 row-wise instantiation measured slower with the extra
+  // paths, also for launches that never use them (workload D 7.65 -> 7.86 ms, D-b4 12.79 -> 13.00 ms)
+  static constexpr bool PAIRS = RW_ && !W8_;
   // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): fp16 (packed
   // from bf16), or fp8 e4m3 decoded to fp16 fragments when read (weight-only quantisation)
   static constexpr bool W8 = W8_;
@@ -1577,12 +1581,43 @@ __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float*
 // stages. Heads in complete groups of 8 are arranged so that the query tiles of one head run on one XCD
 // (consecutive workgroups are on consecutive XCDs, so u % 8 is the XCD class) and share its L2; the
 // remaining heads follow compactly.
+// Where the tasks outnumber the G workgroups by X <= G (batched launches; Shape::PAIRS), the X
+// workgroups that run two tasks run two query tiles of one sample-head, so that the second finds the head's
+// keys and values (and, for self-attention, the sample's own rows) still staged in LDS: pair k < X is query
+// tiles 2 j, 2 j + 1 of sample-head k % nhb (j = k / nhb), its first tile task k and its second task k + G
+// (the same workgroup); tasks X .. G - 1 are the tiles in no pair, ordered by query tile, then sample-head.
 struct AttnTask {
   int hh, qt;
   bool ok;
 };
-__device__ __forceinline__ AttnTask attn_task(int u, int nqt, int nhb) {
+template <bool PAIRS>
+__device__ __forceinline__ AttnTask attn_task(int u, int nqt, int nhb, int G) {
   AttnTask a;
+  const int X = nqt * nhb - G;
+  if (PAIRS && X > 0 && X <= G && X <= nhb * (nqt / 2) && u >= 0) {
+    if (u < X) {
+      a.hh = u % nhb;
+      a.qt = 2 * (u / nhb);
+    } else if (u >= G) {
+      const int k = min(u - G, X - 1);
+      a.hh = k % nhb;
+      a.qt = 2 * (k / nhb) + 1;
+    } else {
+      // the r-th tile in no pair: the sample-heads m .. nhb - 1 of tiles 2 jf and 2 jf + 1 (the partly
+      // paired tile pair), then every sample-head of the later tiles
+      const int jf = X / nhb, m = X % nhb, r = u - X;
+      if (m > 0 && r < 2 * (nhb - m)) {
+        a.qt = 2 * jf + r / (nhb - m);
+        a.hh = m + r % (nhb - m);
+      } else {
+        const int r2 = m > 0 ? r - 2 * (nhb - m) : r;
+        a.qt = 2 * jf + (m > 0 ? 2 : 0) + r2 / nhb;
+        a.hh = r2 % nhb;
+      }
+    }
+    a.ok = u < G + X && a.qt < nqt;
+    return a;
+  }
   const int g8 = nhb & ~7, rem = nhb - g8;
   if (u < nqt * g8) {
     const int k = u >> 3;
@@ -1732,19 +1767,24 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
   const int NHB = p.B * S::NH;
   const bool want_kv = (d.s == 0 && p.cur_k != nullptr && p.R > 0);
   const int u0 = task_first(c, PL_SA);
+  int prev_hh = -1;
   for (int v = u0; v < attn_count(NQT, NHB); v += c.G) {
-    const AttnTask at = attn_task(v, NQT, NHB);
+    const AttnTask at = attn_task<S::PAIRS>(v, NQT, NHB, c.G);
     if (!at.ok) continue;
     const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
     const int kvs = s_ks[b];
+    // a second query tile of the sample-head just done: its memory rows, own keys and values (and their RMS
+    // factors) are still in LDS, and the QKV tasks it waits for have already been waited for
+    const bool resident = S::PAIRS && at.hh == prev_hh;
+    prev_hh = at.hh;
     if (v != u0) {
       wait_vm0();
       __syncthreads();
-      sa_prefetch(c, l, b, hd, kvs);
+      if (!resident) sa_prefetch(c, l, b, hd, kvs);
     }
     // the QKV tasks of this head (q, k, v x two column pairs, every row group): the rows' sums of squares
     // and V^T blocks of one head interleave row groups within cache lines
-    {
+    if (!resident) {
       const int rgq = p.rgs_qkv;
       flag_wait<1>(bc, F_QKV, 6 * rgq, [&](int i) {
         const int k = i % 6, rg = i / 6;
@@ -1761,7 +1801,7 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
       __builtin_amdgcn_global_load_lds(ssqk + (long long)(hd * 2 + j) * NRP + b * Mqp + qq, (lds_void*)sq_l, 4, 0, 0);
     }
     const int rt0 = b * Mqp / 16;
-    for (int k = c.wave; k < 4 + 4 * NKT + 8 * KBO; k += NWAVES) {
+    for (int k = c.wave; k < (resident ? 4 : 4 + 4 * NKT + 8 * KBO); k += NWAVES) {
       if (k < 4) {
         const int db = k >> 1, part = k & 1;
         dma16(qs + ((long long)((2 * hd + db) * RT + rt0 + qt) * 2 + part) * 1024 + c.lane * 16, (part ? Ql : Qh) + db * 1024);
@@ -1781,8 +1821,9 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
     const float ssk1 = ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + rowk];
     // The memory blocks need only the Q tile and the memory K/V (prefetched before it): every wave issued at
     // least 4 own-key DMAs after its Q piece (M >= 1 gives NKT >= 2 and KBO >= 1, 20 DMAs over 4 waves), so
-    // at most 4 outstanding operations means its Q piece has landed.
-    wait_vm_le<4>();
+    // at most 4 outstanding operations means its Q piece has landed (a resident tile loads only its Q tile).
+    if (resident) wait_vm0();
+    else wait_vm_le<4>();
     exec_barrier();
     MKX_TR(c, 1);
     AttnState A;
@@ -1794,16 +1835,18 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
       const int kb = mb0 + beta;
       attn_block(A, c.lane, memK + kb * 4096, nullptr, memVt + kb * 4096, nullptr, kvs - kb * 32, PM - kb * 32, qsc, nullptr);
     }
-    wait_vm0();  // the own keys' K and V^T have landed
-    __syncthreads();
-    if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
-    // own keys beyond the sample's rows have no producer: zero their V
-    for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
-      const int key = Mqp + it / HD, dd = it % HD;
-      *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
-      *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
+    if (!resident) {
+      wait_vm0();  // the own keys' K and V^T have landed
+      __syncthreads();
+      if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
+      // own keys beyond the sample's rows have no producer: zero their V
+      for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
+        const int key = Mqp + it / HD, dd = it % HD;
+        *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
+        *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
+      }
+      __syncthreads();
     }
-    __syncthreads();
     // own-key blocks continue the round-robin over the waves (block beta on wave beta % 4)
     for (int beta = nmb + ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES; beta < nmb + KBO; beta += NWAVES) {
       const int kb = beta - nmb;
@@ -1928,18 +1971,23 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   };
   // (wave 0 too, although its poll then completes only after these loads: the workgroups of this stage
   // enter it two stages before their operands are ready, which leaves the loads several microseconds)
-  if (u0 < cnt) pre(attn_task(u0, NQT, NHB).hh % S::NH);
+  if (u0 < cnt) pre(attn_task<S::PAIRS>(u0, NQT, NHB, c.G).hh % S::NH);
   const int rgo = p.rgs_o;
+  int prev_hh = -1;
   for (int v = u0; v < cnt; v += c.G) {
-    const AttnTask at = attn_task(v, NQT, NHB);
+    const AttnTask at = attn_task<S::PAIRS>(v, NQT, NHB, c.G);
     if (!at.ok) continue;
     const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
     const int S_len = s_ks[MAX_BATCH + b];
     const int nch = (S_len + 127) / 128;
+    // a second query tile of the sample-head just done finds its source keys and values still in the ring
+    // when every chunk was resident (at most 3)
+    const bool resident = S::PAIRS && at.hh == prev_hh && nch <= 3;
+    prev_hh = at.hh;
     if (v != u0) {
       wait_vm0();
       __syncthreads();
-      ca_prefetch(c, l, b, hd, S_len);
+      if (!resident) ca_prefetch(c, l, b, hd, S_len);
       pre(hd);
     }
     const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
@@ -2341,7 +2389,7 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   MKX_TRW(c, 8);
   if (d.st == ST_SA || d.st == ST_CA) {
     const int nqt = p.Mqp / 16;
-    const AttnTask at = attn_task(task_first(c, d.pk), nqt, p.B * S::NH);
+    const AttnTask at = attn_task<S::PAIRS>(task_first(c, d.pk), nqt, p.B * S::NH, c.G);
     if (at.ok) {
       const int b = at.hh / S::NH, hd = at.hh % S::NH;
       if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
