@@ -109,10 +109,12 @@ struct Shape {
   static constexpr int H = H_, I = I_, NH = H / HD, NKB = H / 32, HT = H / 16, IT = I / 16, SK = I / H;
   // RW: the launch form for many row tiles (row-wise GEMM stages, step-tail output tasks over row chunks)
   static constexpr bool RW = RW_;
-  // attention tasks beyond the grid run as second query tiles of a sample-head (attn_task); compiled into the
-  // row-wise form with fp16-packed weights only: the fp8 row-wise instantiation measured slower with the extra
-  // paths, also for launches that never use them (workload D 7.65 -> 7.86 ms, D-b4 12.79 -> 13.00 ms)
-  static constexpr bool PAIRS = RW_ && !W8_;
+  // Row-wise attention variants (RW_ATTN): attention tasks beyond the grid run as second query tiles of a
+  // sample-head (attn_task), and cross-attention DMAs its source K/V after its ready-epoch poll instead of
+  // before it. Compiled into the row-wise form with fp16-packed weights only: the fp8 row-wise instantiation
+  // measured slower with them, also for launches that never run the pairs (workload D 7.65 -> 7.86 ms and
+  // D-b4 12.79 -> 13.00 ms with the pairs; 7.65 -> 7.69 and 12.77 -> 12.86 ms with the late K/V DMA).
+  static constexpr bool RW_ATTN = RW_ && !W8_;
   // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): fp16 (packed
   // from bf16), or fp8 e4m3 decoded to fp16 fragments when read (weight-only quantisation)
   static constexpr bool W8 = W8_;
@@ -1581,7 +1583,7 @@ __device__ __forceinline__ void attn_merge_store(Ctx<S>& c, AttnState& A, float*
 // stages. Heads in complete groups of 8 are arranged so that the query tiles of one head run on one XCD
 // (consecutive workgroups are on consecutive XCDs, so u % 8 is the XCD class) and share its L2; the
 // remaining heads follow compactly.
-// Where the tasks outnumber the G workgroups by X <= G (batched launches; Shape::PAIRS), the X
+// Where the tasks outnumber the G workgroups by X <= G (batched launches; Shape::RW_ATTN), the X
 // workgroups that run two tasks run two query tiles of one sample-head, so that the second finds the head's
 // keys and values (and, for self-attention, the sample's own rows) still staged in LDS: pair k < X is query
 // tiles 2 j, 2 j + 1 of sample-head k % nhb (j = k / nhb), its first tile task k and its second task k + G
@@ -1769,13 +1771,13 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
   const int u0 = task_first(c, PL_SA);
   int prev_hh = -1;
   for (int v = u0; v < attn_count(NQT, NHB); v += c.G) {
-    const AttnTask at = attn_task<S::PAIRS>(v, NQT, NHB, c.G);
+    const AttnTask at = attn_task<S::RW_ATTN>(v, NQT, NHB, c.G);
     if (!at.ok) continue;
     const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
     const int kvs = s_ks[b];
     // a second query tile of the sample-head just done: its memory rows, own keys and values (and their RMS
     // factors) are still in LDS, and the QKV tasks it waits for have already been waited for
-    const bool resident = S::PAIRS && at.hh == prev_hh;
+    const bool resident = S::RW_ATTN && at.hh == prev_hh;
     prev_hh = at.hh;
     if (v != u0) {
       wait_vm0();
@@ -1971,23 +1973,23 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   };
   // (wave 0 too, although its poll then completes only after these loads: the workgroups of this stage
   // enter it two stages before their operands are ready, which leaves the loads several microseconds)
-  if (u0 < cnt) pre(attn_task<S::PAIRS>(u0, NQT, NHB, c.G).hh % S::NH);
+  if (u0 < cnt) pre(attn_task<S::RW_ATTN>(u0, NQT, NHB, c.G).hh % S::NH);
   const int rgo = p.rgs_o;
   int prev_hh = -1;
   for (int v = u0; v < cnt; v += c.G) {
-    const AttnTask at = attn_task<S::PAIRS>(v, NQT, NHB, c.G);
+    const AttnTask at = attn_task<S::RW_ATTN>(v, NQT, NHB, c.G);
     if (!at.ok) continue;
     const int b = at.hh / S::NH, hd = at.hh % S::NH, qt = at.qt;
     const int S_len = s_ks[MAX_BATCH + b];
     const int nch = (S_len + 127) / 128;
     // a second query tile of the sample-head just done finds its source keys and values still in the ring
     // when every chunk was resident (at most 3)
-    const bool resident = S::PAIRS && at.hh == prev_hh && nch <= 3;
+    const bool resident = S::RW_ATTN && at.hh == prev_hh && nch <= 3;
     prev_hh = at.hh;
     if (v != u0) {
       wait_vm0();
       __syncthreads();
-      if (!resident) ca_prefetch(c, l, b, hd, S_len);
+      if (!S::RW_ATTN && !resident) ca_prefetch(c, l, b, hd, S_len);
       pre(hd);
     }
     const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
@@ -2033,7 +2035,15 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     }
     // Everything but the query rows has landed (the prefetched K/V chunks were issued before them); the
     // query rows are waited for where the MFMAs use them.
-    wait_vm_le<KPW>();
+    // In the row-wise form every workgroup is busy in the stage before, so loads issued ahead of the poll
+    // hold it up (they return in issue order): with RW_ATTN the K/V chunks are DMA'd only now, after the
+    // query rows have landed, and arrive during the query projection.
+    if constexpr (S::RW_ATTN) {
+      wait_vm0();
+      if (!resident) ca_prefetch(c, l, b, hd, S_len);
+    } else {
+      wait_vm_le<KPW>();
+    }
     __builtin_amdgcn_sched_barrier(0);  // every query-row load is issued before the first MFMA
     MKX_TR(c, 3);
     {
@@ -2105,6 +2115,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       *reinterpret_cast<u32x2*>(Qh + off) = hi;
       *reinterpret_cast<u32x2*>(Ql + off) = lo;
     }
+    if constexpr (S::RW_ATTN) wait_vm0();  // this wave's K/V DMAs (the barrier covers the other waves')
     __syncthreads();
     MKX_TR(c, 1);
     AttnState A;
@@ -2389,11 +2400,11 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   MKX_TRW(c, 8);
   if (d.st == ST_SA || d.st == ST_CA) {
     const int nqt = p.Mqp / 16;
-    const AttnTask at = attn_task<S::PAIRS>(task_first(c, d.pk), nqt, p.B * S::NH, c.G);
+    const AttnTask at = attn_task<S::RW_ATTN>(task_first(c, d.pk), nqt, p.B * S::NH, c.G);
     if (at.ok) {
       const int b = at.hh / S::NH, hd = at.hh % S::NH;
       if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
-      else ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);
+      else if (!S::RW_ATTN) ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);  // (RW_ATTN: after the poll)
     }
   } else if (d.st == ST_TAIL) {
     // workgroups with a tail task: the final modulation rows, and the Wout rows of the task's dims (the real
