@@ -130,9 +130,10 @@ typedef enum {
   MKX_Q_PROFILE_LEN = 5,   /* entries of the caller's timestamp buffer, 0 when profiling is off */
   MKX_Q_WEIGHT_BYTES = 6,  /* bytes of packed linear weights streamed per Euler step */
   MKX_Q_LDS_BYTES = 7,     /* dynamic LDS per workgroup */
-  MKX_Q_GEMM_FORM = 8      /* GEMM form of the last launch: 0 passes, 1 row-wise, -1 before the first launch
+  MKX_Q_GEMM_FORM = 8,     /* GEMM form of the last launch: 0 passes, 1 row-wise, -1 before the first launch
                               (no reference counterpart: the reference has one form; tune_mk.py:69-72 overrides
                               its tile config instead) */
+  MKX_Q_OPERAND_SHIFT = 9  /* the AdaRMS operand shift of later launches (mkx_set_operand_shift) */
 } mkx_query_key;
 
 /* ExpertMegakernel.__init__ (src/mk_expert.py:436-481). Validates dims, copies and repacks the weights
@@ -164,6 +165,16 @@ int mkx_check(mkx_handle* h, void* stream);
  * returns at once, so a launch that cannot complete still drains. No counterpart in the reference, whose
  * grid barrier spins without bound (README.md:262-263); tests use a tiny bound to exercise the path. */
 int mkx_set_spin_limit(mkx_handle* h, uint32_t polls);
+
+/* AdaRMS operand shift of later launches: the fp16 GEMM operand y = h (1 + scale) of every AdaRMS is stored as
+ * y 2^-shift, with the sums of squares of h 2^-shift and eps 2^-2 shift, so that the row's rsqrt(ss / H + eps)
+ * carries the factor 2^shift back (exact powers of two; 0, the default, leaves every result bit unchanged).
+ * The remedy for MKX_ERANGE from mkx_check: a residual stream whose y passes 65504 overflows the fp16 operand
+ * (the launch returns NaN); with shift s it may reach 65504 2^s. Entries of y below 6.1e-5 2^s fall into
+ * fp16's subnormal range and keep fewer significant bits, so a shift is for checkpoints that need it. No
+ * counterpart in the reference, whose bf16 operands have no such limit (src/mk_expert.py:119). MKX_EINVAL
+ * unless 0 <= shift <= 30. */
+int mkx_set_operand_shift(mkx_handle* h, int32_t shift);
 
 /* ExpertMegakernel.barriers (src/mk_expert.py:517-518): stage boundaries one launch of n_steps passes
  * (1 + n_steps (7 L + 1); the first is a grid barrier, the others per-task ready epochs). */

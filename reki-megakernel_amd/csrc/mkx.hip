@@ -1,6 +1,7 @@
 // mkx C ABI (include/mkx.h): handle creation with weight packing, launch, queries.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
@@ -94,13 +95,18 @@ __global__ void xcc_probe(unsigned* out) {
 
 // The megakernel's instantiations live in their own translation units (mkx_mk768.hip, mkx_mk1024.hip,
 // mkx_mk256.hip with GEMM stages in passes; mkx_mk768r.hip, mkx_mk1024r.hip, mkx_mk256r.hip with row-wise GEMM
-// stages), each compiled with its own code-generation options.
+// stages), each compiled with its own code-generation options; each has a twin that scales the AdaRMS
+// operands (YSHIFT), launched only with an operand shift so that the others compile as without it.
 namespace mkx {
-#define MKX_EXTERN(H, I)                                                          \
-  extern template __global__ void mkx_megakernel<H, I, false, false>(Params); \
-  extern template __global__ void mkx_megakernel<H, I, true, false>(Params);  \
-  extern template __global__ void mkx_megakernel<H, I, false, true>(Params);  \
-  extern template __global__ void mkx_megakernel<H, I, true, true>(Params);
+#define MKX_EXTERN(H, I)                                                                \
+  extern template __global__ void mkx_megakernel<H, I, false, false>(Params);       \
+  extern template __global__ void mkx_megakernel<H, I, true, false>(Params);        \
+  extern template __global__ void mkx_megakernel<H, I, false, true>(Params);        \
+  extern template __global__ void mkx_megakernel<H, I, true, true>(Params);         \
+  extern template __global__ void mkx_megakernel<H, I, false, false, true>(Params); \
+  extern template __global__ void mkx_megakernel<H, I, true, false, true>(Params);  \
+  extern template __global__ void mkx_megakernel<H, I, false, true, true>(Params);  \
+  extern template __global__ void mkx_megakernel<H, I, true, true, true>(Params);
 MKX_EXTERN(768, 3072)
 MKX_EXTERN(1024, 4096)
 MKX_EXTERN(256, 512)
@@ -109,17 +115,23 @@ MKX_EXTERN(256, 512)
 
 namespace {
 
-template <int H, int I, bool ROWWISE>
+template <int H, int I, bool ROWWISE, bool YS>
 const void* kernel_of(bool w8) {
-  return w8 ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, ROWWISE>)
-            : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false, ROWWISE>);
+  return w8 ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, ROWWISE, YS>)
+            : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false, ROWWISE, YS>);
+}
+template <int H, int I>
+const void* kernel_of(bool w8, bool rowwise, bool ys) {
+  return rowwise ? (ys ? kernel_of<H, I, true, true>(w8) : kernel_of<H, I, true, false>(w8))
+                 : (ys ? kernel_of<H, I, false, true>(w8) : kernel_of<H, I, false, false>(w8));
 }
 
-// rowwise: the form whose GEMM stages compute whole-K products per wave (launches with many row tiles)
-const void* pick_kernel(int H, int I, bool w8, bool rowwise) {
-  if (H == 768 && I == 3072) return rowwise ? kernel_of<768, 3072, true>(w8) : kernel_of<768, 3072, false>(w8);
-  if (H == 1024 && I == 4096) return rowwise ? kernel_of<1024, 4096, true>(w8) : kernel_of<1024, 4096, false>(w8);
-  if (H == 256 && I == 512) return rowwise ? kernel_of<256, 512, true>(w8) : kernel_of<256, 512, false>(w8);
+// rowwise: the form whose GEMM stages compute whole-K products per wave (launches with many row tiles); ys: the
+// twin with scaled AdaRMS operands (an operand shift)
+const void* pick_kernel(int H, int I, bool w8, bool rowwise, bool ys = false) {
+  if (H == 768 && I == 3072) return kernel_of<768, 3072>(w8, rowwise, ys);
+  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>(w8, rowwise, ys);
+  if (H == 256 && I == 512) return kernel_of<256, 512>(w8, rowwise, ys);
   return nullptr;
 }
 
@@ -286,9 +298,12 @@ struct mkx_handle {
   int profile = 0;
   int plain_launch = 0;  // MKX_PLAIN_LAUNCH=1 at creation: hipLaunchKernel instead of the cooperative launch
   const void* kernel_rows = nullptr;  // the instantiation with row-wise GEMM stages
+  const void* kernel_ys = nullptr;    // the twins of both with scaled AdaRMS operands (an operand shift)
+  const void* kernel_rows_ys = nullptr;
   int gemm_form = -1;    // MKX_GEMM_FORM at creation: 0 passes, 1 row-wise, -1 chosen per launch
   int last_form = -1;    // form of the last launch (0 passes, 1 row-wise; -1 before the first)
   unsigned spin_limit = SPIN_LIMIT;
+  int operand_shift = 0;  // AdaRMS operands stored as y 2^-shift (mkx_set_operand_shift)
   int captured = 0;      // a launch of this handle was captured into a graph: its scratch pointers are frozen
   unsigned long long gen_before = 0;
   long long last_nbar = 0;
@@ -367,6 +382,8 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   h->w8 = w8 ? 1 : 0;
   h->kernel = kern;
   h->kernel_rows = pick_kernel(d.H, d.I, w8, true);
+  h->kernel_ys = pick_kernel(d.H, d.I, w8, false, true);
+  h->kernel_rows_ys = pick_kernel(d.H, d.I, w8, true, true);
   auto bail = [&](int code) { free_handle(h); return code; };
 #define HCHK(x)                                                                                       \
   do {                                                                                                \
@@ -384,6 +401,10 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel does not fit one workgroup per CU"));
   HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, h->kernel_rows, NTHREADS, 0));
   if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel (row-wise GEMM form) does not fit one workgroup per CU"));
+  for (const void* k : {h->kernel_ys, h->kernel_rows_ys}) {
+    HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NTHREADS, 0));
+    if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel (scaled AdaRMS operands) does not fit one workgroup per CU"));
+  }
   h->G = prop.multiProcessorCount;
   {
     const char* pl = std::getenv("MKX_PLAIN_LAUNCH");
@@ -493,6 +514,13 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
 int mkx_set_spin_limit(mkx_handle* h, uint32_t polls) {
   if (!h) return fail(MKX_EINVAL, "null handle");
   h->spin_limit = polls ? polls : SPIN_LIMIT;
+  return MKX_OK;
+}
+
+int mkx_set_operand_shift(mkx_handle* h, int32_t shift) {
+  if (!h) return fail(MKX_EINVAL, "null handle");
+  if (shift < 0 || shift > 30) return fail(MKX_EINVAL, "mkx_set_operand_shift: shift must be in [0, 30]");
+  h->operand_shift = shift;
   return MKX_OK;
 }
 
@@ -647,7 +675,11 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.shs = (char*)h->vts + vt_bytes;
   p.PM = a->PM; p.SP = a->SP; p.L = L; p.Mq = Mq; p.Mqp = Mqp; p.NR = NR; p.NRP = NRP; p.A = d.A;
   p.act = d.activation == MKX_ACT_GELU_TANH ? 1 : 0;
-  p.eps = d.eps; p.qk_eps = d.qk_eps; p.sm_scale = 1.0f / 8.0f;
+  p.qk_eps = d.qk_eps; p.sm_scale = 1.0f / 8.0f;
+  // AdaRMS operands y 2^-shift: the sums of squares and eps scale by 2^-2 shift (exact), eps_final not
+  p.yinv = std::ldexp(1.0f, -h->operand_shift);
+  p.eps = std::ldexp(d.eps, -2 * h->operand_shift);
+  p.eps_final = d.eps;
   p.frames = h->frames; p.frame_bytes = fb; p.steps = h->steps; p.step_bytes = sb;
   p.bar = h->bar; p.flags = h->flags;
   for (int x = 0; x < MAX_XCD; ++x) p.nx[x] = h->nx[x];
@@ -660,7 +692,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
   p.tpr = lay.tpr; p.nred = lay.nred;
   void* args[] = {&p};
-  const void* kern = rows ? h->kernel_rows : h->kernel;
+  const void* kern = h->operand_shift ? (rows ? h->kernel_rows_ys : h->kernel_ys) : (rows ? h->kernel_rows : h->kernel);
   if (capturing) h->captured = 1;
   if (capturing || h->plain_launch) {
     // co-residency was established at creation (one workgroup per CU fits); capture a plain launch
@@ -1083,6 +1115,7 @@ int64_t mkx_query(const mkx_handle* h, int32_t key) {
     case MKX_Q_WEIGHT_BYTES: return h->weight_bytes;
     case MKX_Q_LDS_BYTES: return lds_of(h->d.H, h->d.I);
     case MKX_Q_GEMM_FORM: return h->last_form;
+    case MKX_Q_OPERAND_SHIFT: return h->operand_shift;
     default: return -1;
   }
 }

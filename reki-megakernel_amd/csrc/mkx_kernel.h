@@ -93,6 +93,12 @@ struct Params {
   int nt_o, nt_cao, nt_down;    // 16-column tiles per out-projection / CA out-projection / down task (1 or NTW)
   int lds_red, lds_mods;        // GEMM stages' LDS map: cross-wave reduction buffer, staged modulation slices
   int tpr, nred;                // down-projection reducers: 16-column tiles per reducer, reducers (HT / tpr)
+  // AdaRMS operand scaling by yinv = 2^-E (the instantiations with Shape::YS; E = 0 otherwise), so that a
+  // residual stream beyond the fp16 range of y can be run: the producers of h store y = h (1 + scale) yinv and
+  // the sums of squares of h yinv, and eps is eps_final yinv^2, so the AdaRMS consumers' rsqrt(ss / H + eps)
+  // is exactly 2^E rstd(h) (powers of two scale exactly) and rstd (y W^T) comes out unchanged; eps_final, the
+  // model's eps, serves the step tail's AdaRMS, which sums the squares of h itself
+  float yinv, eps_final;
 };
 
 // placement kinds (Params::pl)
@@ -104,8 +110,10 @@ typedef const __attribute__((address_space(4))) Params CP;
 
 __host__ __device__ constexpr int ceil_to(int a, int m) { return (a + m - 1) / m * m; }
 
-template <int H_, int I_, bool W8_ = false, bool RW_ = false>
+template <int H_, int I_, bool W8_ = false, bool RW_ = false, bool YS_ = false>
 struct Shape {
+  // YS: AdaRMS operands scaled by Params::yinv (the launches with an operand shift)
+  static constexpr bool YS = YS_;
   static constexpr int H = H_, I = I_, NH = H / HD, NKB = H / 32, HT = H / 16, IT = I / 16, SK = I / H;
   // RW: the launch form for many row tiles (row-wise GEMM stages, step-tail output tasks over row chunks)
   static constexpr bool RW = RW_;
@@ -590,8 +598,9 @@ __device__ __forceinline__ void res_piece(Ctx<S>& c, const Desc& d, int tile, in
   const int so = S::RW ? 16 : S::H;
   const f32x4 h = res + v * ldf4(ml);
   st_sc1(d.out, off, as_u4(h));
-  if (st_h4(d.yout, spiece(row, col, c.RT), h * (1.0f + ldf4(ml + so)))) range_error(c.p.bar);
-  float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
+  const f32x4 hs = S::YS ? h * c.p.yinv : h;  // (the AdaRMS operand scaling)
+  if (st_h4(d.yout, spiece(row, col, c.RT), hs * (1.0f + ldf4(ml + so)))) range_error(c.p.bar);
+  float ss = hs[0] * hs[0] + hs[1] * hs[1] + hs[2] * hs[2] + hs[3] * hs[3];
   ss = xor32_sum(xor16_sum(ss));
   if (L < 16) st_sc1_b32(d.ssout, ss_slot<S::HT>(row, tile), __float_as_uint(ss));
 }
@@ -2294,7 +2303,7 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
 #pragma unroll
         for (int k = 0; k < R; ++k) {
           const int ri = min(r0 + NWAVES * k, r_hi - 1);
-          const float rs = rsqrtf(ss[k] * (1.0f / (float)S::H) + p.eps);
+          const float rs = rsqrtf(ss[k] * (1.0f / (float)S::H) + (S::YS ? p.eps_final : p.eps));
           const float* ml = tail_mods_lds(c, ri / p.T);
 #pragma unroll
           for (int q = 0; q < NP; ++q) {
@@ -2381,8 +2390,9 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
                     __uint_as_float(rg.y & 0xffff0000u)};
         }
         st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
-        if (st_h4(c.y0(sn), spiece(row, col, c.RT), v * (1.0f + sc))) range_error(p.bar);
-        float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        const f32x4 vs = S::YS ? v * p.yinv : v;  // (the AdaRMS operand scaling)
+        if (st_h4(c.y0(sn), spiece(row, col, c.RT), vs * (1.0f + sc))) range_error(p.bar);
+        float ss = vs[0] * vs[0] + vs[1] * vs[1] + vs[2] * vs[2] + vs[3] * vs[3];
         ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
         if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot<S::HT>(row, 2 * t + (q >> 2)), __float_as_uint(ss));
       }
@@ -2510,9 +2520,9 @@ __device__ __forceinline__ StagePos next_stage(unsigned mask, StagePos q, int to
 }
 
 // ------------------------------------------------------------------------------------------------
-template <int H, int I, bool W8, bool ROWWISE>
+template <int H, int I, bool W8, bool ROWWISE, bool YSHIFT = false>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
-  using S = Shape<H, I, W8, ROWWISE>;
+  using S = Shape<H, I, W8, ROWWISE, YSHIFT>;
   __shared__ __attribute__((aligned(1024))) char smem[S::LDS];
   CP& p = *(CP*)(__builtin_amdgcn_kernarg_segment_ptr());
   Ctx<S> c(p, smem);

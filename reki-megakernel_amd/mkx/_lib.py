@@ -11,11 +11,13 @@ MAX_LAYERS = 32
 OK, EINVAL, ENORESIDENT, EHIP, ETIMEOUT, ENOMEM, EUNSUPPORTED, ERANGE = range(8)
 WEIGHTS_BF16, WEIGHTS_FP8_E4M3 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
-Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WEIGHT_BYTES, Q_LDS_BYTES, Q_GEMM_FORM = range(9)
+Q_GRID, Q_BLOCK, Q_BARRIER_COUNT, Q_ERROR_FLAG, _Q_RESERVED, Q_PROFILE_LEN, Q_WEIGHT_BYTES, Q_LDS_BYTES, Q_GEMM_FORM, \
+    Q_OPERAND_SHIFT = range(10)
 
 EXPORTS = ("mkx_create", "mkx_run", "mkx_check", "mkx_barriers", "mkx_set_profile", "mkx_query", "mkx_destroy",
            "mkx_last_error", "mkx_status_string", "mkx_abi_version", "mkx_ring_append", "mkx_source_create", "mkx_source_run", "mkx_source_destroy",
-           "mkx_modulations", "mkx_set_spin_limit", "mkx_source_run_noalloc", "mkx_modulation_input", "mkx_probe")
+           "mkx_modulations", "mkx_set_spin_limit", "mkx_source_run_noalloc", "mkx_modulation_input", "mkx_probe",
+           "mkx_set_operand_shift")
 PROBE_BARRIER, PROBE_HANDOFF = 0, 1
 
 _vp = ctypes.c_void_p
@@ -117,6 +119,7 @@ def lib() -> ctypes.CDLL:
         L.mkx_modulations.argtypes = [ctypes.POINTER(MkxModprojArgs), _vp]
         L.mkx_modulation_input.argtypes = [ctypes.POINTER(MkxModinArgs), _vp]
         L.mkx_set_spin_limit.argtypes = [_vp, ctypes.c_uint32]
+        L.mkx_set_operand_shift.argtypes = [_vp, ctypes.c_int32]
         L.mkx_probe.argtypes = [ctypes.POINTER(MkxProbeArgs), _vp]
         _LIB = L
     return _LIB

@@ -113,6 +113,31 @@ class ExpertMegakernel:
                 tensors[f"{name}[{l}].k"], tensors[f"{name}[{l}].v"] = k, v
         require_device(self.device, **tensors)
 
+    def set_operand_shift(self, shift: int) -> None:
+        """AdaRMS operands of later launches stored as y 2^-shift (0 = the default, every result bit as without
+        it): the remedy when ``check`` raises MKX_ERANGE, a residual stream beyond the fp16 operand range."""
+        check(lib().mkx_set_operand_shift(self._h, int(shift)), "mkx_set_operand_shift")
+
+    @property
+    def operand_shift(self) -> int:
+        return int(lib().mkx_query(self._h, _lib.Q_OPERAND_SHIFT))
+
+    def run_checked(self, x_t: torch.Tensor, mods: torch.Tensor, dt, past, action_dim: int, shift_step: int = 8,
+                    max_shift: int = 24) -> torch.Tensor:
+        """``run``, then ``check`` (synchronises); a launch that overflowed an fp16 operand (MKX_ERANGE) is run
+        again with the operand shift raised by ``shift_step``, up to ``max_shift``, and the handle keeps the shift
+        that worked. Any other error is raised."""
+        while True:
+            x = self.run(x_t, mods, dt, past, action_dim)
+            try:
+                self.check()
+                return x
+            except _lib.MkxError as e:
+                shift = self.operand_shift
+                if e.status != _lib.ERANGE or shift + shift_step > max_shift:
+                    raise
+                self.set_operand_shift(shift + shift_step)
+
     def set_spin_limit(self, polls: int | None) -> None:
         """Spin bound (polls) of every wait of later launches; None restores the default (about 0.5 s)."""
         check(lib().mkx_set_spin_limit(self._h, 0 if polls is None else int(polls)), "mkx_set_spin_limit")

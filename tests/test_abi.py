@@ -105,6 +105,12 @@ def test_spin_limit_setter_rejects_a_null_handle():
     assert L.mkx_set_spin_limit(None, 5) == _lib.EINVAL
 
 
+def test_operand_shift_setter_rejects_a_null_handle():
+    L = _lib.lib()
+    assert L.mkx_set_operand_shift(None, 8) == _lib.EINVAL
+    assert L.mkx_query(None, _lib.Q_OPERAND_SHIFT) == -1
+
+
 class _Past:
     def __init__(self, step, ca):
         self.register_step, self.cross_attn_kv = step, ca
@@ -155,7 +161,7 @@ def test_query_keys_match_the_header():
     assert keys, "no query keys found"
     for name, val in keys.items():
         assert getattr(_lib, name) == val, name
-    assert keys["Q_GEMM_FORM"] == 8
+    assert keys["Q_GEMM_FORM"] == 8 and keys["Q_OPERAND_SHIFT"] == 9
 
 
 @pytest.mark.parametrize("over", [dict(kind=5), dict(n=3), dict(n=0), dict(n=4096), dict(reps=0), dict(bytes=1000)])

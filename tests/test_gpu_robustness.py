@@ -294,3 +294,65 @@ def test_fp16_operand_range_headroom_of_workload_a():
     mk.check()
     assert torch.isfinite(x).all()
     mk.close()
+
+
+def test_operand_shift_runs_a_residual_stream_beyond_the_fp16_range():
+    """The remedy for MKX_ERANGE. The register tokens are scaled by 4^k (exact in bf16) until the register
+    rows' residual stream makes an AdaRMS operand leave the fp16 range: the launch reports MKX_ERANGE at the
+    default operand shift, and run_checked raises the shift by 8 (as often as needed) and returns actions (O(1):
+    the action rows see the register rows only through normalised keys and values) that track the fp32
+    oracle run with the same tokens within the parity bounds; the handle keeps the shift. At the unscaled
+    tokens, shift 8 also stays within the bounds (operands of y below 6.1e-5 x 256 lose bits to fp16
+    subnormals), and shift 0 again gives the default result bit for bit."""
+    cfg = SY.WORKLOADS["A"]
+    case = make_case(cfg)
+    x1 = _first_step(case)
+    mk = ExpertMegakernel(case["model"])
+    n = cfg.num_steps - 1
+    args = (case["mods"], case["dt"], case["past"], cfg.action_dim)
+    x0 = mk.run(x1, *args).clone()
+    mk.check()
+    assert mk.operand_shift == 0
+    tok = case["W"]["reg_tok"]
+    k_bad = None
+    for k in range(1, 20):
+        mk.register_tokens = (tok.float() * float(4 ** k)).to(torch.bfloat16).to(x1.device)
+        mk.run(x1, *args)
+        torch.cuda.synchronize()
+        try:
+            mk.check()
+        except MkxError as e:
+            assert e.status == _lib.ERANGE, e
+            k_bad = k
+            break
+    assert k_bad is not None
+    x = mk.run_checked(x1, *args).clone()
+    shift = mk.operand_shift
+    assert shift >= 8 and torch.isfinite(x).all()
+    W0 = dict(case["W"])
+    case["W"] = dict(W0, reg_tok=(tok.float() * float(4 ** k_bad)).to(torch.bfloat16))
+    try:
+        ref = oracle_steps(case, x1, 1, n, "fp32")
+    finally:
+        case["W"] = W0
+    mx, mean = diff(x, ref, cfg.action_dim)
+    _report("operand shift past the fp16 range (A, register tokens x 4^k)", token_scale=4 ** k_bad, shift=shift,
+            max_abs=mx, mean_abs=mean)
+    assert mx <= 1e-2 and mean <= 2e-3, (mx, mean)
+    mk.register_tokens = tok.to(x1.device)
+    mk.set_operand_shift(8)
+    x8 = mk.run(x1, *args).clone()
+    mk.check()
+    ref1 = oracle_steps(case, x1, 1, n, "fp32")
+    mx8, mean8 = diff(x8, ref1, cfg.action_dim)
+    mx0, mean0 = diff(x0, ref1, cfg.action_dim)
+    _report("operand shift 8 at the unscaled tokens (A)", max_abs=mx8, mean_abs=mean8, shift0_max_abs=mx0,
+            shift0_mean_abs=mean0)
+    assert mx8 <= 1e-2 and mean8 <= 2e-3, (mx8, mean8)
+    mk.set_operand_shift(0)
+    x = mk.run(x1, *args)
+    mk.check()
+    assert torch.equal(x, x0)
+    with pytest.raises(MkxError):
+        mk.set_operand_shift(31)
+    mk.close()
