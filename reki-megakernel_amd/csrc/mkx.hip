@@ -169,6 +169,7 @@ ShapeK shape_k(int H, int I, bool w8) {
 struct Layout {
   int pl[PL_KINDS];
   int rgs_qkv, rgs_o, rgs_cao, nt_o, nt_cao, nt_down, lds_red, lds_mods, tpr, nred;
+  int nrg;  // reducer row groups (row-wise form: the QKV row groups)
   bool disjoint;
 };
 // step-tail output tasks: TAIL_AC dims each, or, in the row-wise form, TAIL_DG dims of TAIL_RCH rows each
@@ -208,7 +209,10 @@ Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A,
   // operand share, and they fit beside the QKV tasks); otherwise one per 16-column tile, so that batched
   // shapes, whose reductions cover many row tiles, spread them over more workgroups
   L.tpr = L.disjoint ? nt : 1;
-  L.nred = k.HT / L.tpr;
+  // the row-wise form's reducers also split the rows, in the QKV stage's row groups (each then loads a third or
+  // a half of a tile's partials, and a QKV task waits only for its own row group's reducers)
+  L.nrg = rows ? L.rgs_qkv : 1;
+  L.nred = k.HT / L.tpr * L.nrg;
   cnt[PL_RED] = L.nred;
   cnt[PL_TIN] = k.NIN;
   cnt[PL_TOUT] = nout;
@@ -590,7 +594,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
     // head (self-attention)
     const int RTn = NRP / 16, NH = H / 64;
     if ((sk.HT / lay.nt_cao) * lay.rgs_cao > 256 || ((RTn + lay.rgs_o - 1) / lay.rgs_o) * NH > 256 ||
-        ((RTn + lay.rgs_cao - 1) / lay.rgs_cao) * NH > 256 || sk.HT > 64 || 6 * lay.rgs_qkv > 64)
+        ((RTn + lay.rgs_cao - 1) / lay.rgs_cao) * NH > 256 || sk.HT > 64 || 6 * lay.rgs_qkv > 64 || lay.nred > 256)
       return fail(MKX_EUNSUPPORTED, "row grouping needs more than 256 ready epochs per wait");
     if (lay.lds_mods + a->B * 2 * H * 4 > sk.SMALL) return fail(MKX_EUNSUPPORTED, "GEMM LDS map does not fit");
   }
@@ -690,7 +694,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.rgs_qkv = lay.rgs_qkv; p.rgs_o = lay.rgs_o; p.rgs_cao = lay.rgs_cao;
   p.nt_o = lay.nt_o; p.nt_cao = lay.nt_cao; p.nt_down = lay.nt_down;
   p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
-  p.tpr = lay.tpr; p.nred = lay.nred;
+  p.tpr = lay.tpr; p.nred = lay.nred; p.nrg = lay.nrg;
   void* args[] = {&p};
   const void* kern = h->operand_shift ? (rows ? h->kernel_rows_ys : h->kernel_ys) : (rows ? h->kernel_rows : h->kernel);
   if (capturing) h->captured = 1;

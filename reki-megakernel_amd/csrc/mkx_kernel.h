@@ -99,6 +99,10 @@ struct Params {
   // is exactly 2^E rstd(h) (powers of two scale exactly) and rstd (y W^T) comes out unchanged; eps_final, the
   // model's eps, serves the step tail's AdaRMS, which sums the squares of h itself
   float yinv, eps_final;
+  // down-projection reducers of the row-wise form: row groups per tile (the QKV stage's row groups, so that a
+  // QKV task waits for its own row group's reducers); reducer r = tile r % HT of row group r / HT; 1 in the
+  // form with passes
+  int nrg;
 };
 
 // placement kinds (Params::pl)
@@ -849,7 +853,12 @@ __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, 
   const int NQT = c.p.Mqp / 16;
   if (d.st == ST_QKV) {
     // every column of its rows: the step tail's in-projection tasks, or the down projection's reducers
-    flag_wait<1>(bc, d.l == 0 ? F_TAIL_IN : F_DOWN, d.l == 0 ? S::NIN : c.p.nred, [](int i) { return i; }, (unsigned long long)g);
+    if (d.l == 0) flag_wait<1>(bc, F_TAIL_IN, S::NIN, [](int i) { return i; }, (unsigned long long)g);
+    else if constexpr (S::RW) {
+      // the reducers of this task's row group (the row groups are the same)
+      const int rg = split;
+      flag_wait<1>(bc, F_DOWN, S::HT, [&](int i) { return rg * S::HT + i; }, (unsigned long long)g);
+    } else flag_wait<1>(bc, F_DOWN, c.p.nred, [](int i) { return i; }, (unsigned long long)g);
   } else if (d.st == ST_O || d.st == ST_CAO) {
     flag_wait(bc, d.st == ST_O ? F_SA : F_CA, (rt_hi - rt_lo) * S::NH, [&](int i) {
       const int rt = rt_lo + i / S::NH, hd = i % S::NH;
@@ -870,7 +879,10 @@ __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, 
 template <class S, int TPR>
 __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc, int g, int r) {
   constexpr int tpr = TPR;
-  const int RT = c.RT, t0 = r * tpr;
+  const int RT = c.RT;
+  // (row-wise form: reducer r covers tile r % HT over the row tiles of row group r / HT)
+  const int rgr = S::RW ? r / S::HT : 0, t0 = (S::RW ? r % S::HT : r) * tpr;
+  const int rlo = rgr * RT / c.p.nrg, nrt = (rgr + 1) * RT / c.p.nrg - rlo;
   // the tile groups (split tasks per split) holding tiles t0 .. t0 + tpr - 1
   const int g0 = t0 / d.nt, ng = (t0 + tpr - 1) / d.nt - g0 + 1;
   flag_wait<1>(bc, F_DPART, S::SK * ng, [&](int i) { return (i % S::SK) * d.tiles + g0 + i / S::SK; }, (unsigned long long)g);
@@ -879,14 +891,14 @@ __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc
   // one (tile, row tile) block of 64 items per wave and round (lanes L, L^16, L^32, L^48 hold one row);
   // the loads of RR rounds are issued together, so their latencies overlap
   constexpr int RR = 3;
-  const int nblk = tpr * RT;
+  const int nblk = tpr * nrt;
   for (int b0 = c.wave; b0 < nblk; b0 += NWAVES * RR) {
     u32x4 xp[RR][S::SK];
     f32x4 res[RR];
 #pragma unroll
     for (int k = 0; k < RR; ++k) {
       const int blk = min(b0 + NWAVES * k, nblk - 1);
-      const int tile = t0 + blk / RT, rtg = blk % RT, L = c.lane;
+      const int tile = t0 + blk / nrt, rtg = rlo + blk % nrt, L = c.lane;
 #pragma unroll
       for (int j = 0; j < S::SK; ++j) xp[k][j] = ld16((const char*)d.part + ((((j * S::HT + tile) * RT + rtg) * 64 + L) * 16));
       res[k] = as_f4(ld16((const char*)d.res + fpiece(rtg * 16 + (L & 15), tile * 16 + 4 * (L >> 4), RT)));
@@ -895,7 +907,7 @@ __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc
     for (int k = 0; k < RR; ++k) {
       const int blk = b0 + NWAVES * k;
       if (blk >= nblk) break;
-      const int tile = t0 + blk / RT, rtg = blk % RT, L = c.lane;
+      const int tile = t0 + blk / nrt, rtg = rlo + blk % nrt, L = c.lane;
       const int row = rtg * 16 + (L & 15), col = tile * 16 + 4 * (L >> 4);
       f32x4 v = as_f4(xp[k][0]);
 #pragma unroll
@@ -2248,7 +2260,8 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     } else if (!d.first) {
       // every tile of the last layer's output (its reducers), and x of this step (the previous step tail's
       // output dims)
-      flag_wait<1>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
+      if (p.nred <= 64) flag_wait<1>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
+      else flag_wait<4>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
       if (d.s > 0) flag_wait<1>(bc, F_TAIL_OUT, nout, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
     }
     // the staged final modulation rows and Wout rows (DMA'd by the prefetch) have landed
@@ -2446,7 +2459,7 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
     if constexpr (S::RW) {
       // one 16-column tile per gated-residual task and per reducer (Params::tpr = 1): its slices only
       if (d.kind == K_RES && t < d.ntask) dma_mods_tile(c, d, t % d.tiles);
-      else if (d.kind == K_SPLIT && task_first(c, PL_RED) < p.nred) dma_mods_tile(c, d, task_first(c, PL_RED));
+      else if (d.kind == K_SPLIT && task_first(c, PL_RED) < p.nred) dma_mods_tile(c, d, task_first(c, PL_RED) % S::HT);
     } else if ((d.kind == K_RES && t < d.ntask) || (d.kind == K_SPLIT && task_first(c, PL_RED) < p.nred)) {
       for (int b = 0; b < p.B; ++b) {
         const float* mr = c.modrow(b, d.s);
