@@ -853,12 +853,14 @@ __device__ __forceinline__ void gemm_wait(Ctx<S>& c, const Desc& d, BarCtx& bc, 
   const int NQT = c.p.Mqp / 16;
   if (d.st == ST_QKV) {
     // every column of its rows: the step tail's in-projection tasks, or the down projection's reducers
-    if (d.l == 0) flag_wait<1>(bc, F_TAIL_IN, S::NIN, [](int i) { return i; }, (unsigned long long)g);
-    else if constexpr (S::RW) {
-      // the reducers of this task's row group (the row groups are the same)
+    if constexpr (S::RW) {
+      // (row-wise form: the reducers of this task's row group; the row groups are the same)
       const int rg = split;
-      flag_wait<1>(bc, F_DOWN, S::HT, [&](int i) { return rg * S::HT + i; }, (unsigned long long)g);
-    } else flag_wait<1>(bc, F_DOWN, c.p.nred, [](int i) { return i; }, (unsigned long long)g);
+      if (d.l == 0) flag_wait<1>(bc, F_TAIL_IN, S::NIN, [](int i) { return i; }, (unsigned long long)g);
+      else flag_wait<1>(bc, F_DOWN, S::HT, [&](int i) { return rg * S::HT + i; }, (unsigned long long)g);
+    } else {
+      flag_wait<1>(bc, d.l == 0 ? F_TAIL_IN : F_DOWN, d.l == 0 ? S::NIN : c.p.nred, [](int i) { return i; }, (unsigned long long)g);
+    }
   } else if (d.st == ST_O || d.st == ST_CAO) {
     flag_wait(bc, d.st == ST_O ? F_SA : F_CA, (rt_hi - rt_lo) * S::NH, [&](int i) {
       const int rt = rt_lo + i / S::NH, hd = i % S::NH;
@@ -880,9 +882,19 @@ template <class S, int TPR>
 __device__ __forceinline__ void down_reduce(Ctx<S>& c, const Desc& d, BarCtx& bc, int g, int r) {
   constexpr int tpr = TPR;
   const int RT = c.RT;
-  // (row-wise form: reducer r covers tile r % HT over the row tiles of row group r / HT)
-  const int rgr = S::RW ? r / S::HT : 0, t0 = (S::RW ? r % S::HT : r) * tpr;
-  const int rlo = rgr * RT / c.p.nrg, nrt = (rgr + 1) * RT / c.p.nrg - rlo;
+  // (row-wise form: reducer r covers tile r % HT over the row tiles of row group r / HT; the form with
+  // passes: tiles r tpr .. of every row tile)
+  int t0, rlo, nrt;
+  if constexpr (S::RW) {
+    const int rgr = r / S::HT;
+    t0 = (r % S::HT) * tpr;
+    rlo = rgr * RT / c.p.nrg;
+    nrt = (rgr + 1) * RT / c.p.nrg - rlo;
+  } else {
+    t0 = r * tpr;
+    rlo = 0;
+    nrt = RT;
+  }
   // the tile groups (split tasks per split) holding tiles t0 .. t0 + tpr - 1
   const int g0 = t0 / d.nt, ng = (t0 + tpr - 1) / d.nt - g0 + 1;
   flag_wait<1>(bc, F_DPART, S::SK * ng, [&](int i) { return (i % S::SK) * d.tiles + g0 + i / S::SK; }, (unsigned long long)g);
@@ -2240,17 +2252,21 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     const bool inproj = t < nin;
     const int a_out = t - nin;
     // in-projection item of this thread (first pass): row, 4-column piece q of the task's 32 columns; its
-    // constant operands
+    // constant operands (row-wise form: the piece's bias, the same in every item, items being 8 per row)
     const int row0 = c.tid >> 3, q0 = c.tid & 7;
     f32x4 sc0 = {0.f, 0.f, 0.f, 0.f}, bv0 = {0.f, 0.f, 0.f, 0.f};
     uint2 rg0 = {0u, 0u};
     f32x4 wt = {0.f, 0.f, 0.f, 0.f};
     if (inproj) {
-      const int b = row0 / p.Mqp, i = row0 - b * p.Mqp, col = t * 32 + 4 * q0;
-      if (row0 < p.NRP) {
-        sc0 = ldf4(c.modrow(min(b, p.B - 1), sn) + col);  // layer 0 self-attention AdaRMS scale
-        if (b < p.B && i < p.T) bv0 = ldf4(p.bin + col);
-        else if (b < p.B && i < p.Mq) rg0 = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
+      if constexpr (S::RW) {
+        bv0 = ldf4(p.bin + t * 32 + 4 * q0);
+      } else {
+        const int b = row0 / p.Mqp, i = row0 - b * p.Mqp, col = t * 32 + 4 * q0;
+        if (row0 < p.NRP) {
+          sc0 = ldf4(c.modrow(min(b, p.B - 1), sn) + col);  // layer 0 self-attention AdaRMS scale
+          if (b < p.B && i < p.T) bv0 = ldf4(p.bin + col);
+          else if (b < p.B && i < p.Mq) rg0 = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
+        }
       }
       if (c.tid < adim * 8) wt = ldf4(p.win + (long long)(c.tid >> 3) * S::H + t * 32 + 4 * (c.tid & 7));
     }
@@ -2260,8 +2276,12 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
     } else if (!d.first) {
       // every tile of the last layer's output (its reducers), and x of this step (the previous step tail's
       // output dims)
-      if (p.nred <= 64) flag_wait<1>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
-      else flag_wait<4>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
+      if constexpr (S::RW) {  // (row-wise form: up to HT x 3 row-group reducers)
+        if (p.nred <= 64) flag_wait<1>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
+        else flag_wait<4>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
+      } else {
+        flag_wait<1>(bc, F_DOWN, p.nred, [](int i) { return i; }, (unsigned long long)g);
+      }
       if (d.s > 0) flag_wait<1>(bc, F_TAIL_OUT, nout, [](int i) { return i; }, (unsigned long long)(g - (STAGES_PER_LAYER * p.L + 1) + 1));
     }
     // the staged final modulation rows and Wout rows (DMA'd by the prefetch) have landed
@@ -2377,37 +2397,79 @@ __device__ __forceinline__ void tail_stage(Ctx<S>& c, const Desc& d, BarCtx& bc,
       __syncthreads();
       MKX_TR(c, 1);
       float* h0n = c.h0(sn);
-      // item: row, 4-column piece q of the task's tiles 2 t (q < 4) and 2 t + 1
-      for (int it = c.tid; it < p.NRP * 8; it += NTHREADS) {
-        const int row = it >> 3, q = it & 7;
-        const int b = row / p.Mqp, i = row - b * p.Mqp;
-        const int col = t * 32 + 4 * q;
-        f32x4 v, sc;
-        uint2 rg;
-        if (it == c.tid) {
-          v = bv0;
-          sc = sc0;
-          rg = rg0;
-        } else {
-          v = f32x4{0.f, 0.f, 0.f, 0.f};
-          rg = uint2{0u, 0u};
-          sc = ldf4(c.modrow(min(b, p.B - 1), sn) + col);
-          if (b < p.B && i < p.T) v = ldf4(p.bin + col);
-          else if (b < p.B && i < p.Mq) rg = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
+      if constexpr (S::RW) {
+        // items: row, 4-column piece q of the task's tiles 2 t (q < 4) and 2 t + 1; a thread's items are rows
+        // 32 apart (many, in this form), IB of them per batch with their loads (the row's sample's layer-0
+        // AdaRMS scale, a register row's token) issued together, so that a batch waits for one memory round
+        // trip, not one per row
+        constexpr int IB = 4;
+        const int q = q0, col = t * 32 + 4 * q;
+        for (int row1 = row0; row1 < p.NRP; row1 += IB * (NTHREADS / 8)) {
+          f32x4 sc[IB];
+          uint2 rg[IB];
+#pragma unroll
+          for (int k = 0; k < IB; ++k) {
+            const int row = min(row1 + k * (NTHREADS / 8), p.NRP - 1);
+            const int b = row / p.Mqp, i = row - b * p.Mqp;
+            sc[k] = ldf4(c.modrow(min(b, p.B - 1), sn) + col);  // layer 0 self-attention AdaRMS scale
+            const int ir = min(max(i - p.T, 0), max(p.R - 1, 0));  // (a valid register row, used for register rows only)
+            rg[k] = p.R > 0 ? *reinterpret_cast<const uint2*>(p.reg_tok + (long long)ir * S::H + col) : uint2{0u, 0u};
+          }
+#pragma unroll
+          for (int k = 0; k < IB; ++k) {
+            const int row = row1 + k * (NTHREADS / 8);
+            if (row >= p.NRP) break;
+            const int b = row / p.Mqp, i = row - b * p.Mqp;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (b < p.B && i < p.T) {
+              v = bv0;
+              const float* xr = xp + (b * p.T + i) * adim;
+              for (int a = 0; a < adim; ++a) v += xr[a] * ldf4(win_t + a * 32 + 4 * q);
+            } else if (b < p.B && i < p.Mq) {
+              v = f32x4{__uint_as_float(rg[k].x << 16), __uint_as_float(rg[k].x & 0xffff0000u), __uint_as_float(rg[k].y << 16),
+                        __uint_as_float(rg[k].y & 0xffff0000u)};
+            }
+            st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
+            const f32x4 vs = S::YS ? v * p.yinv : v;  // (the AdaRMS operand scaling)
+            if (st_h4(c.y0(sn), spiece(row, col, c.RT), vs * (1.0f + sc[k]))) range_error(p.bar);
+            float ss = vs[0] * vs[0] + vs[1] * vs[1] + vs[2] * vs[2] + vs[3] * vs[3];
+            ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
+            if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot<S::HT>(row, 2 * t + (q >> 2)), __float_as_uint(ss));
+          }
         }
-        if (b < p.B && i < p.T) {
-          const float* xr = xp + (b * p.T + i) * adim;
-          for (int a = 0; a < adim; ++a) v += xr[a] * ldf4(win_t + a * 32 + 4 * q);
-        } else if (b < p.B && i < p.Mq) {
-          v = f32x4{__uint_as_float(rg.x << 16), __uint_as_float(rg.x & 0xffff0000u), __uint_as_float(rg.y << 16),
-                    __uint_as_float(rg.y & 0xffff0000u)};
+      } else {
+        // item: row, 4-column piece q of the task's tiles 2 t (q < 4) and 2 t + 1
+        for (int it = c.tid; it < p.NRP * 8; it += NTHREADS) {
+          const int row = it >> 3, q = it & 7;
+          const int b = row / p.Mqp, i = row - b * p.Mqp;
+          const int col = t * 32 + 4 * q;
+          f32x4 v, sc;
+          uint2 rg;
+          if (it == c.tid) {
+            v = bv0;
+            sc = sc0;
+            rg = rg0;
+          } else {
+            v = f32x4{0.f, 0.f, 0.f, 0.f};
+            rg = uint2{0u, 0u};
+            sc = ldf4(c.modrow(min(b, p.B - 1), sn) + col);
+            if (b < p.B && i < p.T) v = ldf4(p.bin + col);
+            else if (b < p.B && i < p.Mq) rg = *reinterpret_cast<const uint2*>(p.reg_tok + (long long)(i - p.T) * S::H + col);
+          }
+          if (b < p.B && i < p.T) {
+            const float* xr = xp + (b * p.T + i) * adim;
+            for (int a = 0; a < adim; ++a) v += xr[a] * ldf4(win_t + a * 32 + 4 * q);
+          } else if (b < p.B && i < p.Mq) {
+            v = f32x4{__uint_as_float(rg.x << 16), __uint_as_float(rg.x & 0xffff0000u), __uint_as_float(rg.y << 16),
+                      __uint_as_float(rg.y & 0xffff0000u)};
+          }
+          st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
+          const f32x4 vs = S::YS ? v * p.yinv : v;  // (the AdaRMS operand scaling)
+          if (st_h4(c.y0(sn), spiece(row, col, c.RT), vs * (1.0f + sc))) range_error(p.bar);
+          float ss = vs[0] * vs[0] + vs[1] * vs[1] + vs[2] * vs[2] + vs[3] * vs[3];
+          ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
+          if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot<S::HT>(row, 2 * t + (q >> 2)), __float_as_uint(ss));
         }
-        st_sc1(h0n, fpiece(row, col, c.RT), as_u4(v));
-        const f32x4 vs = S::YS ? v * p.yinv : v;  // (the AdaRMS operand scaling)
-        if (st_h4(c.y0(sn), spiece(row, col, c.RT), vs * (1.0f + sc))) range_error(p.bar);
-        float ss = vs[0] * vs[0] + vs[1] * vs[1] + vs[2] * vs[2] + vs[3] * vs[3];
-        ss = quad_sum(ss);  // the 4 pieces of one 16-column tile are 4 adjacent lanes
-        if ((q & 3) == 0) st_sc1_b32(c.ss0(sn), ss_slot<S::HT>(row, 2 * t + (q >> 2)), __float_as_uint(ss));
       }
     }
     flag_publish(bc, inproj ? F_TAIL_IN : F_TAIL_OUT, inproj ? t : a_out, (unsigned long long)g + 1);
