@@ -356,3 +356,64 @@ def test_operand_shift_runs_a_residual_stream_beyond_the_fp16_range():
     with pytest.raises(MkxError):
         mk.set_operand_shift(31)
     mk.close()
+
+
+@pytest.mark.parametrize("name", ["B", "tiny fp8 b3"])
+def test_operand_shift_in_the_row_wise_form(name):
+    """The operand shift in the row-wise kernels (fp16-packed and fp8 weights): their shift twins track the fp32
+    oracle at shift 8 and, with register tokens scaled past the fp16 range (MKX_ERANGE at shift 0), after
+    run_checked has raised the shift; shift 0 again gives the default result bit for bit."""
+    cfg = SY.WORKLOADS["B"] if name == "B" else replace(TINY, B=3, weight_dtype="fp8_e4m3")
+    import os
+    old = os.environ.get("MKX_GEMM_FORM")
+    os.environ["MKX_GEMM_FORM"] = "rows"
+    try:
+        case = make_case(cfg)
+        mk = ExpertMegakernel(case["model"])
+    finally:
+        if old is None:
+            os.environ.pop("MKX_GEMM_FORM", None)
+        else:
+            os.environ["MKX_GEMM_FORM"] = old
+    x1 = _first_step(case)
+    n = cfg.num_steps - 1
+    args = (case["mods"], case["dt"], case["past"], cfg.action_dim)
+    x0 = mk.run(x1, *args).clone()
+    mk.check()
+    assert int(_lib.lib().mkx_query(mk._h, _lib.Q_GEMM_FORM)) == 1  # the form of the last launch
+    ref = oracle_steps(case, x1, 1, n, "fp32")
+    mk.set_operand_shift(8)
+    x8 = mk.run(x1, *args).clone()
+    mk.check()
+    mx8, mean8 = diff(x8, ref, cfg.action_dim)
+    mx0, mean0 = diff(x0, ref, cfg.action_dim)
+    assert mx8 <= 1e-2 and mean8 <= 2e-3, (mx8, mean8)
+    mk.set_operand_shift(0)
+    assert torch.equal(mk.run(x1, *args), x0)
+    mk.check()
+    tok = case["W"]["reg_tok"]
+    k_bad = None
+    for k in range(1, 20):
+        mk.register_tokens = (tok.float() * float(4 ** k)).to(torch.bfloat16).to(x1.device)
+        mk.run(x1, *args)
+        torch.cuda.synchronize()
+        try:
+            mk.check()
+        except MkxError as e:
+            assert e.status == _lib.ERANGE, e
+            k_bad = k
+            break
+    assert k_bad is not None
+    x = mk.run_checked(x1, *args).clone()
+    shift = mk.operand_shift
+    W0 = dict(case["W"])
+    case["W"] = dict(W0, reg_tok=(tok.float() * float(4 ** k_bad)).to(torch.bfloat16))
+    try:
+        ref_big = oracle_steps(case, x1, 1, n, "fp32")
+    finally:
+        case["W"] = W0
+    mx, mean = diff(x, ref_big, cfg.action_dim)
+    _report(f"operand shift, row-wise form ({name})", shift8_max_abs=mx8, shift8_mean_abs=mean8, shift0_max_abs=mx0,
+            shift0_mean_abs=mean0, token_scale=4 ** k_bad, shift=shift, max_abs=mx, mean_abs=mean)
+    assert shift >= 8 and mx <= 1e-2 and mean <= 2e-3, (shift, mx, mean)
+    mk.close()
