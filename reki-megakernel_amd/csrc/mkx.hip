@@ -695,6 +695,12 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.nt_o = lay.nt_o; p.nt_cao = lay.nt_cao; p.nt_down = lay.nt_down;
   p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
   p.tpr = lay.tpr; p.nred = lay.nred; p.nrg = lay.nrg;
+  {
+    // cross-attention tasks of two query tiles (row-wise attention variants): where the one-tile tasks
+    // outnumber the workgroups, the two-tile tasks do not, and every source fits the three LDS ring slots
+    const int nhb = a->B * (H / 64), nqt = Mqp / 16;
+    p.ca_grp = rows && !h->w8 && nhb * nqt > h->G && nhb * ((nqt + 1) / 2) <= h->G && a->SP <= 384 ? 1 : 0;
+  }
   void* args[] = {&p};
   const void* kern = h->operand_shift ? (rows ? h->kernel_rows_ys : h->kernel_ys) : (rows ? h->kernel_rows : h->kernel);
   if (capturing) h->captured = 1;

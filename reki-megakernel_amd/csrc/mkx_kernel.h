@@ -103,6 +103,8 @@ struct Params {
   // QKV task waits for its own row group's reducers); reducer r = tile r % HT of row group r / HT; 1 in the
   // form with passes
   int nrg;
+  // row-wise attention variants (Shape::RW_ATTN): cross-attention tasks of two query tiles (ca_stage_pairs)
+  int ca_grp;
 };
 
 // placement kinds (Params::pl)
@@ -2192,6 +2194,329 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
   }
 }
 
+// One block of 32 source keys (keys [0, khi) valid) for NQ query tiles at once: the block's K and V^T
+// fragments are read once, each state's chains are those of attn_block (no residual parts, no key factors).
+template <int NQ>
+__device__ __forceinline__ void attn_block_n(AttnState (&A)[NQ], int lane, const char* K, const char* V, int khi, float qs) {
+  bf16x8 kf[4], vf[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kf[i] = ldsfrag(K + i * 1024 + lane * 16);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) vf[dt] = ldsfrag(V + dt * 1024 + lane * 16);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        s[h] = mfma16(kf[h * 2 + db], A[q].qh[db], s[h]);
+        s[h] = mfma16(kf[h * 2 + db], A[q].ql[db], s[h]);
+      }
+    }
+    float pv[8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+      pv[j] = s[j >> 2][j & 3] * qs + ((key >= 0 && key < khi) ? 0.f : -INFINITY);
+      mb = fmaxf(mb, pv[j]);
+    }
+    mb = xor32_max(xor16_max(mb));
+    const float mn = fmaxf(A[q].m, mb);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __expf(A[q].m - mu);
+    A[q].m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pv[j] = __expf(pv[j] - mu);
+      ps += pv[j];
+    }
+    A[q].den = A[q].den * alpha + ps;
+    bf16x8 ph, pl;
+    split8(pv, ph, pl);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 a = A[q].acc[dt] * alpha;
+      a = mfma16(vf[dt], ph, a);
+      a = mfma16(vf[dt], pl, a);
+      A[q].acc[dt] = a;
+    }
+  }
+}
+
+// Two blocks of 32 source keys as one 64-key step (attn_block2) for NQ query tiles at once, each block's
+// fragments read once.
+template <int NQ>
+__device__ __forceinline__ void attn_block2_n(AttnState (&A)[NQ], int lane, const char* K0, const char* V0, int khi0,
+                                              const char* K1, const char* V1, int khi1, float qs) {
+  bf16x8 kf[2][4], vf[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kf[0][i] = ldsfrag(K0 + i * 1024 + lane * 16);
+    kf[1][i] = ldsfrag(K1 + i * 1024 + lane * 16);
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    vf[0][dt] = ldsfrag(V0 + dt * 1024 + lane * 16);
+    vf[1][dt] = ldsfrag(V1 + dt * 1024 + lane * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 s[2][2];
+#pragma unroll
+    for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) s[bk][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+        for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) s[bk][h] = mfma16(kf[bk][h * 2 + db], hl ? A[q].ql[db] : A[q].qh[db], s[bk][h]);
+    float pv[2][8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int bk = 0; bk < 2; ++bk) {
+      const int khi = bk ? khi1 : khi0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+        pv[bk][j] = s[bk][j >> 2][j & 3] * qs + (key < khi ? 0.f : -INFINITY);
+        mb = fmaxf(mb, pv[bk][j]);
+      }
+    }
+    mb = xor32_max(xor16_max(mb));
+    const float mn = fmaxf(A[q].m, mb);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __expf(A[q].m - mu);
+    A[q].m = mn;
+    float ps[2] = {0.f, 0.f};
+#pragma unroll
+    for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pv[bk][j] = __expf(pv[bk][j] - mu);
+        ps[bk] += pv[bk][j];
+      }
+    A[q].den = A[q].den * alpha + (ps[0] + ps[1]);
+    bf16x8 ph[2], pl[2];
+    split8(pv[0], ph[0], pl[0]);
+    split8(pv[1], ph[1], pl[1]);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 a = A[q].acc[dt] * alpha;
+      a = mfma16(vf[0][dt], ph[0], a);
+      a = mfma16(vf[1][dt], ph[1], a);
+      a = mfma16(vf[0][dt], pl[0], a);
+      a = mfma16(vf[1][dt], pl[1], a);
+      A[q].acc[dt] = a;
+    }
+  }
+}
+
+// Cross-attention with tasks of two query tiles (row-wise attention variants, Params::ca_grp: set where the
+// single-tile tasks outnumber the workgroups, the two-tile tasks do not, and every source fits the three LDS
+// ring slots). Task u: sample-head u % nhb, tiles 2 j and 2 j + 1 (j = u / nhb; a last odd tile alone, whose
+// second state runs on a copy of the first and is discarded). The task loads the head's Wq fragments, the
+// sample's source keys and values and both tiles' rows once, projects the two tiles' queries one after the
+// other (the same steps as ca_stage), and runs both through each key block with the block's fragments read
+// once; each tile's result is merged, stored and published as ca_stage does, so the outputs are the same bits.
+template <class S>
+__device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const int* s_ks, BarCtx& bc, int g) {
+  static_assert(!S::W8, "two-tile cross-attention tasks: fp16 weights only");
+  CP& p = c.p;
+  constexpr int KPW = S::KPW;
+  const int Mqp = p.Mqp, NQT = Mqp / 16, NRP = p.NRP, RT = c.RT;
+  const int l = d.l;
+  char* fr = c.frame(d.s, l);
+  const float* y2 = (const float*)(fr + S::y2_off(NRP));
+  const float* ss2 = (const float*)(fr + S::ss2_off(NRP));
+  float* yca = (float*)(fr + S::yca_off(NRP));
+  const char* wq = p.wqca + l * p.s_o;
+  const char* shs = p.shs + ((long long)(d.s * p.L + l) * 3 + 1) * p.B * S::H * 4;
+  // the LDS map of ca_stage; the second tile's queries are staged in the merge area until both states have
+  // read them
+  char* red = c.smem + S::ABUF + 32768;
+  char* Qh0 = c.smem + S::ABUF + 32768 + NWAVES * 4 * 2 * 68 * 16;
+  float* mrg = (float*)(Qh0 + 4096);
+  char* Qh1 = (char*)mrg;
+  float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
+  const int NHB = p.B * S::NH, NP = (NQT + 1) / 2;
+  const uint32_t vlane = (uint32_t)c.lane * 16;
+  const int u = task_first(c, PL_CA);
+  if (u >= NHB * NP) return;
+  const int hh = u % NHB, qa = 2 * (u / NHB), nq = min(2, NQT - qa);
+  const int b = hh / S::NH, hd = hh % S::NH;
+  const int S_len = s_ks[MAX_BATCH + b];
+  // the Wq fragments of the head and the shift fragments, before the wait (as ca_stage)
+  f16x8 wf[4][KPW], sh[KPW];
+  {
+    const __amdgpu_buffer_rsrc_t rsh =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(shs), (short)0, p.B * S::H * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int kb = c.wave + NWAVES * i;
+      const uint32_t o = (uint32_t)((((c.lane & 15) * S::NKB + kb) * 4 + (c.lane >> 4)) * 32);
+      sh[i] = __builtin_bit_cast(f16x8, bload(rsh, o, 0));
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        wf[nt][i] = wfrag_glb<S>(wq + ((long long)(hd * 4 + nt) * S::NKB + kb) * S::CH, c.lane);
+    }
+  }
+  const int r = 4 * c.wave + (c.lane >> 4), cg = c.lane & 15;
+  const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
+  f32x4 cs[2], sn[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int pos = min((qa + (t ? nq - 1 : 0)) * 16 + r, p.Mq - 1);
+    cs[t] = ldf4(p.ca_cos + pos * HD + 4 * cg);
+    sn[t] = ldf4(p.ca_sin + pos * HD + 4 * cg);
+  }
+  f32x4 accb[4][2];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) accb[nt][0] = accb[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < KPW; ++i)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) accb[nt][i & 1] = mfma16h(wf[nt][i], sh[i], accb[nt][i & 1]);
+  MKX_TR(c, 14);
+  // every out-projection task of the row groups holding the two tiles' rows
+  const int rq0 = b * Mqp / 16 + qa, rq1 = rq0 + nq - 1;
+  {
+    const int to = S::HT / p.nt_o;
+    const int rg0 = row_group_of(rq0, RT, p.rgs_o), rg1 = row_group_of(rq1, RT, p.rgs_o);
+    flag_wait<1>(bc, F_O, to, [&](int i) { return rg0 * to + i; }, (unsigned long long)g);
+    if (rg1 != rg0) flag_wait<1>(bc, F_O, to, [&](int i) { return rg1 * to + i; }, (unsigned long long)g);
+  }
+  MKX_TR(c, 0);
+  // both tiles' sums of squares and y2 fragments
+  f16x8 yh[2][KPW];
+  u32x2 ssv[2][S::HT / 8];
+  {
+    const __amdgpu_buffer_rsrc_t rs_ = rsrc(ss2), ry = rsrc(y2);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int rq = t ? rq1 : rq0;
+      const uint32_t so = ss_slot<S::HT>(rq * 16 + (c.lane & 15), c.wave * (S::HT / 4));
+#pragma unroll
+      for (int i = 0; i < S::HT / 8; ++i) ssv[t][i] = bload8(rs_, so, (uint32_t)i * 128);
+#pragma unroll
+      for (int i = 0; i < KPW; ++i) {
+        const int kb = c.wave + NWAVES * i;
+        yh[t][i] = __builtin_bit_cast(f16x8, bload(ry, vlane, (uint32_t)((kb * RT + rq) * 2048)));
+      }
+    }
+  }
+  // the source K/V chunks after the rows (the poll does not wait behind them)
+  wait_vm0();
+  ca_prefetch(c, l, b, hd, S_len);
+  MKX_TR(c, 3);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (t) __syncthreads();  // the first tile's partials in red and ssw have been read
+    {
+      f32x4 acc[4][2];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) acc[nt][0] = acc[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KPW; ++i)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[nt][i & 1] = mfma16h(wf[nt][i], yh[t][i], acc[nt][i & 1]);
+      const float ssp = ss_pairs_sum<S::HT / 8>(ssv[t]);
+      if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int sl = c.lane + (c.lane >> 4);
+        sts16(red + (((c.wave * 4 + nt) * 2 + 0) * 68 + sl) * 16, as_u4(acc[nt][0] + acc[nt][1]));
+        sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 68 + sl) * 16, as_u4(accb[nt][0] + accb[nt][1]));
+      }
+    }
+    __syncthreads();
+    {
+      const int nt = cg >> 2, lr = r + 16 * (cg & 3), lb = b + 16 * (cg & 3);
+      f32x4 qa4[NWAVES], ba[NWAVES];
+      float sw[NWAVES];
+#pragma unroll
+      for (int w = 0; w < NWAVES; ++w) {
+        qa4[w] = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 0) * 68 + lr + (lr >> 4)) * 16));
+        ba[w] = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 68 + lb + (lb >> 4)) * 16));
+        sw[w] = ssw[16 * w + r];
+      }
+      lds_batch(qa4);
+      lds_batch(ba);
+      lds_batch(sw);
+      f32x4 qv = qa4[0];
+      float bv[4] = {ba[0][0], ba[0][1], ba[0][2], ba[0][3]};
+#pragma unroll
+      for (int w = 1; w < NWAVES; ++w) {
+        qv += qa4[w];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] += ba[w][e];
+      }
+      const float rs = rsqrtf((sw[0] + sw[1] + sw[2] + sw[3]) * (1.0f / (float)S::H) + p.eps);
+      f32x4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = qv[e] * rs + bv[e];
+      float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+      ss = row_sum16(ss);
+      const float rn = rsqrtf(ss / 64.f + p.qk_eps);
+      const f32x4 gw = {1.0f + __uint_as_float(wn.x << 16), 1.0f + __uint_as_float(wn.x & 0xffff0000u),
+                        1.0f + __uint_as_float(wn.y << 16), 1.0f + __uint_as_float(wn.y & 0xffff0000u)};
+      const f32x4 xn = x * rn * gw;
+      const float sgn = cg < 8 ? -1.0f : 1.0f;
+      f32x4 uq;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) uq[e] = xn[e] * cs[t][e] + sgn * lane_xor8(xn[e]) * sn[t][e];
+      const int dd = 4 * cg;
+      const int off = (dd >> 5) * 1024 + (r + 16 * ((dd & 31) >> 3)) * 16 + (dd & 4) * 2;
+      u32x2 hi, lo;
+      hi[0] = cvt_pk(uq[0], uq[1]);
+      hi[1] = cvt_pk(uq[2], uq[3]);
+      lo[0] = cvt_pk(uq[0] - __uint_as_float(hi[0] << 16), uq[1] - __uint_as_float(hi[0] & 0xffff0000u));
+      lo[1] = cvt_pk(uq[2] - __uint_as_float(hi[1] << 16), uq[3] - __uint_as_float(hi[1] & 0xffff0000u));
+      char* Qh = t ? Qh1 : Qh0;
+      *reinterpret_cast<u32x2*>(Qh + off) = hi;
+      *reinterpret_cast<u32x2*>(Qh + 2048 + off) = lo;
+    }
+  }
+  wait_vm0();  // this wave's K/V DMAs (the barrier covers the other waves')
+  __syncthreads();
+  MKX_TR(c, 1);
+  AttnState A[2];
+  attn_begin(A[0], Qh0, Qh0 + 2048, c.lane);
+  attn_begin(A[1], Qh1, Qh1 + 2048, c.lane);
+  __syncthreads();  // every wave holds both tiles' queries: the merge area may be overwritten
+  {
+    const int k0 = c.wave * 32, k1 = 128 + c.wave * 32, k2 = 256 + c.wave * 32;
+    char* s0 = ca_slot(c, 0);
+    char* s1 = ca_slot(c, 1);
+    char* s2 = ca_slot(c, 2);
+    if (k1 < S_len)
+      attn_block2_n<2>(A, c.lane, s0 + c.wave * 4096, s0 + 16384 + c.wave * 4096, S_len - k0, s1 + c.wave * 4096,
+                       s1 + 16384 + c.wave * 4096, S_len - k1, p.sm_scale);
+    else if (k0 < S_len)
+      attn_block_n<2>(A, c.lane, s0 + c.wave * 4096, s0 + 16384 + c.wave * 4096, S_len - k0, p.sm_scale);
+    if (k2 < S_len) attn_block_n<2>(A, c.lane, s2 + c.wave * 4096, s2 + 16384 + c.wave * 4096, S_len - k2, p.sm_scale);
+  }
+  MKX_TR(c, 2);
+  attn_merge_store(c, A[0], mrg, yca, b, hd, qa);
+  if (nq == 2) {
+    __syncthreads();  // the first merge's partials have been read
+    attn_merge_store(c, A[1], mrg, yca, b, hd, qa + 1);
+  }
+  MKX_TR(c, 13);
+  flag_publish(bc, F_CA, hh * NQT + qa, (unsigned long long)g + 1);
+  // the second tile's epoch: the same wait and barrier cover its rows
+  if (nq == 2 && c.tid == 0)
+    __hip_atomic_store(&bc.flags[((long long)F_CA * FLAG_MAX + hh * NQT + qa + 1) * FLAG_STRIDE],
+                       bc.base + (unsigned long long)g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ------------------------------------------------------------------------------------------------
 // Step tail (src/mk_expert.py:254-299): o = AdaRMS_final(h_L); v = o Wout^T + bout; x' = x + dt v;
 // h0' = x'_real Win + bin (action rows), register tokens (register rows), all fp32; with h0' its layer-0
@@ -2573,7 +2898,7 @@ __device__ __forceinline__ unsigned task_mask(Ctx<S>& c) {
   if (task_first(c, PL_QKV) < 6 * S::NH * p.rgs_qkv) m |= 1u << ST_QKV;
   if (task_first(c, PL_SA) < nattn) m |= 1u << ST_SA;
   if (task_first(c, PL_O) < (S::HT / p.nt_o) * p.rgs_o) m |= 1u << ST_O;
-  if (task_first(c, PL_CA) < nattn) m |= 1u << ST_CA;
+  if (task_first(c, PL_CA) < (S::RW_ATTN && p.ca_grp ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_CA;
   if (task_first(c, PL_CAO) < (S::HT / p.nt_cao) * p.rgs_cao) m |= 1u << ST_CAO;
   if (task_first(c, PL_GU) < S::IT) m |= 1u << ST_GU;
   if (task_first(c, PL_DOWN) < (S::HT / p.nt_down) * S::SK || task_first(c, PL_RED) < p.nred) m |= 1u << ST_DOWN;
@@ -2649,7 +2974,14 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       c.dt = dt;
       c.ep = (unsigned)g;
       if (cur.st == ST_SA) sa_stage(c, cur, s_ks, bc, g);
-      else if (cur.st == ST_CA) ca_stage(c, cur, s_ks, bc, g);
+      else if (cur.st == ST_CA) {
+        if constexpr (S::RW_ATTN) {
+          if (c.p.ca_grp) ca_stage_pairs(c, cur, s_ks, bc, g);
+          else ca_stage(c, cur, s_ks, bc, g);
+        } else {
+          ca_stage(c, cur, s_ks, bc, g);
+        }
+      }
       else if (cur.st == ST_TAIL) tail_stage(c, cur, bc, g);
       else if constexpr (S::RW) gemm_stage_rows(c, cur, bc, g);
       else gemm_stage(c, cur, bc, g);
