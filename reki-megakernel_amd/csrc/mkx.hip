@@ -699,7 +699,7 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
     // cross-attention tasks of two query tiles (row-wise attention variants): where the one-tile tasks
     // outnumber the workgroups, the two-tile tasks do not, and every source fits the three LDS ring slots
     const int nhb = a->B * (H / 64), nqt = Mqp / 16;
-    p.ca_grp = rows && !h->w8 && nhb * nqt > h->G && nhb * ((nqt + 1) / 2) <= h->G && a->SP <= 384 ? 1 : 0;
+    p.ca_grp = rows && nhb * nqt > h->G && nhb * ((nqt + 1) / 2) <= h->G && a->SP <= 384 ? 1 : 0;
   }
   void* args[] = {&p};
   const void* kern = h->operand_shift ? (rows ? h->kernel_rows_ys : h->kernel_ys) : (rows ? h->kernel_rows : h->kernel);

@@ -103,7 +103,7 @@ struct Params {
   // QKV task waits for its own row group's reducers); reducer r = tile r % HT of row group r / HT; 1 in the
   // form with passes
   int nrg;
-  // row-wise attention variants (Shape::RW_ATTN): cross-attention tasks of two query tiles (ca_stage_pairs)
+  // row-wise form: cross-attention tasks of two query tiles (ca_stage_pairs)
   int ca_grp;
 };
 
@@ -2319,7 +2319,7 @@ __device__ __forceinline__ void attn_block2_n(AttnState (&A)[NQ], int lane, cons
   }
 }
 
-// Cross-attention with tasks of two query tiles (row-wise attention variants, Params::ca_grp: set where the
+// Cross-attention with tasks of two query tiles (row-wise form, Params::ca_grp: set where the
 // single-tile tasks outnumber the workgroups, the two-tile tasks do not, and every source fits the three LDS
 // ring slots). Task u: sample-head u % nhb, tiles 2 j and 2 j + 1 (j = u / nhb; a last odd tile alone, whose
 // second state runs on a copy of the first and is discarded). The task loads the head's Wq fragments, the
@@ -2328,7 +2328,6 @@ __device__ __forceinline__ void attn_block2_n(AttnState (&A)[NQ], int lane, cons
 // once; each tile's result is merged, stored and published as ca_stage does, so the outputs are the same bits.
 template <class S>
 __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const int* s_ks, BarCtx& bc, int g) {
-  static_assert(!S::W8, "two-tile cross-attention tasks: fp16 weights only");
   CP& p = c.p;
   constexpr int KPW = S::KPW;
   const int Mqp = p.Mqp, NQT = Mqp / 16, NRP = p.NRP, RT = c.RT;
@@ -2370,6 +2369,7 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
   }
   const int r = 4 * c.wave + (c.lane >> 4), cg = c.lane & 15;
   const uint2 wn = *reinterpret_cast<const uint2*>(p.qcan + l * HD + 4 * cg);
+  const f32x4 scq = S::W8 ? ldf4(p.sc_qca + (long long)l * S::H + hd * HD + 4 * cg) : f32x4{1.f, 1.f, 1.f, 1.f};
   f32x4 cs[2], sn[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -2412,9 +2412,10 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
       }
     }
   }
-  // the source K/V chunks after the rows (the poll does not wait behind them)
+  // the source K/V chunks after the rows (the poll does not wait behind them); the fp8 kernel DMAs them
+  // during the barrier before the stage
   wait_vm0();
-  ca_prefetch(c, l, b, hd, S_len);
+  if constexpr (S::RW_ATTN) ca_prefetch(c, l, b, hd, S_len);
   MKX_TR(c, 3);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -2461,7 +2462,7 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
       const float rs = rsqrtf((sw[0] + sw[1] + sw[2] + sw[3]) * (1.0f / (float)S::H) + p.eps);
       f32x4 x;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = qv[e] * rs + bv[e];
+      for (int e = 0; e < 4; ++e) x[e] = (qv[e] * rs + bv[e]) * scq[e];
       float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
       ss = row_sum16(ss);
       const float rn = rsqrtf(ss / 64.f + p.qk_eps);
@@ -2808,7 +2809,19 @@ template <class S>
 __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
   MKX_TRW(c, 8);
-  if (d.st == ST_SA || d.st == ST_CA) {
+  bool ca_pairs = false;
+  if constexpr (S::RW) ca_pairs = d.st == ST_CA && p.ca_grp;
+  if (ca_pairs) {
+    // two-tile cross-attention tasks: task u runs sample-head u % (B NH); the fp8 kernel DMAs its source K/V
+    // here, the fp16 one after the poll
+    if constexpr (!S::RW_ATTN) {
+      const int nhb = p.B * S::NH, u = task_first(c, d.pk);
+      if (u < nhb * ((p.Mqp / 16 + 1) / 2)) {
+        const int hh = u % nhb;
+        ca_prefetch(c, d.l, hh / S::NH, hh % S::NH, s_ks[MAX_BATCH + hh / S::NH]);
+      }
+    }
+  } else if (d.st == ST_SA || d.st == ST_CA) {
     const int nqt = p.Mqp / 16;
     const AttnTask at = attn_task<S::RW_ATTN>(task_first(c, d.pk), nqt, p.B * S::NH, c.G);
     if (at.ok) {
@@ -2898,7 +2911,7 @@ __device__ __forceinline__ unsigned task_mask(Ctx<S>& c) {
   if (task_first(c, PL_QKV) < 6 * S::NH * p.rgs_qkv) m |= 1u << ST_QKV;
   if (task_first(c, PL_SA) < nattn) m |= 1u << ST_SA;
   if (task_first(c, PL_O) < (S::HT / p.nt_o) * p.rgs_o) m |= 1u << ST_O;
-  if (task_first(c, PL_CA) < (S::RW_ATTN && p.ca_grp ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_CA;
+  if (task_first(c, PL_CA) < (S::RW && p.ca_grp ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_CA;
   if (task_first(c, PL_CAO) < (S::HT / p.nt_cao) * p.rgs_cao) m |= 1u << ST_CAO;
   if (task_first(c, PL_GU) < S::IT) m |= 1u << ST_GU;
   if (task_first(c, PL_DOWN) < (S::HT / p.nt_down) * S::SK || task_first(c, PL_RED) < p.nred) m |= 1u << ST_DOWN;
@@ -2975,7 +2988,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       c.ep = (unsigned)g;
       if (cur.st == ST_SA) sa_stage(c, cur, s_ks, bc, g);
       else if (cur.st == ST_CA) {
-        if constexpr (S::RW_ATTN) {
+        if constexpr (S::RW) {
           if (c.p.ca_grp) ca_stage_pairs(c, cur, s_ks, bc, g);
           else ca_stage(c, cur, s_ks, bc, g);
         } else {
