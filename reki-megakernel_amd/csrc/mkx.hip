@@ -106,7 +106,9 @@ namespace mkx {
   extern template __global__ void mkx_megakernel<H, I, false, false, true>(Params); \
   extern template __global__ void mkx_megakernel<H, I, true, false, true>(Params);  \
   extern template __global__ void mkx_megakernel<H, I, false, true, true>(Params);  \
-  extern template __global__ void mkx_megakernel<H, I, true, true, true>(Params);
+  extern template __global__ void mkx_megakernel<H, I, true, true, true>(Params);        \
+  extern template __global__ void mkx_megakernel<H, I, true, true, false, true>(Params);  \
+  extern template __global__ void mkx_megakernel<H, I, true, true, true, true>(Params);
 MKX_EXTERN(768, 3072)
 MKX_EXTERN(1024, 4096)
 MKX_EXTERN(256, 512)
@@ -121,17 +123,22 @@ const void* kernel_of(bool w8) {
             : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false, ROWWISE, YS>);
 }
 template <int H, int I>
-const void* kernel_of(bool w8, bool rowwise, bool ys) {
+const void* kernel_of(bool w8, bool rowwise, bool ys, bool pairs) {
+  // (two-tile self-attention: fp8-weight row-wise instantiations only)
+  if (pairs) return !w8 ? nullptr
+                        : ys ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, true, true, true>)
+                             : reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, true, false, true>);
   return rowwise ? (ys ? kernel_of<H, I, true, true>(w8) : kernel_of<H, I, true, false>(w8))
                  : (ys ? kernel_of<H, I, false, true>(w8) : kernel_of<H, I, false, false>(w8));
 }
 
 // rowwise: the form whose GEMM stages compute whole-K products per wave (launches with many row tiles); ys: the
-// twin with scaled AdaRMS operands (an operand shift)
-const void* pick_kernel(int H, int I, bool w8, bool rowwise, bool ys = false) {
-  if (H == 768 && I == 3072) return kernel_of<768, 3072>(w8, rowwise, ys);
-  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>(w8, rowwise, ys);
-  if (H == 256 && I == 512) return kernel_of<256, 512>(w8, rowwise, ys);
+// twin with scaled AdaRMS operands (an operand shift); pairs: the row-wise form with two-tile self-attention
+// tasks (fp8 weights)
+const void* pick_kernel(int H, int I, bool w8, bool rowwise, bool ys = false, bool pairs = false) {
+  if (H == 768 && I == 3072) return kernel_of<768, 3072>(w8, rowwise, ys, pairs);
+  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>(w8, rowwise, ys, pairs);
+  if (H == 256 && I == 512) return kernel_of<256, 512>(w8, rowwise, ys, pairs);
   return nullptr;
 }
 
@@ -304,6 +311,8 @@ struct mkx_handle {
   const void* kernel_rows = nullptr;  // the instantiation with row-wise GEMM stages
   const void* kernel_ys = nullptr;    // the twins of both with scaled AdaRMS operands (an operand shift)
   const void* kernel_rows_ys = nullptr;
+  const void* kernel_pairs = nullptr;  // the row-wise instantiations with two-tile self-attention tasks (fp8)
+  const void* kernel_pairs_ys = nullptr;
   int gemm_form = -1;    // MKX_GEMM_FORM at creation: 0 passes, 1 row-wise, -1 chosen per launch
   int last_form = -1;    // form of the last launch (0 passes, 1 row-wise; -1 before the first)
   unsigned spin_limit = SPIN_LIMIT;
@@ -388,6 +397,8 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   h->kernel_rows = pick_kernel(d.H, d.I, w8, true);
   h->kernel_ys = pick_kernel(d.H, d.I, w8, false, true);
   h->kernel_rows_ys = pick_kernel(d.H, d.I, w8, true, true);
+  h->kernel_pairs = pick_kernel(d.H, d.I, w8, true, false, true);
+  h->kernel_pairs_ys = pick_kernel(d.H, d.I, w8, true, true, true);
   auto bail = [&](int code) { free_handle(h); return code; };
 #define HCHK(x)                                                                                       \
   do {                                                                                                \
@@ -408,6 +419,11 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   for (const void* k : {h->kernel_ys, h->kernel_rows_ys}) {
     HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NTHREADS, 0));
     if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel (scaled AdaRMS operands) does not fit one workgroup per CU"));
+  }
+  for (const void* k : {h->kernel_pairs, h->kernel_pairs_ys}) {
+    if (!k) continue;
+    HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NTHREADS, 0));
+    if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel (two-tile attention tasks) does not fit one workgroup per CU"));
   }
   h->G = prop.multiProcessorCount;
   {
@@ -695,14 +711,20 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
   p.nt_o = lay.nt_o; p.nt_cao = lay.nt_cao; p.nt_down = lay.nt_down;
   p.lds_red = lay.lds_red; p.lds_mods = lay.lds_mods;
   p.tpr = lay.tpr; p.nred = lay.nred; p.nrg = lay.nrg;
+  bool pairs;
   {
-    // cross-attention tasks of two query tiles (row-wise attention variants): where the one-tile tasks
-    // outnumber the workgroups, the two-tile tasks do not, and every source fits the three LDS ring slots
+    // attention tasks of two query tiles (row-wise form): where the one-tile tasks outnumber the workgroups and
+    // the two-tile tasks do not (cross-attention: and every source fits the three LDS ring slots)
     const int nhb = a->B * (H / 64), nqt = Mqp / 16;
-    p.ca_grp = rows && nhb * nqt > h->G && nhb * ((nqt + 1) / 2) <= h->G && a->SP <= 384 ? 1 : 0;
+    pairs = rows && nhb * nqt > h->G && nhb * ((nqt + 1) / 2) <= h->G;
+    p.ca_grp = pairs && a->SP <= 384 ? 1 : 0;
+    // self-attention: the fp8 kernels; the fp16 ones run a second query tile of a sample-head with its keys and
+    // values still in LDS (two-tile tasks measured slower there: workload B 5.84 -> 5.90 ms)
+    pairs = pairs && h->w8;
   }
   void* args[] = {&p};
-  const void* kern = h->operand_shift ? (rows ? h->kernel_rows_ys : h->kernel_ys) : (rows ? h->kernel_rows : h->kernel);
+  const void* kern = h->operand_shift ? (pairs ? h->kernel_pairs_ys : rows ? h->kernel_rows_ys : h->kernel_ys)
+                                      : (pairs ? h->kernel_pairs : rows ? h->kernel_rows : h->kernel);
   if (capturing) h->captured = 1;
   if (capturing || h->plain_launch) {
     // co-residency was established at creation (one workgroup per CU fits); capture a plain launch

@@ -103,7 +103,8 @@ struct Params {
   // QKV task waits for its own row group's reducers); reducer r = tile r % HT of row group r / HT; 1 in the
   // form with passes
   int nrg;
-  // row-wise form: cross-attention tasks of two query tiles (ca_stage_pairs)
+  // row-wise form: cross-attention tasks of two query tiles (ca_stage_pairs; the self-attention ones are the
+  // Shape::PAIRS instantiations')
   int ca_grp;
 };
 
@@ -116,7 +117,7 @@ typedef const __attribute__((address_space(4))) Params CP;
 
 __host__ __device__ constexpr int ceil_to(int a, int m) { return (a + m - 1) / m * m; }
 
-template <int H_, int I_, bool W8_ = false, bool RW_ = false, bool YS_ = false>
+template <int H_, int I_, bool W8_ = false, bool RW_ = false, bool YS_ = false, bool PR_ = false>
 struct Shape {
   // YS: AdaRMS operands scaled by Params::yinv (the launches with an operand shift)
   static constexpr bool YS = YS_;
@@ -129,6 +130,12 @@ struct Shape {
   // measured slower with them, also for launches that never run the pairs (workload D 7.65 -> 7.86 ms and
   // D-b4 12.79 -> 13.00 ms with the pairs; 7.65 -> 7.69 and 12.77 -> 12.86 ms with the late K/V DMA).
   static constexpr bool RW_ATTN = RW_ && !W8_;
+  // PAIRS: the fp8-weight row-wise instantiations for launches whose attention tasks run two query tiles each
+  // (chosen by the host where the one-tile tasks outnumber the workgroups and the two-tile tasks do not):
+  // self-attention by sa_stage_pairs only. Separate instantiations, so that the others keep their code (and
+  // register allocation) unchanged: compiled into them, the two-tile path made the kernels slower for every
+  // launch (workload D 7.59 -> 7.90 ms without taking it).
+  static constexpr bool PAIRS = RW_ && PR_;
   // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): fp16 (packed
   // from bf16), or fp8 e4m3 decoded to fp16 fragments when read (weight-only quantisation)
   static constexpr bool W8 = W8_;
@@ -2247,6 +2254,75 @@ __device__ __forceinline__ void attn_block_n(AttnState (&A)[NQ], int lane, const
   }
 }
 
+// One block of 32 keys for NQ query tiles at once (the arguments of attn_block, with one score scale per
+// tile): the block's K and V^T fragments (and residual parts, key factors) are read once, each state's
+// chains and softmax arithmetic are those of attn_block.
+template <int NQ>
+__device__ __forceinline__ void attn_block_nq(AttnState (&A)[NQ], int lane, const char* K, const char* Kl, const char* V,
+                                              const char* Vl, int klo, int khi, const float (&qs)[NQ], const float* rk) {
+  bf16x8 kf[4], kl[4], vf[4], vl[4];
+  f32x4 rkv[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kf[i] = ldsfrag(K + i * 1024 + lane * 16);
+    if (Kl) kl[i] = ldsfrag(Kl + i * 1024 + lane * 16);
+  }
+  if (rk) {
+    rkv[0] = *reinterpret_cast<const f32x4*>(rk + 4 * (lane >> 4));
+    rkv[1] = *reinterpret_cast<const f32x4*>(rk + 16 + 4 * (lane >> 4));
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    vf[dt] = ldsfrag(V + dt * 1024 + lane * 16);
+    if (Vl) vl[dt] = ldsfrag(Vl + dt * 1024 + lane * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        s[h] = mfma16(kf[h * 2 + db], A[q].qh[db], s[h]);
+        s[h] = mfma16(kf[h * 2 + db], A[q].ql[db], s[h]);
+        if (Kl) s[h] = mfma16(kl[h * 2 + db], A[q].qh[db], s[h]);
+      }
+    }
+    float pv[8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+      const float sc = qs[q] * rkv[j >> 2][j & 3];
+      pv[j] = s[j >> 2][j & 3] * sc + ((key >= klo && key < khi) ? 0.f : -INFINITY);
+      mb = fmaxf(mb, pv[j]);
+    }
+    mb = xor32_max(xor16_max(mb));
+    const float mn = fmaxf(A[q].m, mb);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __expf(A[q].m - mu);
+    A[q].m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pv[j] = __expf(pv[j] - mu);
+      ps += pv[j];
+    }
+    A[q].den = A[q].den * alpha + ps;
+    bf16x8 ph, pl;
+    split8(pv, ph, pl);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 a = A[q].acc[dt] * alpha;
+      a = mfma16(vf[dt], ph, a);
+      a = mfma16(vf[dt], pl, a);
+      if (Vl) a = mfma16(vl[dt], ph, a);
+      A[q].acc[dt] = a;
+    }
+  }
+}
+
 // Two blocks of 32 source keys as one 64-key step (attn_block2) for NQ query tiles at once, each block's
 // fragments read once.
 template <int NQ>
@@ -2317,6 +2393,155 @@ __device__ __forceinline__ void attn_block2_n(AttnState (&A)[NQ], int lane, cons
       A[q].acc[dt] = a;
     }
   }
+}
+
+// register rows' k (normed, rotated) and v of step 1, bf16 [L][B][R][NH][64] (src/mk_expert.py:440-470), from
+// the own keys and values staged in LDS (hi + lo parts) and the key RMS factors (sa_stage's own copy of these
+// steps is kept inline there: as a call it changes that function's register allocation)
+template <class S>
+__device__ __forceinline__ void sa_register_kv(Ctx<S>& c, const char* Kh, const char* Kl, const char* Vh, const char* Vl,
+                                               const float* rk, int l, int b, int hd) {
+  CP& p = c.p;
+  for (int it = c.tid; it < p.R * 8; it += NTHREADS) {
+    const int i = p.T + it / 8, dd = (it % 8) * 8;
+    bf16x8 kh = ldsfrag(Kh + kchunk_off(i, dd)), kl = ldsfrag(Kl + kchunk_off(i, dd));
+    const u32x4 khu = __builtin_bit_cast(u32x4, kh), klu = __builtin_bit_cast(u32x4, kl);
+    float kf[8], kr[8], vf[8];
+    unpack8(khu, kf);
+    unpack8(klu, kr);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kf[e] = (kf[e] + kr[e]) * rk[i];
+      vf[e] = bf2f(*reinterpret_cast<const bf16_t*>(Vh + vt_off(i, dd + e))) +
+              bf2f(*reinterpret_cast<const bf16_t*>(Vl + vt_off(i, dd + e)));
+    }
+    const long long o = ((((long long)l * p.B + b) * p.R + (i - p.T)) * S::NH + hd) * HD + dd;
+    u32x4 wk, wv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      wk[e] = cvt_pk(kf[2 * e], kf[2 * e + 1]);
+      wv[e] = cvt_pk(vf[2 * e], vf[2 * e + 1]);
+    }
+    *reinterpret_cast<u32x4*>(p.cur_k + o) = wk;
+    *reinterpret_cast<u32x4*>(p.cur_v + o) = wv;
+  }
+}
+
+// Self-attention with tasks of two query tiles (the Shape::PAIRS instantiations, for launches whose one-tile
+// tasks outnumber the workgroups and whose two-tile tasks do not). Task u: sample-head u % nhb, tiles 2 j and 2 j + 1
+// (j = u / nhb; a last odd tile alone, its second state a discarded copy of the first). The head's memory
+// rows, own keys and values are staged once and both tiles' states run through each key block with the
+// block's fragments read once; the second tile's query rows and sums of squares are staged in the merge
+// area until both states have read them. Each state's arithmetic is that of sa_stage.
+template <class S>
+__device__ __forceinline__ void sa_stage_pairs(Ctx<S>& c, const Desc& d, const int* s_ks, BarCtx& bc, int g) {
+  CP& p = c.p;
+  const int M = p.Mq, Mqp = p.Mqp, PM = p.PM, PMP = ceil_to(PM, 32), NOWN32 = ceil_to(M, 32);
+  const int NQT = Mqp / 16, NKT = NOWN32 / 16, KBO = NOWN32 / 32, NRP = p.NRP, RT = c.RT;
+  const int l = d.l;
+  char* fr = c.frame(d.s, l);
+  const char* qs = fr + S::qs_off(NRP);
+  const char* ks = fr + S::ks_off(NRP);
+  const char* vt = fr + S::vtb_off(NRP);
+  const float* ssqk = (const float*)(fr + S::ssqk_off(NRP));
+  float* ysa = (float*)(fr + S::ysa_off(NRP));
+  char* memK = c.smem + S::WBUF;
+  char* memVt = memK + PMP * 128;
+  char* Qh = c.smem + S::ABUF;
+  char* Ql = Qh + 2048;
+  char* Kh = Ql + 2048;
+  char* Kl = Kh + NOWN32 * 128;
+  char* Vh = Kl + NOWN32 * 128;
+  char* Vl = Vh + NOWN32 * 128;
+  float* rk = (float*)(Vl + NOWN32 * 128);
+  float* mrg = rk + 128;
+  float* sq_l = mrg;                 // [tile][column half][16 rows]
+  char* Qh1 = (char*)(mrg + 64);     // the second tile's Q chunks (hi, lo)
+  char* Ql1 = Qh1 + 2048;
+  const int NHB = p.B * S::NH, NP = (NQT + 1) / 2;
+  const bool want_kv = (d.s == 0 && p.cur_k != nullptr && p.R > 0);
+  const int u = task_first(c, PL_SA);
+  if (u >= NHB * NP) return;
+  const int hh = u % NHB, qa = 2 * (u / NHB), nq = min(2, NQT - qa);
+  const int b = hh / S::NH, hd = hh % S::NH;
+  const int kvs = s_ks[b];
+  {
+    const int rgq = p.rgs_qkv;
+    flag_wait<1>(bc, F_QKV, 6 * rgq, [&](int i) {
+      const int k = i % 6, rg = i / 6;
+      return rg * 6 * S::NH + (k >> 1) * 2 * S::NH + 2 * hd + (k & 1);
+    }, (unsigned long long)g);
+  }
+  MKX_TR(c, 0);
+  const int rt0 = b * Mqp / 16;
+  if (c.wave == 0) {
+    // lane: row lane % 16, column half (lane / 16) % 2, tile lane / 32
+    const int qt = qa + ((c.lane >> 5) ? nq - 1 : 0);
+    const int qq = qt * 16 + (c.lane & 15), j = (c.lane >> 4) & 1;
+    __builtin_amdgcn_global_load_lds(ssqk + (long long)(hd * 2 + j) * NRP + b * Mqp + qq, (lds_void*)sq_l, 4, 0, 0);
+  }
+  // each wave's first DMAs are its pieces of the two Q tiles, then K tiles of all own keys and V^T blocks
+  for (int k = c.wave; k < 8 + 4 * NKT + 8 * KBO; k += NWAVES) {
+    if (k < 8) {
+      const int t = k >> 2, db = (k >> 1) & 1, part = k & 1;
+      const int qt = qa + (t ? nq - 1 : 0);
+      char* dst = t ? (part ? Ql1 : Qh1) : (part ? Ql : Qh);
+      dma16(qs + ((long long)((2 * hd + db) * RT + rt0 + qt) * 2 + part) * 1024 + c.lane * 16, dst + db * 1024);
+    } else if (k < 8 + 4 * NKT) {
+      const int kk = k - 8, kt = kk >> 2, db = (kk >> 1) & 1, part = kk & 1;
+      const int rtk = rt0 + min(kt, NQT - 1);
+      dma16(ks + ((long long)((2 * hd + db) * RT + rtk) * 2 + part) * 1024 + c.lane * 16, (part ? Kl : Kh) + (kt * 2 + db) * 1024);
+    } else {
+      const int vv = k - 8 - 4 * NKT;
+      dma16(vt + ((long long)hh * KBO * 8 + vv) * 1024 + c.lane * 16, ((vv & 1) ? Vl : Vh) + (vv >> 1) * 1024);
+    }
+  }
+  const int rowk = b * Mqp + min(c.tid, Mqp - 1);
+  const float ssk0 = ssqk[(long long)((S::NH + hd) * 2) * NRP + rowk];
+  const float ssk1 = ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + rowk];
+  // every wave issued at least 4 own-key DMAs after its Q pieces (4 NKT + 8 KBO >= 16 over 4 waves)
+  wait_vm_le<4>();
+  exec_barrier();
+  MKX_TR(c, 1);
+  AttnState A[2];
+  attn_begin(A[0], Qh, Ql, c.lane);
+  attn_begin(A[1], Qh1, Ql1, c.lane);
+  float qsc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float ssq = sq_l[32 * t + (c.lane & 15)] + sq_l[32 * t + 16 + (c.lane & 15)];
+    qsc[t] = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
+  }
+  const int mb0 = kvs >> 5, nmb = PMP / 32 - mb0;
+  for (int beta = c.wave; beta < nmb; beta += NWAVES) {
+    const int kb = mb0 + beta;
+    attn_block_nq<2>(A, c.lane, memK + kb * 4096, nullptr, memVt + kb * 4096, nullptr, kvs - kb * 32, PM - kb * 32, qsc, nullptr);
+  }
+  wait_vm0();  // the own keys' K and V^T have landed
+  __syncthreads();
+  if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
+  for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
+    const int key = Mqp + it / HD, dd = it % HD;
+    *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
+    *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
+  }
+  __syncthreads();  // (also: every wave has read both tiles' queries before the merge area is reused)
+  for (int beta = nmb + ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES; beta < nmb + KBO; beta += NWAVES) {
+    const int kb = beta - nmb;
+    attn_block_nq<2>(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
+  }
+  MKX_TR(c, 2);
+  attn_merge_store(c, A[0], mrg, ysa, b, hd, qa);
+  if (nq == 2) {
+    __syncthreads();  // the first merge's partials have been read
+    attn_merge_store(c, A[1], mrg, ysa, b, hd, qa + 1);
+  }
+  if (want_kv && qa == 0) sa_register_kv(c, Kh, Kl, Vh, Vl, rk, l, b, hd);
+  flag_publish(bc, F_SA, hh * NQT + qa, (unsigned long long)g + 1);
+  // the second tile's epoch: the same wait and barrier cover its rows
+  if (nq == 2 && c.tid == 0)
+    __hip_atomic_store(&bc.flags[((long long)F_SA * FLAG_MAX + hh * NQT + qa + 1) * FLAG_STRIDE],
+                       bc.base + (unsigned long long)g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Cross-attention with tasks of two query tiles (row-wise form, Params::ca_grp: set where the
@@ -2809,9 +3034,17 @@ template <class S>
 __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const int* s_ks) {
   CP& p = c.p;
   MKX_TRW(c, 8);
-  bool ca_pairs = false;
+  bool ca_pairs = false, sa_pairs = false;
   if constexpr (S::RW) ca_pairs = d.st == ST_CA && p.ca_grp;
-  if (ca_pairs) {
+  if constexpr (S::PAIRS) sa_pairs = d.st == ST_SA;
+  if (sa_pairs) {
+    // two-tile self-attention tasks: task u runs sample-head u % (B NH)
+    const int nhb = p.B * S::NH, u = task_first(c, d.pk);
+    if (u < nhb * ((p.Mqp / 16 + 1) / 2)) {
+      const int hh = u % nhb;
+      sa_prefetch(c, d.l, hh / S::NH, hh % S::NH, s_ks[hh / S::NH]);
+    }
+  } else if (ca_pairs) {
     // two-tile cross-attention tasks: task u runs sample-head u % (B NH); the fp8 kernel DMAs its source K/V
     // here, the fp16 one after the poll
     if constexpr (!S::RW_ATTN) {
@@ -2909,7 +3142,7 @@ __device__ __forceinline__ unsigned task_mask(Ctx<S>& c) {
   const int nattn = attn_count(p.Mqp / 16, p.B * S::NH), nout = tail_nout<S>(p);
   unsigned m = 0;
   if (task_first(c, PL_QKV) < 6 * S::NH * p.rgs_qkv) m |= 1u << ST_QKV;
-  if (task_first(c, PL_SA) < nattn) m |= 1u << ST_SA;
+  if (task_first(c, PL_SA) < (S::PAIRS ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_SA;
   if (task_first(c, PL_O) < (S::HT / p.nt_o) * p.rgs_o) m |= 1u << ST_O;
   if (task_first(c, PL_CA) < (S::RW && p.ca_grp ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_CA;
   if (task_first(c, PL_CAO) < (S::HT / p.nt_cao) * p.rgs_cao) m |= 1u << ST_CAO;
@@ -2933,9 +3166,9 @@ __device__ __forceinline__ StagePos next_stage(unsigned mask, StagePos q, int to
 }
 
 // ------------------------------------------------------------------------------------------------
-template <int H, int I, bool W8, bool ROWWISE, bool YSHIFT = false>
+template <int H, int I, bool W8, bool ROWWISE, bool YSHIFT = false, bool PAIRS = false>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
-  using S = Shape<H, I, W8, ROWWISE, YSHIFT>;
+  using S = Shape<H, I, W8, ROWWISE, YSHIFT, PAIRS>;
   __shared__ __attribute__((aligned(1024))) char smem[S::LDS];
   CP& p = *(CP*)(__builtin_amdgcn_kernarg_segment_ptr());
   Ctx<S> c(p, smem);
@@ -2986,7 +3219,10 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
       Ctx<S> c(*pl, smem);
       c.dt = dt;
       c.ep = (unsigned)g;
-      if (cur.st == ST_SA) sa_stage(c, cur, s_ks, bc, g);
+      if (cur.st == ST_SA) {
+        if constexpr (S::PAIRS) sa_stage_pairs(c, cur, s_ks, bc, g);
+        else sa_stage(c, cur, s_ks, bc, g);
+      }
       else if (cur.st == ST_CA) {
         if constexpr (S::RW) {
           if (c.p.ca_grp) ca_stage_pairs(c, cur, s_ks, bc, g);

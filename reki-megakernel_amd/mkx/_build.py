@@ -29,6 +29,9 @@ UNITS = (
     ("mkx_mk768r.hip", ()),
     ("mkx_mk1024r.hip", ()),
     ("mkx_mk256r.hip", ()),
+    ("mkx_mk768p.hip", ()),
+    ("mkx_mk1024p.hip", ()),
+    ("mkx_mk256p.hip", ()),
 )
 COMMON = ("--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
           # packed fp32 instructions stay off: every HIP source is compiled without them

@@ -358,12 +358,13 @@ def test_operand_shift_runs_a_residual_stream_beyond_the_fp16_range():
     mk.close()
 
 
-@pytest.mark.parametrize("name", ["B", "tiny fp8 b3"])
+@pytest.mark.parametrize("name", ["B", "tiny fp8 b3", "D-b4"])
 def test_operand_shift_in_the_row_wise_form(name):
-    """The operand shift in the row-wise kernels (fp16-packed and fp8 weights): their shift twins track the fp32
-    oracle at shift 8 and, with register tokens scaled past the fp16 range (MKX_ERANGE at shift 0), after
-    run_checked has raised the shift; shift 0 again gives the default result bit for bit."""
-    cfg = SY.WORKLOADS["B"] if name == "B" else replace(TINY, B=3, weight_dtype="fp8_e4m3")
+    """The operand shift in the row-wise kernels (fp16-packed and fp8 weights; D-b4: the fp8 instantiations with
+    two-tile attention tasks, 384 one-tile tasks on 256 workgroups): their shift twins track the fp32 oracle at
+    shift 8 and, with register tokens scaled past the fp16 range (MKX_ERANGE at shift 0), after run_checked has
+    raised the shift; shift 0 again gives the default result bit for bit."""
+    cfg = SY.WORKLOADS[name] if name in SY.WORKLOADS else replace(TINY, B=3, weight_dtype="fp8_e4m3")
     import os
     old = os.environ.get("MKX_GEMM_FORM")
     os.environ["MKX_GEMM_FORM"] = "rows"
