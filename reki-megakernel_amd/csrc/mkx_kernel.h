@@ -2637,10 +2637,10 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
       }
     }
   }
-  // the source K/V chunks after the rows (the poll does not wait behind them); the fp8 kernel DMAs them
-  // during the barrier before the stage
+  // the source K/V chunks after the rows (the poll does not wait behind them); the fp8 kernels without
+  // two-tile self-attention DMA them during the barrier before the stage
   wait_vm0();
-  if constexpr (S::RW_ATTN) ca_prefetch(c, l, b, hd, S_len);
+  if constexpr (S::RW_ATTN || S::PAIRS) ca_prefetch(c, l, b, hd, S_len);
   MKX_TR(c, 3);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -3045,9 +3045,9 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
       sa_prefetch(c, d.l, hh / S::NH, hh % S::NH, s_ks[hh / S::NH]);
     }
   } else if (ca_pairs) {
-    // two-tile cross-attention tasks: task u runs sample-head u % (B NH); the fp8 kernel DMAs its source K/V
-    // here, the fp16 one after the poll
-    if constexpr (!S::RW_ATTN) {
+    // two-tile cross-attention tasks: task u runs sample-head u % (B NH); the fp8 kernels without two-tile
+    // self-attention DMA its source K/V here, the others after the poll
+    if constexpr (!S::RW_ATTN && !S::PAIRS) {
       const int nhb = p.B * S::NH, u = task_first(c, d.pk);
       if (u < nhb * ((p.Mqp / 16 + 1) / 2)) {
         const int hh = u % nhb;
