@@ -194,6 +194,23 @@ def test_batch_of_eight_long_source_rowwise():
     _check_loop("b8 S 520 (row-wise, tile pairs, streamed source)", make_case(replace(SY.WORKLOADS["B"], L=2, S=520, SP=520)))
 
 
+def test_two_tile_attention_tasks_with_a_lone_last_tile():
+    # fp8 weights, batch 4 of 40 action + 32 register rows: 5 query tiles per sample, 320 one-tile attention
+    # tasks on 256 workgroups, so both attention stages run in tasks of two query tiles (the fp8 two-tile
+    # instantiations), the fifth tile of each sample-head alone
+    from dataclasses import replace
+    _check_loop("fp8 b4 T40 (two-tile attention tasks, lone last tile)",
+                make_case(replace(SY.WORKLOADS["D-b4"], L=2, T_act=40)))
+
+
+def test_two_tile_self_attention_with_a_streamed_source():
+    # the same shape with 520 source rows: two-tile self-attention tasks, one-tile cross-attention tasks that
+    # stream their K/V through the LDS ring (sources beyond the three ring slots)
+    from dataclasses import replace
+    _check_loop("fp8 b4 T40 S520 (two-tile self-attention, streamed source)",
+                make_case(replace(SY.WORKLOADS["D-b4"], L=2, T_act=40, S=520, SP=520)))
+
+
 def test_config_A_rowwise_form():
     # the headline shape forced into the row-wise form (one-tile tasks, row-wise GEMMs and step tail)
     with _gemm_form("rows"):
