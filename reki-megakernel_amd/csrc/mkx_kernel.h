@@ -130,6 +130,10 @@ struct Shape {
   // measured slower with them, also for launches that never run the pairs (workload D 7.65 -> 7.86 ms and
   // D-b4 12.79 -> 13.00 ms with the pairs; 7.65 -> 7.69 and 12.77 -> 12.86 ms with the late K/V DMA).
   static constexpr bool RW_ATTN = RW_ && !W8_;
+  // CA_LATE: cross-attention DMAs its source K/V after its ready-epoch poll and query rows: the fp16 row-wise
+  // instantiations and the two-tile ones (not the other fp8 row-wise ones, whose launches, workload D, measured
+  // 7.59 -> 7.74 ms with it)
+  static constexpr bool CA_LATE = RW_ && (!W8_ || PR_);
   // PAIRS: the fp8-weight row-wise instantiations for launches whose attention tasks run two query tiles each
   // (chosen by the host where the one-tile tasks outnumber the workgroups and the two-tile tasks do not):
   // self-attention by sa_stage_pairs only. Separate instantiations, so that the others keep their code (and
@@ -2031,7 +2035,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     if (v != u0) {
       wait_vm0();
       __syncthreads();
-      if (!S::RW_ATTN && !resident) ca_prefetch(c, l, b, hd, S_len);
+      if (!S::CA_LATE && !resident) ca_prefetch(c, l, b, hd, S_len);
       pre(hd);
     }
     const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
@@ -2078,9 +2082,9 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     // Everything but the query rows has landed (the prefetched K/V chunks were issued before them); the
     // query rows are waited for where the MFMAs use them.
     // In the row-wise form every workgroup is busy in the stage before, so loads issued ahead of the poll
-    // hold it up (they return in issue order): with RW_ATTN the K/V chunks are DMA'd only now, after the
+    // hold it up (they return in issue order): with CA_LATE the K/V chunks are DMA'd only now, after the
     // query rows have landed, and arrive during the query projection.
-    if constexpr (S::RW_ATTN) {
+    if constexpr (S::CA_LATE) {
       wait_vm0();
       if (!resident) ca_prefetch(c, l, b, hd, S_len);
     } else {
@@ -2157,7 +2161,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       *reinterpret_cast<u32x2*>(Qh + off) = hi;
       *reinterpret_cast<u32x2*>(Ql + off) = lo;
     }
-    if constexpr (S::RW_ATTN) wait_vm0();  // this wave's K/V DMAs (the barrier covers the other waves')
+    if constexpr (S::CA_LATE) wait_vm0();  // this wave's K/V DMAs (the barrier covers the other waves')
     __syncthreads();
     MKX_TR(c, 1);
     AttnState A;
@@ -2640,7 +2644,7 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
   // the source K/V chunks after the rows (the poll does not wait behind them); the fp8 kernels without
   // two-tile self-attention DMA them during the barrier before the stage
   wait_vm0();
-  if constexpr (S::RW_ATTN || S::PAIRS) ca_prefetch(c, l, b, hd, S_len);
+  if constexpr (S::CA_LATE) ca_prefetch(c, l, b, hd, S_len);
   MKX_TR(c, 3);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -3047,7 +3051,7 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   } else if (ca_pairs) {
     // two-tile cross-attention tasks: task u runs sample-head u % (B NH); the fp8 kernels without two-tile
     // self-attention DMA its source K/V here, the others after the poll
-    if constexpr (!S::RW_ATTN && !S::PAIRS) {
+    if constexpr (!S::CA_LATE) {
       const int nhb = p.B * S::NH, u = task_first(c, d.pk);
       if (u < nhb * ((p.Mqp / 16 + 1) / 2)) {
         const int hh = u % nhb;
@@ -3060,7 +3064,7 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
     if (at.ok) {
       const int b = at.hh / S::NH, hd = at.hh % S::NH;
       if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
-      else if (!S::RW_ATTN) ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);  // (RW_ATTN: after the poll)
+      else if (!S::CA_LATE) ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);  // (CA_LATE: after the poll)
     }
   } else if (d.st == ST_TAIL) {
     // workgroups with a tail task: the final modulation rows, and the Wout rows of the task's dims (the real
