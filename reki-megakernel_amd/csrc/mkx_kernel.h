@@ -2552,8 +2552,8 @@ __device__ __forceinline__ void sa_stage_pairs(Ctx<S>& c, const Desc& d, const i
 // single-tile tasks outnumber the workgroups, the two-tile tasks do not, and every source fits the three LDS
 // ring slots). Task u: sample-head u % nhb, tiles 2 j and 2 j + 1 (j = u / nhb; a last odd tile alone, whose
 // second state runs on a copy of the first and is discarded). The task loads the head's Wq fragments, the
-// sample's source keys and values and both tiles' rows once, projects the two tiles' queries one after the
-// other (the same steps as ca_stage), and runs both through each key block with the block's fragments read
+// sample's source keys and values and both tiles' rows once, projects the two tiles' queries in one pass over
+// the k-blocks (per tile the steps of ca_stage), and runs both through each key block with the block's fragments read
 // once; each tile's result is merged, stored and published as ca_stage does, so the outputs are the same bits.
 template <class S>
 __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const int* s_ks, BarCtx& bc, int g) {
@@ -2567,13 +2567,13 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
   float* yca = (float*)(fr + S::yca_off(NRP));
   const char* wq = p.wqca + l * p.s_o;
   const char* shs = p.shs + ((long long)(d.s * p.L + l) * 3 + 1) * p.B * S::H * 4;
-  // the LDS map of ca_stage; the second tile's queries are staged in the merge area until both states have
-  // read them
+  // the LDS map of ca_stage; the second tile's query partials, then its queries, are staged in the merge area
+  // until both states have read them
   char* red = c.smem + S::ABUF + 32768;
   char* Qh0 = c.smem + S::ABUF + 32768 + NWAVES * 4 * 2 * 68 * 16;
   float* mrg = (float*)(Qh0 + 4096);
   char* Qh1 = (char*)mrg;
-  float* ssw = (float*)(c.smem + S::SMALL);  // [4 waves][16 rows]
+  float* ssw = (float*)(c.smem + S::SMALL);  // [tile][4 waves][16 rows]
   const int NHB = p.B * S::NH, NP = (NQT + 1) / 2;
   const uint32_t vlane = (uint32_t)c.lane * 16;
   const int u = task_first(c, PL_CA);
@@ -2646,48 +2646,67 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
   wait_vm0();
   if constexpr (S::CA_LATE) ca_prefetch(c, l, b, hd, S_len);
   MKX_TR(c, 3);
+  {
+    // both tiles' query rows in one pass over the k-blocks ([tile][column tile][k-block parity]); the second
+    // tile's partials go to the merge area, the shift partials (the same for both) to red once
+    f32x4 acc[2][4][2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if (t) __syncthreads();  // the first tile's partials in red and ssw have been read
-    {
-      f32x4 acc[4][2];
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) acc[nt][0] = acc[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < 4; ++nt) acc[t][nt][0] = acc[t][nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < KPW; ++i)
+    for (int i = 0; i < KPW; ++i)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[nt][i & 1] = mfma16h(wf[nt][i], yh[t][i], acc[nt][i & 1]);
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[t][nt][i & 1] = mfma16h(wf[nt][i], yh[t][i], acc[t][nt][i & 1]);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
       const float ssp = ss_pairs_sum<S::HT / 8>(ssv[t]);
-      if (c.lane < 16) ssw[c.wave * 16 + c.lane] = ssp;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int sl = c.lane + (c.lane >> 4);
-        sts16(red + (((c.wave * 4 + nt) * 2 + 0) * 68 + sl) * 16, as_u4(acc[nt][0] + acc[nt][1]));
-        sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 68 + sl) * 16, as_u4(accb[nt][0] + accb[nt][1]));
-      }
+      if (c.lane < 16) ssw[t * 64 + c.wave * 16 + c.lane] = ssp;
     }
-    __syncthreads();
-    {
-      const int nt = cg >> 2, lr = r + 16 * (cg & 3), lb = b + 16 * (cg & 3);
-      f32x4 qa4[NWAVES], ba[NWAVES];
+    const int sl = c.lane + (c.lane >> 4);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      sts16(red + (((c.wave * 4 + nt) * 2 + 0) * 68 + sl) * 16, as_u4(acc[0][nt][0] + acc[0][nt][1]));
+      sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 68 + sl) * 16, as_u4(accb[nt][0] + accb[nt][1]));
+      sts16((char*)mrg + ((c.wave * 4 + nt) * 68 + sl) * 16, as_u4(acc[1][nt][0] + acc[1][nt][1]));
+    }
+  }
+  __syncthreads();
+  // q of row r, columns 4 cg .. 4 cg + 3, of both tiles (the steps of ca_stage)
+  const int dd = 4 * cg;
+  const int qoff = (dd >> 5) * 1024 + (r + 16 * ((dd & 31) >> 3)) * 16 + (dd & 4) * 2;
+  u32x2 qhi[2], qlo[2];
+  {
+    const int nt = cg >> 2, lr = r + 16 * (cg & 3), lb = b + 16 * (cg & 3);
+    f32x4 ba[NWAVES];
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) ba[w] = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 68 + lb + (lb >> 4)) * 16));
+    lds_batch(ba);
+    float bv[4] = {ba[0][0], ba[0][1], ba[0][2], ba[0][3]};
+#pragma unroll
+    for (int w = 1; w < NWAVES; ++w)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] += ba[w][e];
+    const f32x4 gw = {1.0f + __uint_as_float(wn.x << 16), 1.0f + __uint_as_float(wn.x & 0xffff0000u),
+                      1.0f + __uint_as_float(wn.y << 16), 1.0f + __uint_as_float(wn.y & 0xffff0000u)};
+    const float sgn = cg < 8 ? -1.0f : 1.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 qa4[NWAVES];
       float sw[NWAVES];
 #pragma unroll
       for (int w = 0; w < NWAVES; ++w) {
-        qa4[w] = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 0) * 68 + lr + (lr >> 4)) * 16));
-        ba[w] = ldf4((const float*)(red + (((w * 4 + nt) * 2 + 1) * 68 + lb + (lb >> 4)) * 16));
-        sw[w] = ssw[16 * w + r];
+        const int slot = ((w * 4 + nt) * (t ? 1 : 2)) * 68 + lr + (lr >> 4);
+        qa4[w] = ldf4((const float*)((t ? (char*)mrg : red) + slot * 16));
+        sw[w] = ssw[t * 64 + 16 * w + r];
       }
       lds_batch(qa4);
-      lds_batch(ba);
       lds_batch(sw);
       f32x4 qv = qa4[0];
-      float bv[4] = {ba[0][0], ba[0][1], ba[0][2], ba[0][3]};
 #pragma unroll
-      for (int w = 1; w < NWAVES; ++w) {
-        qv += qa4[w];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] += ba[w][e];
-      }
+      for (int w = 1; w < NWAVES; ++w) qv += qa4[w];
       const float rs = rsqrtf((sw[0] + sw[1] + sw[2] + sw[3]) * (1.0f / (float)S::H) + p.eps);
       f32x4 x;
 #pragma unroll
@@ -2695,25 +2714,21 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
       float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
       ss = row_sum16(ss);
       const float rn = rsqrtf(ss / 64.f + p.qk_eps);
-      const f32x4 gw = {1.0f + __uint_as_float(wn.x << 16), 1.0f + __uint_as_float(wn.x & 0xffff0000u),
-                        1.0f + __uint_as_float(wn.y << 16), 1.0f + __uint_as_float(wn.y & 0xffff0000u)};
       const f32x4 xn = x * rn * gw;
-      const float sgn = cg < 8 ? -1.0f : 1.0f;
       f32x4 uq;
 #pragma unroll
       for (int e = 0; e < 4; ++e) uq[e] = xn[e] * cs[t][e] + sgn * lane_xor8(xn[e]) * sn[t][e];
-      const int dd = 4 * cg;
-      const int off = (dd >> 5) * 1024 + (r + 16 * ((dd & 31) >> 3)) * 16 + (dd & 4) * 2;
-      u32x2 hi, lo;
-      hi[0] = cvt_pk(uq[0], uq[1]);
-      hi[1] = cvt_pk(uq[2], uq[3]);
-      lo[0] = cvt_pk(uq[0] - __uint_as_float(hi[0] << 16), uq[1] - __uint_as_float(hi[0] & 0xffff0000u));
-      lo[1] = cvt_pk(uq[2] - __uint_as_float(hi[1] << 16), uq[3] - __uint_as_float(hi[1] & 0xffff0000u));
-      char* Qh = t ? Qh1 : Qh0;
-      *reinterpret_cast<u32x2*>(Qh + off) = hi;
-      *reinterpret_cast<u32x2*>(Qh + 2048 + off) = lo;
+      qhi[t][0] = cvt_pk(uq[0], uq[1]);
+      qhi[t][1] = cvt_pk(uq[2], uq[3]);
+      qlo[t][0] = cvt_pk(uq[0] - __uint_as_float(qhi[t][0] << 16), uq[1] - __uint_as_float(qhi[t][0] & 0xffff0000u));
+      qlo[t][1] = cvt_pk(uq[2] - __uint_as_float(qhi[t][1] << 16), uq[3] - __uint_as_float(qhi[t][1] & 0xffff0000u));
     }
   }
+  *reinterpret_cast<u32x2*>(Qh0 + qoff) = qhi[0];
+  *reinterpret_cast<u32x2*>(Qh0 + 2048 + qoff) = qlo[0];
+  __syncthreads();  // every thread has read the second tile's partials in the merge area
+  *reinterpret_cast<u32x2*>(Qh1 + qoff) = qhi[1];
+  *reinterpret_cast<u32x2*>(Qh1 + 2048 + qoff) = qlo[1];
   wait_vm0();  // this wave's K/V DMAs (the barrier covers the other waves')
   __syncthreads();
   MKX_TR(c, 1);
