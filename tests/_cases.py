@@ -16,11 +16,13 @@ def oracle_dims(cfg: SY.ExpertConfig) -> ER.ExpertDims:
                          tdim=cfg.tdim, eps=cfg.eps, qk_eps=cfg.qk_eps, act=cfg.act)
 
 
-def make_case(cfg: SY.ExpertConfig, device="cuda", seed=0, random_mods=False, nan_pads=False):
+def make_case(cfg: SY.ExpertConfig, device="cuda", seed=0, random_mods=False, nan_pads=False, ca_len=None,
+              kv_start=None):
+    """ca_len / kv_start: per-sample source lengths and first valid memory rows (default cfg.S, cfg.kv_start)."""
     W = SY.make_weights(cfg, seed)
     model = SY.SyntheticReki(cfg, W, device=device)
     inp = SY.make_inputs(cfg)
-    past = model.register_prepare(inp["ctx"], inp["mem_states"])
+    past = model.register_prepare(inp["ctx"], inp["mem_states"], ca_len=ca_len, kv_start=kv_start)
     mods, dt = model._step_modulations(cfg.num_steps, inp["state_cond"])
     if random_mods:
         g = torch.Generator().manual_seed(99)

@@ -211,6 +211,22 @@ def test_two_tile_self_attention_with_a_streamed_source():
                 make_case(replace(SY.WORKLOADS["D-b4"], L=2, T_act=40, S=520, SP=520)))
 
 
+def test_ragged_lengths_in_two_tile_cross_attention_fp16():
+    # batch 8 at H 768 (two-tile cross-attention tasks; the second self-attention tiles resident) with a
+    # source length and a memory start of its own per sample: 1 to 300 source rows, 1 to 96 memory rows
+    from dataclasses import replace
+    case = make_case(replace(SY.WORKLOADS["B"], L=2), ca_len=[300, 1, 33, 150, 299, 32, 128, 7],
+                     kv_start=[0, 32, 64, 95, 16, 0, 48, 80])
+    _check_loop("b8 ragged source and memory (two-tile cross-attention)", case)
+
+
+def test_ragged_lengths_in_two_tile_attention_fp8():
+    # the fp8 two-tile instantiations (both attention stages in two-tile tasks) with ragged samples
+    from dataclasses import replace
+    case = make_case(replace(SY.WORKLOADS["D-b4"], L=2), ca_len=[300, 1, 129, 257], kv_start=[0, 95, 33, 64])
+    _check_loop("fp8 b4 ragged source and memory (two-tile attention tasks)", case)
+
+
 def test_config_A_rowwise_form():
     # the headline shape forced into the row-wise form (one-tile tasks, row-wise GEMMs and step tail)
     with _gemm_form("rows"):
