@@ -25,7 +25,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFS = 2500.0  # dense fp16 (and bf16) MFMA peak
 KERNEL_SOURCES = ("mkx_kernel.h", "mkx_device.h", "mkx.hip", "mkx_mk768.hip", "mkx_mk1024.hip", "mkx_mk256.hip",
                   "mkx_mk768r.hip", "mkx_mk1024r.hip", "mkx_mk256r.hip", "mkx_mk768p.hip", "mkx_mk1024p.hip",
-                  "mkx_mk256p.hip")
+                  "mkx_mk256p.hip", "mkx_mk768l.hip", "mkx_mk1024l.hip", "mkx_mk256l.hip")
 
 
 def kernel_source_hash() -> str:

@@ -108,7 +108,11 @@ namespace mkx {
   extern template __global__ void mkx_megakernel<H, I, false, true, true>(Params);  \
   extern template __global__ void mkx_megakernel<H, I, true, true, true>(Params);        \
   extern template __global__ void mkx_megakernel<H, I, true, true, false, true>(Params);  \
-  extern template __global__ void mkx_megakernel<H, I, true, true, true, true>(Params);
+  extern template __global__ void mkx_megakernel<H, I, true, true, true, true>(Params);   \
+  extern template __global__ void mkx_megakernel<H, I, false, false, false, false, true>(Params); \
+  extern template __global__ void mkx_megakernel<H, I, true, false, false, false, true>(Params);  \
+  extern template __global__ void mkx_megakernel<H, I, false, false, true, false, true>(Params);  \
+  extern template __global__ void mkx_megakernel<H, I, true, false, true, false, true>(Params);
 MKX_EXTERN(768, 3072)
 MKX_EXTERN(1024, 4096)
 MKX_EXTERN(256, 512)
@@ -123,22 +127,27 @@ const void* kernel_of(bool w8) {
             : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false, ROWWISE, YS>);
 }
 template <int H, int I>
-const void* kernel_of(bool w8, bool rowwise, bool ys, bool pairs) {
+const void* kernel_of(bool w8, bool rowwise, bool ys, bool pairs, bool longsrc) {
   // (two-tile self-attention: fp8-weight row-wise instantiations only)
   if (pairs) return !w8 ? nullptr
                         : ys ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, true, true, true>)
                              : reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, true, false, true>);
+  if (longsrc && !rowwise)
+    return w8 ? (ys ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, false, true, false, true>)
+                    : reinterpret_cast<const void*>(&mkx_megakernel<H, I, true, false, false, false, true>))
+              : (ys ? reinterpret_cast<const void*>(&mkx_megakernel<H, I, false, false, true, false, true>)
+                    : reinterpret_cast<const void*>(&mkx_megakernel<H, I, false, false, false, false, true>));
   return rowwise ? (ys ? kernel_of<H, I, true, true>(w8) : kernel_of<H, I, true, false>(w8))
                  : (ys ? kernel_of<H, I, false, true>(w8) : kernel_of<H, I, false, false>(w8));
 }
 
 // rowwise: the form whose GEMM stages compute whole-K products per wave (launches with many row tiles); ys: the
 // twin with scaled AdaRMS operands (an operand shift); pairs: the row-wise form with two-tile self-attention
-// tasks (fp8 weights)
-const void* pick_kernel(int H, int I, bool w8, bool rowwise, bool ys = false, bool pairs = false) {
-  if (H == 768 && I == 3072) return kernel_of<768, 3072>(w8, rowwise, ys, pairs);
-  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>(w8, rowwise, ys, pairs);
-  if (H == 256 && I == 512) return kernel_of<256, 512>(w8, rowwise, ys, pairs);
+// tasks (fp8 weights); longsrc: the form with passes for sources beyond the three-chunk ring
+const void* pick_kernel(int H, int I, bool w8, bool rowwise, bool ys = false, bool pairs = false, bool longsrc = false) {
+  if (H == 768 && I == 3072) return kernel_of<768, 3072>(w8, rowwise, ys, pairs, longsrc);
+  if (H == 1024 && I == 4096) return kernel_of<1024, 4096>(w8, rowwise, ys, pairs, longsrc);
+  if (H == 256 && I == 512) return kernel_of<256, 512>(w8, rowwise, ys, pairs, longsrc);
   return nullptr;
 }
 
@@ -313,6 +322,8 @@ struct mkx_handle {
   const void* kernel_rows_ys = nullptr;
   const void* kernel_pairs = nullptr;  // the row-wise instantiations with two-tile self-attention tasks (fp8)
   const void* kernel_pairs_ys = nullptr;
+  const void* kernel_long = nullptr;  // the form with passes for sources beyond the three-chunk ring
+  const void* kernel_long_ys = nullptr;
   int gemm_form = -1;    // MKX_GEMM_FORM at creation: 0 passes, 1 row-wise, -1 chosen per launch
   int last_form = -1;    // form of the last launch (0 passes, 1 row-wise; -1 before the first)
   unsigned spin_limit = SPIN_LIMIT;
@@ -399,6 +410,8 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
   h->kernel_rows_ys = pick_kernel(d.H, d.I, w8, true, true);
   h->kernel_pairs = pick_kernel(d.H, d.I, w8, true, false, true);
   h->kernel_pairs_ys = pick_kernel(d.H, d.I, w8, true, true, true);
+  h->kernel_long = pick_kernel(d.H, d.I, w8, false, false, false, true);
+  h->kernel_long_ys = pick_kernel(d.H, d.I, w8, false, true, false, true);
   auto bail = [&](int code) { free_handle(h); return code; };
 #define HCHK(x)                                                                                       \
   do {                                                                                                \
@@ -420,7 +433,7 @@ int mkx_create(const mkx_dims* dims, const mkx_weights* w, void* stream_, mkx_ha
     HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NTHREADS, 0));
     if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel (scaled AdaRMS operands) does not fit one workgroup per CU"));
   }
-  for (const void* k : {h->kernel_pairs, h->kernel_pairs_ys}) {
+  for (const void* k : {h->kernel_pairs, h->kernel_pairs_ys, h->kernel_long, h->kernel_long_ys}) {
     if (!k) continue;
     HCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NTHREADS, 0));
     if (per_cu < 1) return bail(fail(MKX_ENORESIDENT, "megakernel (two-tile attention tasks) does not fit one workgroup per CU"));
@@ -723,8 +736,10 @@ int mkx_run(mkx_handle* h, const mkx_step_args* a, void* stream_) {
     pairs = pairs && h->w8;
   }
   void* args[] = {&p};
-  const void* kern = h->operand_shift ? (pairs ? h->kernel_pairs_ys : rows ? h->kernel_rows_ys : h->kernel_ys)
-                                      : (pairs ? h->kernel_pairs : rows ? h->kernel_rows : h->kernel);
+  // the form with passes: sources beyond the three 128-row chunks of the cross-attention ring stream the rest
+  const bool longsrc = !rows && a->SP > 384;
+  const void* kern = h->operand_shift ? (pairs ? h->kernel_pairs_ys : rows ? h->kernel_rows_ys : longsrc ? h->kernel_long_ys : h->kernel_ys)
+                                      : (pairs ? h->kernel_pairs : rows ? h->kernel_rows : longsrc ? h->kernel_long : h->kernel);
   if (capturing) h->captured = 1;
   if (capturing || h->plain_launch) {
     // co-residency was established at creation (one workgroup per CU fits); capture a plain launch

@@ -117,7 +117,7 @@ typedef const __attribute__((address_space(4))) Params CP;
 
 __host__ __device__ constexpr int ceil_to(int a, int m) { return (a + m - 1) / m * m; }
 
-template <int H_, int I_, bool W8_ = false, bool RW_ = false, bool YS_ = false, bool PR_ = false>
+template <int H_, int I_, bool W8_ = false, bool RW_ = false, bool YS_ = false, bool PR_ = false, bool LS_ = false>
 struct Shape {
   // YS: AdaRMS operands scaled by Params::yinv (the launches with an operand shift)
   static constexpr bool YS = YS_;
@@ -140,6 +140,10 @@ struct Shape {
   // register allocation) unchanged: compiled into them, the two-tile path made the kernels slower for every
   // launch (workload D 7.59 -> 7.90 ms without taking it).
   static constexpr bool PAIRS = RW_ && PR_;
+  // LONG: the instantiations of the form with passes for sources longer than the three-chunk LDS ring (the
+  // host picks them for launches whose source exceeds 384 rows): cross-attention streams the chunks beyond
+  // the third into registers (ca_stage). Separate instantiations, so that the others keep their code.
+  static constexpr bool LONG = LS_ && !RW_;
   // packed weight chunks (16 output columns x 32 K values, one MFMA operand fragment per lane): fp16 (packed
   // from bf16), or fp8 e4m3 decoded to fp16 fragments when read (weight-only quantisation)
   static constexpr bool W8 = W8_;
@@ -1571,6 +1575,52 @@ __device__ __forceinline__ void attn_block2(AttnState& A, int lane, const char* 
   }
 }
 
+// attn_block for one block of 32 source keys (keys [0, khi) valid; no residual parts, no key factors) whose
+// K and V^T fragments are already in registers: the fragments attn_block reads from LDS, in the same order, so
+// the result is the same bits.
+__device__ __forceinline__ void attn_block_rf(AttnState& A, int lane, const bf16x8 (&kf)[4], const bf16x8 (&vf)[4], int khi,
+                                              float qs) {
+  f32x4 s[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      s[h] = mfma16(kf[h * 2 + db], A.qh[db], s[h]);
+      s[h] = mfma16(kf[h * 2 + db], A.ql[db], s[h]);
+    }
+  }
+  float pv[8];
+  float mb = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+    pv[j] = s[j >> 2][j & 3] * qs + ((key >= 0 && key < khi) ? 0.f : -INFINITY);
+    mb = fmaxf(mb, pv[j]);
+  }
+  mb = xor32_max(xor16_max(mb));
+  const float mn = fmaxf(A.m, mb);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float alpha = __expf(A.m - mu);
+  A.m = mn;
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    pv[j] = __expf(pv[j] - mu);
+    ps += pv[j];
+  }
+  A.den = A.den * alpha + ps;
+  bf16x8 ph, pl;
+  split8(pv, ph, pl);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    f32x4 a = A.acc[dt] * alpha;
+    a = mfma16(vf[dt], ph, a);
+    a = mfma16(vf[dt], pl, a);
+    A.acc[dt] = a;
+  }
+}
+
 __device__ __forceinline__ void attn_begin(AttnState& A, const char* Qh, const char* Ql, int lane) {
 #pragma unroll
   for (int db = 0; db < 2; ++db) {
@@ -2180,22 +2230,65 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
       if (k2 < S_len)
         attn_block(A, c.lane, s2 + c.wave * 4096, nullptr, s2 + 16384 + c.wave * 4096, nullptr, 0, S_len - k2, p.sm_scale, nullptr);
     }
-    for (int cc = 0; nch > 3 && cc < nch; ++cc) {
-      if (cc >= 3) {
-        // chunk cc was issued three iterations ago; the younger chunks cc + 1, cc + 2 may still be in
-        // flight: 8 DMAs per wave each, except the last chunk, which may issue fewer
-        if (cc + 2 < nch - 1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-        else if (cc + 1 < nch - 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else wait_vm0();
-        __syncthreads();
+    if constexpr (S::LONG) {
+      if (nch > 3) {
+        // chunks 0-2 from the LDS ring (DMA'd before the stage); the later chunks streamed into registers,
+        // each wave loading only its own 32-key block of a chunk (the fragments attn_block would read from the
+        // ring, from the addresses ca_dma_chunk copies) one chunk ahead of its use: no ring refills and no
+        // barriers between chunks. Blocks in the same order with the same arithmetic: the same bits.
+        const bf16_t* kb_ = p.kca[l] + (long long)b * p.src_sb;
+        const int ncb = p.SPP / 32;
+        const bf16_t* vt = p.cavt + ((long long)(l * p.B + b) * S::NH + hd) * ncb * 2048;
+        bf16x8 kn[4], vn[4];
+        // wave w's block of chunk cc: K chunks 4 w + i of the ring (key tile 2 w + i / 2, d-block i % 2), V^T
+        // block 4 cc + w; rows beyond the length repeat the last valid one and blocks beyond it are not used
+        auto load_block = [&](int cc) {
+          const int kbl = min(cc * 4 + c.wave, ncb - 1);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = min(cc * 128 + (2 * c.wave + (i >> 1)) * 16 + (c.lane & 15), S_len - 1);
+            kn[i] = __builtin_bit_cast(bf16x8, ld16(kb_ + ((long long)key * S::NH + hd) * HD + (i & 1) * 32 + 8 * (c.lane >> 4)));
+          }
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) vn[dt] = __builtin_bit_cast(bf16x8, ld16(vt + ((long long)kbl * 4 + dt) * 512 + c.lane * 8));
+        };
+        // one chunk in flight ahead of the one in use (two measured slower)
+        load_block(3);
+        for (int cc = 0; cc < 3; ++cc) {
+          char* slot = ca_slot(c, cc);
+          const int k0 = cc * 128 + c.wave * 32;  // (< S_len: more than three chunks)
+          attn_block(A, c.lane, slot + c.wave * 4096, nullptr, slot + 16384 + c.wave * 4096, nullptr, 0, S_len - k0, p.sm_scale, nullptr);
+        }
+        for (int cc = 3; cc < nch; ++cc) {
+          bf16x8 kc[4], vc[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            kc[i] = kn[i];
+            vc[i] = vn[i];
+          }
+          if (cc + 1 < nch) load_block(cc + 1);
+          const int k0 = cc * 128 + c.wave * 32;
+          if (k0 < S_len) attn_block_rf(A, c.lane, kc, vc, S_len - k0, p.sm_scale);
+        }
       }
-      char* slot = ca_slot(c, cc);
-      const int k0 = cc * 128 + c.wave * 32;
-      if (k0 < S_len)
-        attn_block(A, c.lane, slot + c.wave * 4096, nullptr, slot + 16384 + c.wave * 4096, nullptr, 0, S_len - k0, p.sm_scale, nullptr);
-      if (cc + 3 < nch) {
-        __syncthreads();
-        ca_dma_chunk(c, l, b, hd, cc + 3, S_len);
+    } else {
+      for (int cc = 0; nch > 3 && cc < nch; ++cc) {
+        if (cc >= 3) {
+          // chunk cc was issued three iterations ago; the younger chunks cc + 1, cc + 2 may still be in
+          // flight: 8 DMAs per wave each, except the last chunk, which may issue fewer
+          if (cc + 2 < nch - 1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+          else if (cc + 1 < nch - 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+          else wait_vm0();
+          __syncthreads();
+        }
+        char* slot = ca_slot(c, cc);
+        const int k0 = cc * 128 + c.wave * 32;
+        if (k0 < S_len)
+          attn_block(A, c.lane, slot + c.wave * 4096, nullptr, slot + 16384 + c.wave * 4096, nullptr, 0, S_len - k0, p.sm_scale, nullptr);
+        if (cc + 3 < nch) {
+          __syncthreads();
+          ca_dma_chunk(c, l, b, hd, cc + 3, S_len);
+        }
       }
     }
     MKX_TR(c, 2);
@@ -3185,9 +3278,9 @@ __device__ __forceinline__ StagePos next_stage(unsigned mask, StagePos q, int to
 }
 
 // ------------------------------------------------------------------------------------------------
-template <int H, int I, bool W8, bool ROWWISE, bool YSHIFT = false, bool PAIRS = false>
+template <int H, int I, bool W8, bool ROWWISE, bool YSHIFT = false, bool PAIRS = false, bool LONGSRC = false>
 __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
-  using S = Shape<H, I, W8, ROWWISE, YSHIFT, PAIRS>;
+  using S = Shape<H, I, W8, ROWWISE, YSHIFT, PAIRS, LONGSRC>;
   __shared__ __attribute__((aligned(1024))) char smem[S::LDS];
   CP& p = *(CP*)(__builtin_amdgcn_kernarg_segment_ptr());
   Ctx<S> c(p, smem);

@@ -32,6 +32,9 @@ UNITS = (
     ("mkx_mk768p.hip", ()),
     ("mkx_mk1024p.hip", ()),
     ("mkx_mk256p.hip", ()),
+    ("mkx_mk768l.hip", ("-mllvm", "-amdgpu-sched-strategy=max-memory-clause")),
+    ("mkx_mk1024l.hip", ()),
+    ("mkx_mk256l.hip", ()),
 )
 COMMON = ("--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
           # packed fp32 instructions stay off: every HIP source is compiled without them
