@@ -2351,6 +2351,115 @@ __device__ __forceinline__ void attn_block_n(AttnState (&A)[NQ], int lane, const
   }
 }
 
+// attn_block_n and attn_block2_n on K and V^T fragments already in registers (the fragments they read from
+// LDS, in the same order): the same bits.
+template <int NQ>
+__device__ __forceinline__ void attn_block_n_rf(AttnState (&A)[NQ], int lane, const bf16x8 (&kf)[4], const bf16x8 (&vf)[4], int khi,
+                                                float qs) {
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        s[h] = mfma16(kf[h * 2 + db], A[q].qh[db], s[h]);
+        s[h] = mfma16(kf[h * 2 + db], A[q].ql[db], s[h]);
+      }
+    }
+    float pv[8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+      pv[j] = s[j >> 2][j & 3] * qs + ((key >= 0 && key < khi) ? 0.f : -INFINITY);
+      mb = fmaxf(mb, pv[j]);
+    }
+    mb = xor32_max(xor16_max(mb));
+    const float mn = fmaxf(A[q].m, mb);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __expf(A[q].m - mu);
+    A[q].m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pv[j] = __expf(pv[j] - mu);
+      ps += pv[j];
+    }
+    A[q].den = A[q].den * alpha + ps;
+    bf16x8 ph, pl;
+    split8(pv, ph, pl);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 a = A[q].acc[dt] * alpha;
+      a = mfma16(vf[dt], ph, a);
+      a = mfma16(vf[dt], pl, a);
+      A[q].acc[dt] = a;
+    }
+  }
+}
+
+template <int NQ>
+__device__ __forceinline__ void attn_block2_n_rf(AttnState (&A)[NQ], int lane, const bf16x8 (&k0f)[4], const bf16x8 (&v0f)[4],
+                                                 int khi0, const bf16x8 (&k1f)[4], const bf16x8 (&v1f)[4], int khi1, float qs) {
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 s[2][2];
+#pragma unroll
+    for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) s[bk][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+        for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            s[bk][h] = mfma16((bk ? k1f : k0f)[h * 2 + db], hl ? A[q].ql[db] : A[q].qh[db], s[bk][h]);
+    float pv[2][8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int bk = 0; bk < 2; ++bk) {
+      const int khi = bk ? khi1 : khi0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+        pv[bk][j] = s[bk][j >> 2][j & 3] * qs + (key < khi ? 0.f : -INFINITY);
+        mb = fmaxf(mb, pv[bk][j]);
+      }
+    }
+    mb = xor32_max(xor16_max(mb));
+    const float mn = fmaxf(A[q].m, mb);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __expf(A[q].m - mu);
+    A[q].m = mn;
+    float ps[2] = {0.f, 0.f};
+#pragma unroll
+    for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pv[bk][j] = __expf(pv[bk][j] - mu);
+        ps[bk] += pv[bk][j];
+      }
+    A[q].den = A[q].den * alpha + (ps[0] + ps[1]);
+    bf16x8 ph[2], pl[2];
+    split8(pv[0], ph[0], pl[0]);
+    split8(pv[1], ph[1], pl[1]);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 a = A[q].acc[dt] * alpha;
+      a = mfma16(v0f[dt], ph[0], a);
+      a = mfma16(v1f[dt], ph[1], a);
+      a = mfma16(v0f[dt], pl[0], a);
+      a = mfma16(v1f[dt], pl[1], a);
+      A[q].acc[dt] = a;
+    }
+  }
+}
+
 // One block of 32 keys for NQ query tiles at once (the arguments of attn_block, with one score scale per
 // tile): the block's K and V^T fragments (and residual parts, key factors) are read once, each state's
 // chains and softmax arithmetic are those of attn_block.
@@ -2734,10 +2843,30 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
       }
     }
   }
-  // the source K/V chunks after the rows (the poll does not wait behind them); the fp8 kernels without
-  // two-tile self-attention DMA them during the barrier before the stage
-  wait_vm0();
-  if constexpr (S::CA_LATE) ca_prefetch(c, l, b, hd, S_len);
+  // the source K/V after the rows (the poll does not wait behind them): with CA_LATE, this wave's three
+  // 32-key blocks (w, w + 4, w + 8: the fragments the LDS ring would hold for it) straight into registers, as
+  // they are read by this wave only (as LDS DMA, 96 KB took ~2.6 us to issue, holding the waves before the
+  // query projection); the other fp8 kernels DMA the ring during the barrier before the stage
+  bf16x8 kvk[3][4], kvv[3][4];
+  if constexpr (S::CA_LATE) {
+    const bf16_t* kb_ = p.kca[l] + (long long)b * p.src_sb;
+    const int ncb = p.SPP / 32;
+    const bf16_t* vt = p.cavt + ((long long)(l * p.B + b) * S::NH + hd) * ncb * 2048;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      // rows beyond the length repeat a valid one and blocks beyond it are not used
+      const int kbl = min(j * 4 + c.wave, ncb - 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = min(j * 128 + (2 * c.wave + (i >> 1)) * 16 + (c.lane & 15), max(S_len - 1, 0));
+        kvk[j][i] = __builtin_bit_cast(bf16x8, ld16(kb_ + ((long long)key * S::NH + hd) * HD + (i & 1) * 32 + 8 * (c.lane >> 4)));
+      }
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) kvv[j][dt] = __builtin_bit_cast(bf16x8, ld16(vt + ((long long)kbl * 4 + dt) * 512 + c.lane * 8));
+    }
+  } else {
+    wait_vm0();
+  }
   MKX_TR(c, 3);
   {
     // both tiles' query rows in one pass over the k-blocks ([tile][column tile][k-block parity]); the second
@@ -2822,14 +2951,21 @@ __device__ __forceinline__ void ca_stage_pairs(Ctx<S>& c, const Desc& d, const i
   __syncthreads();  // every thread has read the second tile's partials in the merge area
   *reinterpret_cast<u32x2*>(Qh1 + qoff) = qhi[1];
   *reinterpret_cast<u32x2*>(Qh1 + 2048 + qoff) = qlo[1];
-  wait_vm0();  // this wave's K/V DMAs (the barrier covers the other waves')
+  if constexpr (!S::CA_LATE) wait_vm0();  // this wave's K/V DMAs (the barrier covers the other waves')
   __syncthreads();
   MKX_TR(c, 1);
   AttnState A[2];
   attn_begin(A[0], Qh0, Qh0 + 2048, c.lane);
   attn_begin(A[1], Qh1, Qh1 + 2048, c.lane);
   __syncthreads();  // every wave holds both tiles' queries: the merge area may be overwritten
-  {
+  if constexpr (S::CA_LATE) {
+    const int k0 = c.wave * 32, k1 = 128 + c.wave * 32, k2 = 256 + c.wave * 32;
+    if (k1 < S_len)
+      attn_block2_n_rf<2>(A, c.lane, kvk[0], kvv[0], S_len - k0, kvk[1], kvv[1], S_len - k1, p.sm_scale);
+    else if (k0 < S_len)
+      attn_block_n_rf<2>(A, c.lane, kvk[0], kvv[0], S_len - k0, p.sm_scale);
+    if (k2 < S_len) attn_block_n_rf<2>(A, c.lane, kvk[2], kvv[2], S_len - k2, p.sm_scale);
+  } else {
     const int k0 = c.wave * 32, k1 = 128 + c.wave * 32, k2 = 256 + c.wave * 32;
     char* s0 = ca_slot(c, 0);
     char* s1 = ca_slot(c, 1);
