@@ -134,6 +134,10 @@ struct Shape {
   // instantiations and the two-tile ones (not the other fp8 row-wise ones, whose launches, workload D, measured
   // 7.59 -> 7.74 ms with it)
   static constexpr bool CA_LATE = RW_ && (!W8_ || PR_);
+  // CA_REG: the other fp8 row-wise instantiations: one-tile cross-attention over at most three 128-row chunks
+  // loads each wave's source K/V blocks into registers after its poll (ca_stage) instead of the LDS ring DMA'd
+  // ahead of it
+  static constexpr bool CA_REG = RW_ && !CA_LATE;
   // PAIRS: the fp8-weight row-wise instantiations for launches whose attention tasks run two query tiles each
   // (chosen by the host where the one-tile tasks outnumber the workgroups and the two-tile tasks do not):
   // self-attention by sa_stage_pairs only. Separate instantiations, so that the others keep their code (and
@@ -1621,6 +1625,63 @@ __device__ __forceinline__ void attn_block_rf(AttnState& A, int lane, const bf16
   }
 }
 
+// attn_block2 on K and V^T fragments already in registers (the fragments it reads from LDS, in the same order):
+// the same bits.
+__device__ __forceinline__ void attn_block2_rf(AttnState& A, int lane, const bf16x8 (&k0f)[4], const bf16x8 (&v0f)[4], int khi0,
+                                               const bf16x8 (&k1f)[4], const bf16x8 (&v1f)[4], int khi1, float qs) {
+  f32x4 s[2][2];
+#pragma unroll
+  for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) s[bk][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+      for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) s[bk][h] = mfma16((bk ? k1f : k0f)[h * 2 + db], hl ? A.ql[db] : A.qh[db], s[bk][h]);
+  float pv[2][8];
+  float mb = -INFINITY;
+#pragma unroll
+  for (int bk = 0; bk < 2; ++bk) {
+    const int khi = bk ? khi1 : khi0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+      pv[bk][j] = s[bk][j >> 2][j & 3] * qs + (key < khi ? 0.f : -INFINITY);
+      mb = fmaxf(mb, pv[bk][j]);
+    }
+  }
+  mb = xor32_max(xor16_max(mb));
+  const float mn = fmaxf(A.m, mb);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float alpha = __expf(A.m - mu);
+  A.m = mn;
+  float ps[2] = {0.f, 0.f};
+#pragma unroll
+  for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pv[bk][j] = __expf(pv[bk][j] - mu);
+      ps[bk] += pv[bk][j];
+    }
+  A.den = A.den * alpha + (ps[0] + ps[1]);
+  bf16x8 ph[2], pl[2];
+  split8(pv[0], ph[0], pl[0]);
+  split8(pv[1], ph[1], pl[1]);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    f32x4 a = A.acc[dt] * alpha;
+    a = mfma16(v0f[dt], ph[0], a);
+    a = mfma16(v1f[dt], ph[1], a);
+    a = mfma16(v0f[dt], pl[0], a);
+    a = mfma16(v1f[dt], pl[1], a);
+    A.acc[dt] = a;
+  }
+}
+
 __device__ __forceinline__ void attn_begin(AttnState& A, const char* Qh, const char* Ql, int lane) {
 #pragma unroll
   for (int db = 0; db < 2; ++db) {
@@ -2085,7 +2146,7 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     if (v != u0) {
       wait_vm0();
       __syncthreads();
-      if (!S::CA_LATE && !resident) ca_prefetch(c, l, b, hd, S_len);
+      if (!S::CA_LATE && !resident && !(S::CA_REG && nch <= 3)) ca_prefetch(c, l, b, hd, S_len);
       pre(hd);
     }
     const int rq = b * Mqp / 16 + qt;  // row tile of the query rows
@@ -2160,6 +2221,26 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
         sts16(red + (((c.wave * 4 + nt) * 2 + 1) * 68 + sl) * 16, as_u4(accb[nt][0] + accb[nt][1]));
       }
     }
+    // (CA_REG, at most three chunks) this wave's source blocks w, w + 4 and w + 8 into registers: the fragments
+    // the LDS ring would hold for it, loaded once the query projection's MFMAs have freed their registers, while
+    // the projection is finished
+    bf16x8 kvk[3][4], kvv[3][4];
+    if (S::CA_REG && nch <= 3) {
+      const bf16_t* kb_ = p.kca[l] + (long long)b * p.src_sb;
+      const int ncb = p.SPP / 32;
+      const bf16_t* vt = p.cavt + ((long long)(l * p.B + b) * S::NH + hd) * ncb * 2048;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int kbl = min(j * 4 + c.wave, ncb - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = min(j * 128 + (2 * c.wave + (i >> 1)) * 16 + (c.lane & 15), max(S_len - 1, 0));
+          kvk[j][i] = __builtin_bit_cast(bf16x8, ld16(kb_ + ((long long)key * S::NH + hd) * HD + (i & 1) * 32 + 8 * (c.lane >> 4)));
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) kvv[j][dt] = __builtin_bit_cast(bf16x8, ld16(vt + ((long long)kbl * 4 + dt) * 512 + c.lane * 8));
+      }
+    }
     __syncthreads();
     MKX_TR(c, 7);
     {
@@ -2216,7 +2297,15 @@ __device__ __forceinline__ void ca_stage(Ctx<S>& c, const Desc& d, const int* s_
     MKX_TR(c, 1);
     AttnState A;
     attn_begin(A, Qh, Ql, c.lane);
-    if (nch <= 3) {
+    if (S::CA_REG && nch <= 3) {
+      // the same blocks from registers
+      const int k0 = c.wave * 32, k1 = 128 + c.wave * 32, k2 = 256 + c.wave * 32;
+      if (k1 < S_len)
+        attn_block2_rf(A, c.lane, kvk[0], kvv[0], S_len - k0, kvk[1], kvv[1], S_len - k1, p.sm_scale);
+      else if (k0 < S_len)
+        attn_block_rf(A, c.lane, kvk[0], kvv[0], S_len - k0, p.sm_scale);
+      if (k2 < S_len) attn_block_rf(A, c.lane, kvk[2], kvv[2], S_len - k2, p.sm_scale);
+    } else if (nch <= 3) {
       // every chunk is resident: wave w's 32-key blocks w, w + 4 (one 64-key step) and w + 8
       const int k0 = c.wave * 32, k1 = 128 + c.wave * 32, k2 = 256 + c.wave * 32;
       char* s0 = ca_slot(c, 0);
@@ -3283,7 +3372,7 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
   CP& p = c.p;
   MKX_TRW(c, 8);
   bool ca_pairs = false, sa_pairs = false;
-  if constexpr (S::RW) ca_pairs = d.st == ST_CA && p.ca_grp;
+  if constexpr (S::RW && !S::CA_REG) ca_pairs = d.st == ST_CA && p.ca_grp;
   if constexpr (S::PAIRS) sa_pairs = d.st == ST_SA;
   if (sa_pairs) {
     // two-tile self-attention tasks: task u runs sample-head u % (B NH)
@@ -3308,7 +3397,8 @@ __device__ __forceinline__ void prefetch_body(Ctx<S>& c, const Desc& d, const in
     if (at.ok) {
       const int b = at.hh / S::NH, hd = at.hh % S::NH;
       if (d.st == ST_SA) sa_prefetch(c, d.l, b, hd, s_ks[b]);
-      else if (!S::CA_LATE) ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);  // (CA_LATE: after the poll)
+      else if (!S::CA_LATE && !(S::CA_REG && s_ks[MAX_BATCH + b] <= 384))
+        ca_prefetch(c, d.l, b, hd, s_ks[MAX_BATCH + b]);  // (CA_LATE: after the poll; CA_REG: into registers)
     }
   } else if (d.st == ST_TAIL) {
     // workgroups with a tail task: the final modulation rows, and the Wout rows of the task's dims (the real
@@ -3392,7 +3482,7 @@ __device__ __forceinline__ unsigned task_mask(Ctx<S>& c) {
   if (task_first(c, PL_QKV) < 6 * S::NH * p.rgs_qkv) m |= 1u << ST_QKV;
   if (task_first(c, PL_SA) < (S::PAIRS ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_SA;
   if (task_first(c, PL_O) < (S::HT / p.nt_o) * p.rgs_o) m |= 1u << ST_O;
-  if (task_first(c, PL_CA) < (S::RW && p.ca_grp ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_CA;
+  if (task_first(c, PL_CA) < (S::RW && !S::CA_REG && p.ca_grp ? p.B * S::NH * ((p.Mqp / 16 + 1) / 2) : nattn)) m |= 1u << ST_CA;
   if (task_first(c, PL_CAO) < (S::HT / p.nt_cao) * p.rgs_cao) m |= 1u << ST_CAO;
   if (task_first(c, PL_GU) < S::IT) m |= 1u << ST_GU;
   if (task_first(c, PL_DOWN) < (S::HT / p.nt_down) * S::SK || task_first(c, PL_RED) < p.nred) m |= 1u << ST_DOWN;
@@ -3472,7 +3562,9 @@ __global__ void __launch_bounds__(NTHREADS, 1) mkx_megakernel(Params params) {
         else sa_stage(c, cur, s_ks, bc, g);
       }
       else if (cur.st == ST_CA) {
-        if constexpr (S::RW) {
+        // (the CA_REG instantiations never run two-tile tasks: the host takes the two-tile instantiations for
+        // fp8 launches that pair)
+        if constexpr (S::RW && !S::CA_REG) {
           if (c.p.ca_grp) ca_stage_pairs(c, cur, s_ks, bc, g);
           else ca_stage(c, cur, s_ks, bc, g);
         } else {
