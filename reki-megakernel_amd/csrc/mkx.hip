@@ -269,7 +269,11 @@ Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A,
     L.pl[PL_SA] = md(G - nattn);
     L.pl[PL_CA] = md(G - 2 * nattn);
     L.pl[PL_TIN] = md(G - k.NIN);
-    L.pl[PL_RED] = L.pl[PL_TOUT] = md(G - k.NIN - L.nred);
+    L.pl[PL_RED] = md(G - k.NIN - L.nred);
+    // the step tail's output tasks: with the reducers (passes); on the in-projection tasks' workgroups
+    // (row-wise form), which run no reducer, so that the output tasks' prefetch (Wout rows and the final
+    // modulation rows) is issued while the reducers still run rather than after one
+    L.pl[PL_TOUT] = rows ? L.pl[PL_TIN] : L.pl[PL_RED];
   }
   return L;
 }
