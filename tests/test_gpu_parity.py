@@ -144,7 +144,7 @@ def test_gelu_variant_tiny():
 
 
 def test_gelu_variant_at_config_A_size():
-    # the GELU(tanh) MLP that BASELINE's text names, at the headline shape (H 768, I 3072, 10 layers)
+    # the GELU(tanh) MLP of the benchmark's expert description, at the headline shape (H 768, I 3072, 10 layers)
     from dataclasses import replace
     _check_loop("A gelu_tanh", make_case(replace(SY.WORKLOADS["A"], act="gelu_tanh")))
 
