@@ -138,6 +138,10 @@ struct Shape {
   // loads each wave's source K/V blocks into registers after its poll (ca_stage) instead of the LDS ring DMA'd
   // ahead of it
   static constexpr bool CA_REG = RW_ && !CA_LATE;
+  // SA_REG: the same instantiations' self-attention loads each wave's own-key block (K, V^T, hi and lo parts)
+  // and its keys' RMS factors into registers (sa_stage) instead of DMAing every own key into LDS after the
+  // poll, except in launches that also store the register rows' K/V (they read them from LDS)
+  static constexpr bool SA_REG = CA_REG;
   // PAIRS: the fp8-weight row-wise instantiations for launches whose attention tasks run two query tiles each
   // (chosen by the host where the one-tile tasks outnumber the workgroups and the two-tile tasks do not):
   // self-attention by sa_stage_pairs only. Separate instantiations, so that the others keep their code (and
@@ -1625,6 +1629,55 @@ __device__ __forceinline__ void attn_block_rf(AttnState& A, int lane, const bf16
   }
 }
 
+// attn_block on K, V^T fragments and their residual parts already in registers, with the key RMS factors of
+// the lane's 8 keys (the values attn_block reads from LDS, in the same order): the same bits.
+__device__ __forceinline__ void attn_block_rfx(AttnState& A, int lane, const bf16x8 (&kf)[4], const bf16x8 (&kl)[4],
+                                               const bf16x8 (&vf)[4], const bf16x8 (&vl)[4], int khi, float qs,
+                                               const f32x4 (&rkv)[2]) {
+  f32x4 s[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      s[h] = mfma16(kf[h * 2 + db], A.qh[db], s[h]);
+      s[h] = mfma16(kf[h * 2 + db], A.ql[db], s[h]);
+      s[h] = mfma16(kl[h * 2 + db], A.qh[db], s[h]);
+    }
+  }
+  float pv[8];
+  float mb = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+    const float sc = qs * rkv[j >> 2][j & 3];
+    pv[j] = s[j >> 2][j & 3] * sc + ((key >= 0 && key < khi) ? 0.f : -INFINITY);
+    mb = fmaxf(mb, pv[j]);
+  }
+  mb = xor32_max(xor16_max(mb));
+  const float mn = fmaxf(A.m, mb);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float alpha = __expf(A.m - mu);
+  A.m = mn;
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    pv[j] = __expf(pv[j] - mu);
+    ps += pv[j];
+  }
+  A.den = A.den * alpha + ps;
+  bf16x8 ph, pl;
+  split8(pv, ph, pl);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    f32x4 a = A.acc[dt] * alpha;
+    a = mfma16(vf[dt], ph, a);
+    a = mfma16(vf[dt], pl, a);
+    a = mfma16(vl[dt], ph, a);
+    A.acc[dt] = a;
+  }
+}
+
 // attn_block2 on K and V^T fragments already in registers (the fragments it reads from LDS, in the same order):
 // the same bits.
 __device__ __forceinline__ void attn_block2_rf(AttnState& A, int lane, const bf16x8 (&k0f)[4], const bf16x8 (&v0f)[4], int khi0,
@@ -1960,7 +2013,9 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
       __builtin_amdgcn_global_load_lds(ssqk + (long long)(hd * 2 + j) * NRP + b * Mqp + qq, (lds_void*)sq_l, 4, 0, 0);
     }
     const int rt0 = b * Mqp / 16;
-    for (int k = c.wave; k < (resident ? 4 : 4 + 4 * NKT + 8 * KBO); k += NWAVES) {
+    // (SA_REG: only the Q tile goes through LDS; each wave loads its own-key block itself below)
+    const bool reg = S::SA_REG && !want_kv;
+    for (int k = c.wave; k < (resident || reg ? 4 : 4 + 4 * NKT + 8 * KBO); k += NWAVES) {
       if (k < 4) {
         const int db = k >> 1, part = k & 1;
         dma16(qs + ((long long)((2 * hd + db) * RT + rt0 + qt) * 2 + part) * 1024 + c.lane * 16, (part ? Ql : Qh) + db * 1024);
@@ -1981,7 +2036,7 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
     // The memory blocks need only the Q tile and the memory K/V (prefetched before it): every wave issued at
     // least 4 own-key DMAs after its Q piece (M >= 1 gives NKT >= 2 and KBO >= 1, 20 DMAs over 4 waves), so
     // at most 4 outstanding operations means its Q piece has landed (a resident tile loads only its Q tile).
-    if (resident) wait_vm0();
+    if (resident || reg) wait_vm0();
     else wait_vm_le<4>();
     exec_barrier();
     MKX_TR(c, 1);
@@ -1990,26 +2045,79 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
     const float ssq = sq_l[c.lane & 15] + sq_l[16 + (c.lane & 15)];
     const float qsc = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
     const int mb0 = kvs >> 5, nmb = PMP / 32 - mb0;
+    // SA_REG: this wave's own-key block jo (blocks continue the round-robin over the waves after the memory
+    // blocks; at most one per wave, NOWN32 <= 128): its K and V^T chunks (the ones the DMAs above would have
+    // put in LDS for it) and the RMS factors of the lane's 8 keys, issued now so that they land during the
+    // memory blocks
+    const int jo = ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES;
+    bf16x8 okh[4], okl[4], ovh[4], ovl[4];
+    float ssa[8], ssb[8];
+    if (S::SA_REG && reg && jo < KBO) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kt = 2 * jo + (i >> 1), db = i & 1;
+        const int rtk = rt0 + min(kt, NQT - 1);
+        const char* kp = ks + ((long long)((2 * hd + db) * RT + rtk) * 2) * 1024 + c.lane * 16;
+        okh[i] = __builtin_bit_cast(bf16x8, ld16(kp));
+        okl[i] = __builtin_bit_cast(bf16x8, ld16(kp + 1024));
+        const char* vp = vt + ((long long)at.hh * KBO * 8 + 2 * (jo * 4 + i)) * 1024 + c.lane * 16;
+        ovh[i] = __builtin_bit_cast(bf16x8, ld16(vp));
+        ovl[i] = __builtin_bit_cast(bf16x8, ld16(vp + 1024));
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = jo * 32 + (e >> 2) * 16 + 4 * (c.lane >> 4) + (e & 3);
+        const int row = b * Mqp + min(key, Mqp - 1);
+        ssa[e] = ssqk[(long long)((S::NH + hd) * 2) * NRP + row];
+        ssb[e] = ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + row];
+      }
+    }
     for (int beta = c.wave; beta < nmb; beta += NWAVES) {
       const int kb = mb0 + beta;
       attn_block(A, c.lane, memK + kb * 4096, nullptr, memVt + kb * 4096, nullptr, kvs - kb * 32, PM - kb * 32, qsc, nullptr);
     }
-    if (!resident) {
-      wait_vm0();  // the own keys' K and V^T have landed
-      __syncthreads();
-      if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
-      // own keys beyond the sample's rows have no producer: zero their V
-      for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
-        const int key = Mqp + it / HD, dd = it % HD;
-        *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
-        *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
+    if (S::SA_REG && reg) {
+      if (jo < KBO) {
+        // the lane's key factors, and zero V for own keys beyond the sample's rows (no producer): element j of
+        // a V^T fragment is key (j / 4) 16 + 4 (lane / 16) + j % 4 of the block
+        f32x4 rkv[2];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rkv[e >> 2][e & 3] = rsqrtf((ssa[e] + ssb[e]) / 64.f + p.qk_eps);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          u32x4 hv = __builtin_bit_cast(u32x4, ovh[dt]), lv = __builtin_bit_cast(u32x4, ovl[dt]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int key = jo * 32 + (j >> 2) * 16 + 4 * (c.lane >> 4) + (j & 3);
+            if (key >= Mqp) {
+              const uint32_t keep = (j & 1) ? 0x0000ffffu : 0xffff0000u;
+              hv[j >> 1] &= keep;
+              lv[j >> 1] &= keep;
+            }
+          }
+          ovh[dt] = __builtin_bit_cast(bf16x8, hv);
+          ovl[dt] = __builtin_bit_cast(bf16x8, lv);
+        }
+        attn_block_rfx(A, c.lane, okh, okl, ovh, ovl, M - jo * 32, qsc, rkv);
       }
-      __syncthreads();
-    }
-    // own-key blocks continue the round-robin over the waves (block beta on wave beta % 4)
-    for (int beta = nmb + ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES; beta < nmb + KBO; beta += NWAVES) {
-      const int kb = beta - nmb;
-      attn_block(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
+    } else {
+      if (!resident) {
+        wait_vm0();  // the own keys' K and V^T have landed
+        __syncthreads();
+        if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
+        // own keys beyond the sample's rows have no producer: zero their V
+        for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
+          const int key = Mqp + it / HD, dd = it % HD;
+          *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
+          *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
+        }
+        __syncthreads();
+      }
+      // own-key blocks continue the round-robin over the waves (block beta on wave beta % 4)
+      for (int beta = nmb + ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES; beta < nmb + KBO; beta += NWAVES) {
+        const int kb = beta - nmb;
+        attn_block(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
+      }
     }
     MKX_TR(c, 2);
     attn_merge_store(c, A, mrg, ysa, b, hd, qt);
