@@ -138,16 +138,17 @@ struct Shape {
   // loads each wave's source K/V blocks into registers after its poll (ca_stage) instead of the LDS ring DMA'd
   // ahead of it
   static constexpr bool CA_REG = RW_ && !CA_LATE;
-  // SA_REG: the same instantiations' self-attention loads each wave's own-key block (K, V^T, hi and lo parts)
-  // and its keys' RMS factors into registers (sa_stage) instead of DMAing every own key into LDS after the
-  // poll, except in launches that also store the register rows' K/V (they read them from LDS)
-  static constexpr bool SA_REG = CA_REG;
   // PAIRS: the fp8-weight row-wise instantiations for launches whose attention tasks run two query tiles each
   // (chosen by the host where the one-tile tasks outnumber the workgroups and the two-tile tasks do not):
   // self-attention by sa_stage_pairs only. Separate instantiations, so that the others keep their code (and
   // register allocation) unchanged: compiled into them, the two-tile path made the kernels slower for every
   // launch (workload D 7.59 -> 7.90 ms without taking it).
   static constexpr bool PAIRS = RW_ && PR_;
+  // SA_REG: the same instantiations' and the two-tile ones' self-attention loads each wave's own-key block
+  // (K, V^T, hi and lo parts) and its keys' RMS factors into registers (sa_stage, sa_stage_pairs) instead of
+  // DMAing every own key into LDS after the poll, except in launches that also store the register rows' K/V
+  // (they read them from LDS)
+  static constexpr bool SA_REG = CA_REG || PAIRS;
   // LONG: the instantiations of the form with passes for sources longer than the three-chunk LDS ring (the
   // host picks them for launches whose source exceeds 384 rows): cross-attention streams the chunks beyond
   // the third into registers (ca_stage). Separate instantiations, so that the others keep their code.
@@ -2120,6 +2121,9 @@ __device__ __forceinline__ void sa_stage(Ctx<S>& c, const Desc& d, const int* s_
       }
     }
     MKX_TR(c, 2);
+    // every wave has read the query rows' sums of squares (sq_l, in the merge area) before the merge writes
+    // there (the own-key barriers above order them otherwise)
+    if (resident || (S::SA_REG && reg)) exec_barrier();
     attn_merge_store(c, A, mrg, ysa, b, hd, qt);
     if (want_kv && qt == 0) {
       // register rows' k (normed, rotated) and v of step 1, bf16 [L][B][R][NH][64] (src/mk_expert.py:440-470)
@@ -2657,6 +2661,59 @@ __device__ __forceinline__ void attn_block2_n_rf(AttnState (&A)[NQ], int lane, c
   }
 }
 
+// attn_block_nq on K, V^T fragments and their residual parts already in registers, with the key RMS factors of
+// the lane's 8 keys (what attn_block_nq reads from LDS, in the same order): the same bits.
+template <int NQ>
+__device__ __forceinline__ void attn_block_nq_rf(AttnState (&A)[NQ], int lane, const bf16x8 (&kf)[4], const bf16x8 (&kl)[4],
+                                                 const bf16x8 (&vf)[4], const bf16x8 (&vl)[4], int khi, const float (&qs)[NQ],
+                                                 const f32x4 (&rkv)[2]) {
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        s[h] = mfma16(kf[h * 2 + db], A[q].qh[db], s[h]);
+        s[h] = mfma16(kf[h * 2 + db], A[q].ql[db], s[h]);
+        s[h] = mfma16(kl[h * 2 + db], A[q].qh[db], s[h]);
+      }
+    }
+    float pv[8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = (j >> 2) * 16 + 4 * (lane >> 4) + (j & 3);
+      const float sc = qs[q] * rkv[j >> 2][j & 3];
+      pv[j] = s[j >> 2][j & 3] * sc + ((key >= 0 && key < khi) ? 0.f : -INFINITY);
+      mb = fmaxf(mb, pv[j]);
+    }
+    mb = xor32_max(xor16_max(mb));
+    const float mn = fmaxf(A[q].m, mb);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __expf(A[q].m - mu);
+    A[q].m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pv[j] = __expf(pv[j] - mu);
+      ps += pv[j];
+    }
+    A[q].den = A[q].den * alpha + ps;
+    bf16x8 ph, pl;
+    split8(pv, ph, pl);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 a = A[q].acc[dt] * alpha;
+      a = mfma16(vf[dt], ph, a);
+      a = mfma16(vf[dt], pl, a);
+      a = mfma16(vl[dt], ph, a);
+      A[q].acc[dt] = a;
+    }
+  }
+}
+
 // One block of 32 keys for NQ query tiles at once (the arguments of attn_block, with one score scale per
 // tile): the block's K and V^T fragments (and residual parts, key factors) are read once, each state's
 // chains and softmax arithmetic are those of attn_block.
@@ -2884,7 +2941,9 @@ __device__ __forceinline__ void sa_stage_pairs(Ctx<S>& c, const Desc& d, const i
     __builtin_amdgcn_global_load_lds(ssqk + (long long)(hd * 2 + j) * NRP + b * Mqp + qq, (lds_void*)sq_l, 4, 0, 0);
   }
   // each wave's first DMAs are its pieces of the two Q tiles, then K tiles of all own keys and V^T blocks
-  for (int k = c.wave; k < 8 + 4 * NKT + 8 * KBO; k += NWAVES) {
+  // (SA_REG: the Q tiles only; each wave loads its own-key block itself below)
+  const bool reg = S::SA_REG && !want_kv;
+  for (int k = c.wave; k < (reg ? 8 : 8 + 4 * NKT + 8 * KBO); k += NWAVES) {
     if (k < 8) {
       const int t = k >> 2, db = (k >> 1) & 1, part = k & 1;
       const int qt = qa + (t ? nq - 1 : 0);
@@ -2903,7 +2962,8 @@ __device__ __forceinline__ void sa_stage_pairs(Ctx<S>& c, const Desc& d, const i
   const float ssk0 = ssqk[(long long)((S::NH + hd) * 2) * NRP + rowk];
   const float ssk1 = ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + rowk];
   // every wave issued at least 4 own-key DMAs after its Q pieces (4 NKT + 8 KBO >= 16 over 4 waves)
-  wait_vm_le<4>();
+  if (reg) wait_vm0();
+  else wait_vm_le<4>();
   exec_barrier();
   MKX_TR(c, 1);
   AttnState A[2];
@@ -2916,22 +2976,74 @@ __device__ __forceinline__ void sa_stage_pairs(Ctx<S>& c, const Desc& d, const i
     qsc[t] = p.sm_scale * rsqrtf(ssq / 64.f + p.qk_eps);
   }
   const int mb0 = kvs >> 5, nmb = PMP / 32 - mb0;
+  // SA_REG: this wave's own-key block jo and its lanes' key factors into registers, landing during the memory
+  // blocks (as in sa_stage)
+  const int jo = ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES;
+  bf16x8 okh[4], okl[4], ovh[4], ovl[4];
+  float ssa[8], ssb[8];
+  if (reg && jo < KBO) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kt = 2 * jo + (i >> 1), db = i & 1;
+      const int rtk = rt0 + min(kt, NQT - 1);
+      const char* kp = ks + ((long long)((2 * hd + db) * RT + rtk) * 2) * 1024 + c.lane * 16;
+      okh[i] = __builtin_bit_cast(bf16x8, ld16(kp));
+      okl[i] = __builtin_bit_cast(bf16x8, ld16(kp + 1024));
+      const char* vp = vt + ((long long)hh * KBO * 8 + 2 * (jo * 4 + i)) * 1024 + c.lane * 16;
+      ovh[i] = __builtin_bit_cast(bf16x8, ld16(vp));
+      ovl[i] = __builtin_bit_cast(bf16x8, ld16(vp + 1024));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = jo * 32 + (e >> 2) * 16 + 4 * (c.lane >> 4) + (e & 3);
+      const int row = b * Mqp + min(key, Mqp - 1);
+      ssa[e] = ssqk[(long long)((S::NH + hd) * 2) * NRP + row];
+      ssb[e] = ssqk[(long long)((S::NH + hd) * 2 + 1) * NRP + row];
+    }
+  }
   for (int beta = c.wave; beta < nmb; beta += NWAVES) {
     const int kb = mb0 + beta;
     attn_block_nq<2>(A, c.lane, memK + kb * 4096, nullptr, memVt + kb * 4096, nullptr, kvs - kb * 32, PM - kb * 32, qsc, nullptr);
   }
-  wait_vm0();  // the own keys' K and V^T have landed
-  __syncthreads();
-  if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
-  for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
-    const int key = Mqp + it / HD, dd = it % HD;
-    *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
-    *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
-  }
-  __syncthreads();  // (also: every wave has read both tiles' queries before the merge area is reused)
-  for (int beta = nmb + ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES; beta < nmb + KBO; beta += NWAVES) {
-    const int kb = beta - nmb;
-    attn_block_nq<2>(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
+  if (reg) {
+    if (jo < KBO) {
+      // the lanes' key factors, and zero V for own keys beyond the sample's rows (no producer)
+      f32x4 rkv[2];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rkv[e >> 2][e & 3] = rsqrtf((ssa[e] + ssb[e]) / 64.f + p.qk_eps);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        u32x4 hv = __builtin_bit_cast(u32x4, ovh[dt]), lv = __builtin_bit_cast(u32x4, ovl[dt]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int key = jo * 32 + (j >> 2) * 16 + 4 * (c.lane >> 4) + (j & 3);
+          if (key >= Mqp) {
+            const uint32_t keep = (j & 1) ? 0x0000ffffu : 0xffff0000u;
+            hv[j >> 1] &= keep;
+            lv[j >> 1] &= keep;
+          }
+        }
+        ovh[dt] = __builtin_bit_cast(bf16x8, hv);
+        ovl[dt] = __builtin_bit_cast(bf16x8, lv);
+      }
+      attn_block_nq_rf<2>(A, c.lane, okh, okl, ovh, ovl, M - jo * 32, qsc, rkv);
+    }
+    // every wave has read both tiles' queries and sums of squares (in the merge area) before the merge
+    exec_barrier();
+  } else {
+    wait_vm0();  // the own keys' K and V^T have landed
+    __syncthreads();
+    if (c.tid < NOWN32) rk[c.tid] = rsqrtf((ssk0 + ssk1) / 64.f + p.qk_eps);
+    for (int it = c.tid; it < (NOWN32 - Mqp) * HD; it += NTHREADS) {
+      const int key = Mqp + it / HD, dd = it % HD;
+      *reinterpret_cast<bf16_t*>(Vh + vt_off(key, dd)) = 0;
+      *reinterpret_cast<bf16_t*>(Vl + vt_off(key, dd)) = 0;
+    }
+    __syncthreads();  // (also: every wave has read both tiles' queries before the merge area is reused)
+    for (int beta = nmb + ((c.wave - nmb) % NWAVES + NWAVES) % NWAVES; beta < nmb + KBO; beta += NWAVES) {
+      const int kb = beta - nmb;
+      attn_block_nq<2>(A, c.lane, Kh + kb * 4096, Kl + kb * 4096, Vh + kb * 4096, Vl + kb * 4096, 0, M - kb * 32, qsc, rk + kb * 32);
+    }
   }
   MKX_TR(c, 2);
   attn_merge_store(c, A[0], mrg, ysa, b, hd, qa);
