@@ -144,11 +144,11 @@ struct Shape {
   // register allocation) unchanged: compiled into them, the two-tile path made the kernels slower for every
   // launch (workload D 7.59 -> 7.90 ms without taking it).
   static constexpr bool PAIRS = RW_ && PR_;
-  // SA_REG: the same instantiations' and the two-tile ones' self-attention loads each wave's own-key block
-  // (K, V^T, hi and lo parts) and its keys' RMS factors into registers (sa_stage, sa_stage_pairs) instead of
-  // DMAing every own key into LDS after the poll, except in launches that also store the register rows' K/V
-  // (they read them from LDS)
-  static constexpr bool SA_REG = CA_REG || PAIRS;
+  // SA_REG: the same instantiations', the two-tile ones' and the long-source ones' self-attention loads each
+  // wave's own-key block (K, V^T, hi and lo parts) and its keys' RMS factors into registers (sa_stage,
+  // sa_stage_pairs) instead of DMAing every own key into LDS after the poll, except in launches that also
+  // store the register rows' K/V (they read them from LDS)
+  static constexpr bool SA_REG = CA_REG || PAIRS || (LS_ && !RW_);
   // LONG: the instantiations of the form with passes for sources longer than the three-chunk LDS ring (the
   // host picks them for launches whose source exceeds 384 rows): cross-attention streams the chunks beyond
   // the third into registers (ca_stage). Separate instantiations, so that the others keep their code.
