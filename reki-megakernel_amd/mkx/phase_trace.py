@@ -11,7 +11,11 @@ per stage kind, medians over the launch's layers of:
   to the last consumer task passing its ready-epoch wait: the time a stage boundary costs beyond the work;
 - ``work``: from there to the stage's last task finishing;
 - for GEMM stages in the pass form, the phases of a median task after its wait: first operands landed,
-  MFMAs and cross-wave sum, epilogue, publish (store acknowledgements and the ready epoch).
+  MFMAs and cross-wave sum, epilogue, publish (store acknowledgements and the ready epoch);
+- for the attention stages in the pass form, likewise: self-attention's query tile and own keys landed
+  (with the barrier after them), attention over every key block, merge of the four waves' states, store and
+  publish; cross-attention's query rows landed, query projection MFMAs, its epilogue (norm, RoPE, the query
+  tile into LDS and the barrier), attention, merge and store, publish.
 
 The trace build times slightly differently from libmkx.so (its stamps are stores on the critical path).
 """
@@ -33,6 +37,12 @@ TRACE_LIB = os.path.join(PKG, "libmkx_trace.so")
 TRACE_BASE, TRACE_SLOTS = 8192, 16  # the kernel's trace layout (csrc/mkx_kernel.h)
 STAGES = ["qkv", "sa_attn", "sa_o", "ca_attn", "ca_o", "gate_up", "down"]
 GEMM = {"qkv", "sa_o", "ca_o", "gate_up", "down"}
+# attention stages in the pass form: phase -> (from stamp slot, to stamp slot) of sa_stage / ca_stage
+ATTN = {
+    "sa_attn": {"operands": (0, 1), "attention": (1, 2), "merge_store_publish": (2, 4)},
+    "ca_attn": {"query_rows": (0, 3), "query_projection": (3, 7), "query_epilogue": (7, 1), "attention": (1, 2),
+                "merge_store": (2, 13), "publish": (13, 4)},
+}
 
 
 def build() -> str:
@@ -105,6 +115,10 @@ def trace(workload: str, raw_out: str = "") -> dict:
             rec["mfma_and_sum"] = _nanmed((a[:, 2] - a[:, 1]).tolist())
             rec["epilogue"] = _nanmed((a[:, 3] - a[:, 2]).tolist())
             rec["publish"] = _nanmed((a[:, 4] - a[:, 3]).tolist())
+        if kind in ATTN and not rows_form:
+            a = us[g, act]
+            for name, (s0, s1) in ATTN[kind].items():
+                rec[name] = _nanmed((a[:, s1] - a[:, s0]).tolist())
         rows[kind].append(rec)
     out = {"workload": workload, "form": "row-wise" if rows_form else "passes",
            "launch_us": float(torch.nan_to_num(us[total - 1, :, 4], nan=-1.0).max()), "stages": {}}
