@@ -201,8 +201,16 @@ Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A,
   auto clampi = [](int v, int lo, int hi) { return std::max(lo, std::min(hi, v)); };
   const int ndown_d = (k.HT / nt) * k.SK, nred_d = k.HT / nt;
   L.disjoint = k.IT + ndown_d <= G && 6 * k.NH + std::max(nred_d, nattn) <= G;
+  // narrow row-wise launches (at most 8 row tiles: each task's row groups fit one per wave): one row group
+  // per QKV and out-projection task, which takes no longer, so that QKV, self-attention and the
+  // out-projection, then cross-attention and its out-projection, run on disjoint workgroup ranges
+  const bool narrow = rows && !L.disjoint && RT <= 8 && 6 * k.NH + k.HT + nattn <= G && nattn <= 6 * k.NH &&
+                      6 * k.NH + 2 * k.HT <= G;
   int cnt[PL_KINDS] = {};
-  if (L.disjoint) {
+  if (narrow) {
+    L.nt_o = L.nt_cao = L.nt_down = 1;
+    L.rgs_qkv = L.rgs_o = L.rgs_cao = 1;
+  } else if (L.disjoint) {
     L.nt_o = L.nt_cao = L.nt_down = nt;
     L.rgs_cao = clampi(ndown_d / (k.HT / nt), 1, RT);
     // QKV leaves room for the self-attention tasks and the reducers; the out-projection sits inside the QKV
@@ -264,6 +272,16 @@ Layout plan_layout(const ShapeK& k, int G, int RT, int B, int nqt, int H, int A,
     place(PL_CA, {PL_O, PL_SA, PL_CAO});
     place(PL_TIN, {PL_RED, PL_QKV});
     place(PL_TOUT, {PL_QKV, PL_TIN, PL_DOWN});
+  } else if (narrow) {
+    // QKV [0, 6 NH), self-attention at the top, the out-projection between them; cross-attention on the QKV
+    // tasks' workgroups and its out-projection at the top, above the out-projection's (each range idle in the
+    // two stages before); gate/up and down on every workgroup
+    L.pl[PL_QKV] = L.pl[PL_CA] = L.pl[PL_GU] = L.pl[PL_DOWN] = 0;
+    L.pl[PL_SA] = md(G - nattn);
+    L.pl[PL_CAO] = md(G - k.HT);
+    L.pl[PL_O] = 6 * k.NH;
+    L.pl[PL_TIN] = L.pl[PL_TOUT] = md(G - k.NIN);
+    L.pl[PL_RED] = md(G - k.NIN - L.nred);
   } else {
     L.pl[PL_QKV] = L.pl[PL_O] = L.pl[PL_CAO] = L.pl[PL_GU] = L.pl[PL_DOWN] = 0;
     L.pl[PL_SA] = md(G - nattn);
